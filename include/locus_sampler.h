@@ -1,0 +1,165 @@
+/*
+ * locus_sampler.h - C ABI of the MI355X (gfx950) token sampler.
+ *
+ * The drop-in boundary for the reference's per-step sampling path. The
+ * reference has no C ABI for it: its callers use free C++ functions
+ * (src/locus/model/sampling.hpp:70-89, llama.hpp:351-352) on host spans, one
+ * row at a time (engine.cpp:423-450, engine.cpp:357-396). This ABI is what a
+ * backend-registry entry (registry.hpp:107-131) or any FFI binds: plain
+ * pointers and sizes, no exceptions, stream-ordered and asynchronous.
+ *
+ * All buffer pointers in lcs_batch / lcs_out / lcs_verify_* are DEVICE
+ * pointers unless the field says "host". Every call is asynchronous on the
+ * given HIP stream (a hipStream_t passed as void*, NULL = default stream);
+ * outputs are valid once the stream has been synchronised. One context must
+ * not be used by two threads at once; separate contexts are independent.
+ */
+#ifndef LOCUS_SAMPLER_H
+#define LOCUS_SAMPLER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct lcs_ctx lcs_ctx;
+
+enum lcs_status {
+    LCS_OK = 0,
+    LCS_ERR_INVALID_ARG = -1, /* bad pointer, size, alignment or dtype */
+    LCS_ERR_NO_DEVICE = -2,   /* no usable gfx950 device */
+    LCS_ERR_HIP = -3,         /* a HIP runtime call failed (see lcs_last_error) */
+    LCS_ERR_CAPACITY = -4     /* request exceeds the context's create-time limits */
+};
+
+enum lcs_dtype { LCS_F32 = 0, LCS_BF16 = 1 };
+
+enum lcs_flags {
+    LCS_WANT_LOGPROBS = 1u,   /* write chosen_lp and the n_top alternatives */
+    LCS_WRITE_PENALIZED = 2u  /* write penalised logits back in place (f32 only) */
+};
+
+/* Per-row sampling parameters: field-for-field the reference's
+ * SamplingParams (src/locus/model/sampling.hpp:23-40), 32 bytes. */
+typedef struct lcs_params {
+    float temperature;        /* <= 0: greedy (argmax) */
+    uint32_t top_k;           /* 0: disabled */
+    float top_p;              /* 1: disabled */
+    float min_p;              /* 0: disabled */
+    float repeat_penalty;     /* 1: disabled */
+    float frequency_penalty;  /* 0: disabled */
+    float presence_penalty;   /* 0: disabled */
+    uint32_t repeat_last_n;   /* trailing history entries the penalties see */
+} lcs_params;
+
+/* One batch of rows to sample: the batched form of
+ * sample(logits, params, history, rng, constraint) (sampling.hpp:70-73)
+ * followed, when LCS_WANT_LOGPROBS is set, by
+ * logprobs_from(raw logits, chosen, n_top, ...) (sampling.hpp:86-89),
+ * per row exactly as Engine::sample_from does (engine.cpp:423-450). */
+typedef struct lcs_batch {
+    uint32_t rows;
+    uint32_t vocab;            /* V, 1 <= V <= 262144 */
+    uint32_t dtype;            /* lcs_dtype */
+    uint32_t flags;            /* lcs_flags */
+    uint64_t row_stride;       /* elements between rows; multiple of 4 (f32) / 8 (bf16) */
+    const void* logits;        /* rows x row_stride, 16-byte aligned, raw logits */
+    const lcs_params* params;  /* rows */
+    const lcs_params* params_host; /* optional HOST copy of params (dispatch hint) or NULL */
+    const uint32_t* hist_off;  /* rows + 1 CSR offsets into hist_ids, or NULL */
+    const int32_t* hist_ids;   /* token history (the request's generated ids) */
+    const double* u;           /* rows: uniform in [0,1) per stochastic row, the
+                                  generate_canonical<double,53> draw of the row's
+                                  mt19937_64 (libstdc++ random.tcc:3348-3380) */
+    const uint32_t* mask;      /* rows x mask_words allow-bits (bit t&31 of word
+                                  t>>5, LSB first), or NULL for no constraint */
+    const uint8_t* has_mask;   /* rows, nonzero = row constrained; NULL = all rows
+                                  constrained when mask != NULL */
+    uint32_t mask_words;       /* >= ceil(V/32) when mask != NULL */
+    uint32_t n_top;            /* alternatives per row (<= the context's max_top) */
+} lcs_batch;
+
+/* Per-row diagnostics (optional output): the survivor set of the reference's
+ * candidate walk (sampling.cpp:160-238). */
+typedef struct lcs_row_diag {
+    uint32_t n_cand;    /* candidates after the constraint */
+    uint32_t keep;      /* survivors after top-k, top-p, min-p (0 for greedy) */
+    float maxl;         /* max penalised candidate logit */
+    float boundary;     /* logit of the last survivor */
+    uint32_t path;      /* implementation path taken (LCS_PATH_*) */
+    uint32_t reserved;
+    double sum;         /* softmax normaliser over the candidate list */
+    double kept_sum;    /* mass of the survivors */
+} lcs_row_diag;
+
+enum lcs_path {
+    LCS_PATH_GREEDY = 1u,     /* sliced argmax */
+    LCS_PATH_WINDOW = 2u,     /* sliced min-p window, certified normaliser */
+    LCS_PATH_WINDOW_EXACT = 3u, /* window with an exactly recomputed normaliser */
+    LCS_PATH_GENERAL = 4u     /* single-workgroup exact selection */
+};
+
+typedef struct lcs_out {
+    int32_t* ids;              /* rows: sampled token id */
+    float* chosen_lp;          /* rows (LCS_WANT_LOGPROBS) */
+    int32_t* top_ids;          /* rows x n_top (LCS_WANT_LOGPROBS) */
+    float* top_lp;             /* rows x n_top (LCS_WANT_LOGPROBS) */
+    lcs_row_diag* diag;        /* rows, or NULL */
+} lcs_out;
+
+/* Speculative-decoding verify (engine.cpp:357-396): row j of sequence s holds
+ * the logits that predict draft[s*rows_per_seq + j]. */
+typedef struct lcs_verify_batch {
+    uint32_t n_seq;
+    uint32_t rows_per_seq;     /* 1..64 */
+    uint32_t vocab;
+    uint32_t dtype;            /* lcs_dtype */
+    uint64_t row_stride;       /* elements; multiple of 4 (f32) / 8 (bf16) */
+    const void* logits;        /* (n_seq * rows_per_seq) x row_stride */
+    const int32_t* draft;      /* n_seq * rows_per_seq draft ids */
+} lcs_verify_batch;
+
+typedef struct lcs_verify_out {
+    int32_t* argmax_ids;       /* per row: argmax (llama.cpp:1237-1245) */
+    float* draft_lp;           /* per row: logprobs_from(row, draft, 0).chosen_lp */
+    uint32_t* accept_len;      /* per sequence: leading rows whose argmax == draft */
+} lcs_verify_out;
+
+/* Number of usable gfx950 devices (0 when none). Replaces the runtime probe
+ * that sets Backend::available (registry.cpp:148-223, cuda_stub.cpp:29). */
+int lcs_probe(int* n_devices);
+
+/* Allocates the per-context workspace on `device` once; no call below
+ * allocates device memory. Returns NULL on failure (lcs_last_error(NULL)). */
+lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab,
+                    uint32_t max_hist, uint32_t max_top);
+void lcs_destroy(lcs_ctx* ctx);
+
+/* Batched sample (+ logprobs): replaces per-row sample()/logprobs_from()
+ * (sampling.hpp:70-89) as called from engine.cpp:430-442. */
+int lcs_sample(lcs_ctx* ctx, const lcs_batch* batch, const lcs_out* out, void* stream);
+
+/* Batched greedy verify: replaces the argmax loop of engine.cpp:357-396 and
+ * adds the draft logprob (sampling.cpp:241-261 with chosen = draft). */
+int lcs_verify(lcs_ctx* ctx, const lcs_verify_batch* batch, const lcs_verify_out* out,
+               void* stream);
+
+/* Sticky device-side status bits of ctx (LCS_STATUS_*), set by kernels that
+ * met an input they could not serve (the affected rows get id -1). Blocking:
+ * reads device memory; call after the work's stream has been synchronised.
+ * No counterpart in the reference (its sampler cannot fail). */
+int lcs_get_status(lcs_ctx* ctx, uint32_t* status_out, int reset);
+
+enum lcs_status_bits {
+    LCS_STATUS_HIST_CAPACITY = 1u,  /* a penalty window exceeded max_hist */
+    LCS_STATUS_SELECT = 2u          /* a selection bin exceeded its capacity */
+};
+
+/* Message of the last failure on ctx (or of the last lcs_create when NULL). */
+const char* lcs_last_error(const lcs_ctx* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LOCUS_SAMPLER_H */

@@ -1,0 +1,278 @@
+// C ABI of the sampler (include/locus_sampler.h): context workspace,
+// argument validation and kernel dispatch. No call after lcs_create
+// allocates device memory.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "lcs_internal.hpp"
+#include "locus_sampler.h"
+
+namespace lcs {
+hipError_t launch_slice(const SampleArgs& a, hipStream_t st);
+hipError_t launch_general(const SampleArgs& a, hipStream_t st);
+hipError_t launch_verify(const VerifyArgs& a, hipStream_t st);
+}  // namespace lcs
+
+struct lcs_ctx {
+    int device = 0;
+    uint32_t max_rows = 0, max_vocab = 0, max_hist = 0, max_top = 0;
+    uint32_t max_slices = 0;
+    uint32_t* recs = nullptr;
+    uint32_t* counters = nullptr;
+    uint32_t* vcounters = nullptr;
+    uint32_t* d_ids = nullptr;
+    float* d_raw = nullptr;
+    float* d_pen = nullptr;
+    uint32_t* status = nullptr;
+    std::string err;
+};
+
+namespace {
+
+thread_local std::string g_create_error;
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+int fail(lcs_ctx* c, int code, const std::string& msg) {
+    if (c) c->err = msg;
+    return code;
+}
+int hip_fail(lcs_ctx* c, hipError_t e, const char* what) {
+    return fail(c, LCS_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+bool is_gfx950(int dev) {
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, dev) != hipSuccess) return false;
+    return std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
+}
+
+uint32_t slices_for(uint32_t vocab) {
+    return (vocab + lcs::kSliceMax - 1) / lcs::kSliceMax;
+}
+uint32_t slice_len_for(uint32_t vocab) {
+    const uint32_t s = slices_for(vocab);
+    const uint32_t per = (vocab + s - 1) / s;
+    return (per + 7u) & ~7u;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lcs_probe(int* n_devices) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    int usable = 0;
+    for (int d = 0; d < n; ++d) usable += is_gfx950(d) ? 1 : 0;
+    if (n_devices) *n_devices = usable;
+    return usable > 0 ? LCS_OK : LCS_ERR_NO_DEVICE;
+}
+
+lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t max_hist,
+                    uint32_t max_top) {
+    g_create_error.clear();
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n || !is_gfx950(device)) {
+        g_create_error = "no usable gfx950 device at index " + std::to_string(device);
+        return nullptr;
+    }
+    if (max_rows == 0 || max_vocab == 0 || max_vocab > lcs::kMaxVocab ||
+        max_hist > lcs::kGenHistCap || max_top > lcs::kTopMax) {
+        g_create_error = "lcs_create: limits out of range (rows >= 1, 1 <= vocab <= 262144, "
+                         "hist <= 8192, top <= 20)";
+        return nullptr;
+    }
+    auto* c = new (std::nothrow) lcs_ctx();
+    if (!c) {
+        g_create_error = "out of host memory";
+        return nullptr;
+    }
+    DeviceGuard g(device);
+    c->device = device;
+    c->max_rows = max_rows;
+    c->max_vocab = max_vocab;
+    c->max_hist = max_hist > 0 ? max_hist : 1;
+    c->max_top = max_top;
+    c->max_slices = slices_for(max_vocab);
+    const size_t rec_bytes = (size_t)max_rows * c->max_slices * lcs::rec::kWords * 4;
+    const size_t d_elems = (size_t)max_rows * c->max_hist;
+    hipError_t e = hipSuccess;
+    if ((e = hipMalloc(&c->recs, rec_bytes)) != hipSuccess ||
+        (e = hipMalloc(&c->counters, (size_t)max_rows * 4)) != hipSuccess ||
+        (e = hipMalloc(&c->vcounters, (size_t)max_rows * 4)) != hipSuccess ||
+        (e = hipMalloc(&c->d_ids, d_elems * 4)) != hipSuccess ||
+        (e = hipMalloc(&c->d_raw, d_elems * 4)) != hipSuccess ||
+        (e = hipMalloc(&c->d_pen, d_elems * 4)) != hipSuccess ||
+        (e = hipMalloc(&c->status, 4)) != hipSuccess ||
+        (e = hipMemset(c->counters, 0, (size_t)max_rows * 4)) != hipSuccess ||
+        (e = hipMemset(c->vcounters, 0, (size_t)max_rows * 4)) != hipSuccess ||
+        (e = hipMemset(c->status, 0, 4)) != hipSuccess ||
+        (e = hipDeviceSynchronize()) != hipSuccess) {
+        g_create_error = std::string("lcs_create: ") + hipGetErrorString(e);
+        lcs_destroy(c);
+        return nullptr;
+    }
+    return c;
+}
+
+void lcs_destroy(lcs_ctx* c) {
+    if (!c) return;
+    DeviceGuard g(c->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(c->recs);
+    (void)hipFree(c->counters);
+    (void)hipFree(c->vcounters);
+    (void)hipFree(c->d_ids);
+    (void)hipFree(c->d_raw);
+    (void)hipFree(c->d_pen);
+    (void)hipFree(c->status);
+    delete c;
+}
+
+const char* lcs_last_error(const lcs_ctx* c) {
+    return c ? c->err.c_str() : g_create_error.c_str();
+}
+
+int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
+    if (!c) return LCS_ERR_INVALID_ARG;
+    if (!b || !o) return fail(c, LCS_ERR_INVALID_ARG, "null batch or output");
+    if (b->rows == 0) return LCS_OK;
+    if (b->dtype != LCS_F32 && b->dtype != LCS_BF16) return fail(c, LCS_ERR_INVALID_ARG, "dtype");
+    const uint32_t G = b->dtype == LCS_BF16 ? 8u : 4u;
+    if (!b->logits || !b->params || !o->ids) return fail(c, LCS_ERR_INVALID_ARG, "null logits/params/ids");
+    if (b->vocab == 0 || b->row_stride < b->vocab || b->row_stride % G != 0 ||
+        (reinterpret_cast<uintptr_t>(b->logits) & 15u) != 0) {
+        return fail(c, LCS_ERR_INVALID_ARG, "logits must be 16-byte aligned with row_stride >= vocab and a multiple of 4 (f32) / 8 (bf16)");
+    }
+    if (b->rows > c->max_rows || b->vocab > c->max_vocab) {
+        return fail(c, LCS_ERR_CAPACITY, "rows or vocab above the context limits");
+    }
+    const bool want_lp = (b->flags & LCS_WANT_LOGPROBS) != 0;
+    if (want_lp && (!o->chosen_lp || (b->n_top > 0 && (!o->top_ids || !o->top_lp)))) {
+        return fail(c, LCS_ERR_INVALID_ARG, "logprob outputs missing");
+    }
+    if (want_lp && b->n_top > c->max_top) return fail(c, LCS_ERR_CAPACITY, "n_top above max_top");
+    if (b->mask && b->mask_words < (b->vocab + 31) / 32) return fail(c, LCS_ERR_INVALID_ARG, "mask_words < ceil(vocab/32)");
+    if (b->hist_off && !b->hist_ids) return fail(c, LCS_ERR_INVALID_ARG, "hist_ids missing");
+    if ((b->flags & LCS_WRITE_PENALIZED) && b->dtype != LCS_F32) {
+        return fail(c, LCS_ERR_INVALID_ARG, "LCS_WRITE_PENALIZED needs f32 logits");
+    }
+    if (!b->u && b->params_host) {
+        for (uint32_t r = 0; r < b->rows; ++r) {
+            if (b->params_host[r].temperature > 0.0f) return fail(c, LCS_ERR_INVALID_ARG, "u missing for a stochastic row");
+        }
+    }
+    // Which kernels to launch: a row runs in exactly one of them (the
+    // kernels re-derive each row's mode on the device). Without a host copy
+    // of the params both are launched.
+    bool any_slice = true, any_general = true;
+    if (b->params_host) {
+        any_slice = any_general = false;
+        for (uint32_t r = 0; r < b->rows; ++r) {
+            const lcs_params& p = b->params_host[r];
+            for (int mk = 0; mk < 2; ++mk) {
+                const bool masked = mk == 1;
+                if (masked && !b->mask) continue;
+                if (!masked && b->mask && !b->has_mask) continue;  // every row masked
+                const uint32_t m = lcs::row_mode(p, masked, b->vocab);
+                any_slice = any_slice || m != lcs::kModeGeneral;
+                any_general = any_general || m == lcs::kModeGeneral;
+            }
+        }
+    }
+    if (b->flags & LCS_WRITE_PENALIZED) { any_slice = false; any_general = true; }
+
+    lcs::SampleArgs a{};
+    a.logits = b->logits;
+    a.row_stride = b->row_stride;
+    a.rows = b->rows;
+    a.vocab = b->vocab;
+    a.dtype = b->dtype;
+    a.flags = b->flags;
+    a.n_top = want_lp ? b->n_top : 0;
+    a.mask_words = b->mask_words;
+    a.params = b->params;
+    a.hist_off = b->hist_off;
+    a.hist_ids = b->hist_ids;
+    a.u = b->u;
+    a.mask = b->mask;
+    a.has_mask = b->has_mask;
+    a.ids = o->ids;
+    a.chosen_lp = o->chosen_lp;
+    a.top_ids = o->top_ids;
+    a.top_lp = o->top_lp;
+    a.diag = o->diag;
+    a.recs = c->recs;
+    a.counters = c->counters;
+    a.d_ids = c->d_ids;
+    a.d_raw = c->d_raw;
+    a.d_pen = c->d_pen;
+    a.max_hist = c->max_hist;
+    a.status = c->status;
+    a.slices = slices_for(b->vocab);
+    a.slice_len = slice_len_for(b->vocab);
+
+    DeviceGuard g(c->device);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e = hipSuccess;
+    if (any_general && (e = lcs::launch_general(a, st)) != hipSuccess) return hip_fail(c, e, "general kernel launch");
+    if (any_slice && (e = lcs::launch_slice(a, st)) != hipSuccess) return hip_fail(c, e, "slice kernel launch");
+    return LCS_OK;
+}
+
+int lcs_verify(lcs_ctx* c, const lcs_verify_batch* b, const lcs_verify_out* o, void* stream) {
+    if (!c) return LCS_ERR_INVALID_ARG;
+    if (!b || !o || !b->logits || !b->draft || !o->argmax_ids || !o->draft_lp || !o->accept_len) {
+        return fail(c, LCS_ERR_INVALID_ARG, "null verify argument");
+    }
+    if (b->n_seq == 0) return LCS_OK;
+    if (b->dtype != LCS_F32 && b->dtype != LCS_BF16) return fail(c, LCS_ERR_INVALID_ARG, "dtype");
+    const uint32_t G = b->dtype == LCS_BF16 ? 8u : 4u;
+    if (b->rows_per_seq == 0 || b->rows_per_seq > 64) return fail(c, LCS_ERR_INVALID_ARG, "rows_per_seq must be 1..64");
+    if (b->vocab == 0 || b->row_stride < b->vocab || b->row_stride % G != 0 ||
+        (reinterpret_cast<uintptr_t>(b->logits) & 15u) != 0) {
+        return fail(c, LCS_ERR_INVALID_ARG, "logits must be 16-byte aligned with row_stride >= vocab and a multiple of 4 (f32) / 8 (bf16)");
+    }
+    if (b->n_seq > c->max_rows) return fail(c, LCS_ERR_CAPACITY, "n_seq above max_rows");
+    lcs::VerifyArgs a{};
+    a.logits = b->logits;
+    a.row_stride = b->row_stride;
+    a.n_seq = b->n_seq;
+    a.rows_per_seq = b->rows_per_seq;
+    a.vocab = b->vocab;
+    a.dtype = b->dtype;
+    a.draft = b->draft;
+    a.argmax_ids = o->argmax_ids;
+    a.draft_lp = o->draft_lp;
+    a.accept_len = o->accept_len;
+    a.counters = c->vcounters;
+    DeviceGuard g(c->device);
+    const hipError_t e = lcs::launch_verify(a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(c, e, "verify kernel launch");
+    return LCS_OK;
+}
+
+int lcs_get_status(lcs_ctx* c, uint32_t* status_out, int reset) {
+    if (!c || !status_out) return LCS_ERR_INVALID_ARG;
+    DeviceGuard g(c->device);
+    hipError_t e = hipMemcpy(status_out, c->status, 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(c, e, "status read");
+    if (reset && (e = hipMemset(c->status, 0, 4)) != hipSuccess) return hip_fail(c, e, "status reset");
+    return LCS_OK;
+}
+
+}  // extern "C"

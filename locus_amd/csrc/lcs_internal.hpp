@@ -1,0 +1,106 @@
+// Internal definitions shared by the sampler kernels and the host dispatch.
+#pragma once
+
+#include <stdint.h>
+
+#include "locus_sampler.h"
+
+namespace lcs {
+
+// ---- sliced (multi-workgroup) path ----
+constexpr int kSliceThreads = 256;      // threads per slice workgroup
+constexpr int kSliceElems = 32;         // logits held in registers per thread
+constexpr uint32_t kSliceMax = kSliceThreads * kSliceElems;  // 8192 per slice
+constexpr uint32_t kMaxVocab = 262144;
+constexpr uint32_t kMaxSlices = kMaxVocab / kSliceMax;       // 32
+constexpr uint32_t kTopMax = 20;        // logprob alternatives per row
+constexpr uint32_t kWinCap = 64;        // min-p window entries per slice
+constexpr uint32_t kFastHistMax = 4096; // penalty window handled by the sliced path
+
+// Slice record (uint32 words), written with device-scope stores and read by
+// the row's last-arriving workgroup.
+namespace rec {
+constexpr uint32_t kMRaw = 0;       // f32 raw max of the slice
+constexpr uint32_t kSRaw = 2;       // f64 sum exp(raw - kMRaw)
+constexpr uint32_t kMAll = 4;       // f32 penalised max over all ids, then idx
+constexpr uint32_t kIAll = 5;
+constexpr uint32_t kMMsk = 6;       // f32 penalised max over allowed ids, then idx
+constexpr uint32_t kIMsk = 7;
+constexpr uint32_t kNAllowed = 8;
+constexpr uint32_t kNWin = 9;
+constexpr uint32_t kOverflow = 10;
+constexpr uint32_t kNTop = 11;
+constexpr uint32_t kBulk = 12;      // f64 sum over non-window ids of exp((p - kMAll)/T)
+constexpr uint32_t kBulkErr = 14;   // f64 error bound of kBulk
+constexpr uint32_t kTop = 16;       // kTopMax x (f32 value, u32 idx)
+constexpr uint32_t kWin = kTop + 2 * kTopMax;   // kWinCap x (f32 value, u32 idx)
+constexpr uint32_t kWords = ((kWin + 2 * kWinCap) + 63) / 64 * 64;
+}  // namespace rec
+
+// ---- single-workgroup exact path ----
+constexpr int kGenThreads = 1024;
+constexpr uint32_t kGenBins = 2048;
+constexpr uint32_t kGenCap = 2048;
+constexpr uint32_t kGenHistCap = 8192;
+// inline fallback inside the sliced kernel (256 threads, small LDS)
+constexpr uint32_t kFbBins = 512;
+constexpr uint32_t kFbCap = 512;
+constexpr uint32_t kFbHistCap = kFastHistMax;
+
+enum RowMode : uint32_t { kModeGreedy = 1, kModeWindow = 2, kModeGeneral = 4 };
+
+// Which implementation path a row takes; pure function of its parameters.
+__host__ __device__ inline uint32_t row_mode(const lcs_params& p, bool masked, uint32_t vocab) {
+    if (p.temperature <= 0.0f) return kModeGreedy;
+    const bool pen = !(p.repeat_penalty == 1.0f && p.frequency_penalty == 0.0f &&
+                       p.presence_penalty == 0.0f);
+    const bool topk = p.top_k > 0 && p.top_k < vocab;
+    if (p.min_p > 0.0f && !masked && !topk && (!pen || p.repeat_last_n <= kFastHistMax)) {
+        return kModeWindow;
+    }
+    return kModeGeneral;
+}
+
+struct SampleArgs {
+    const void* logits;
+    uint64_t row_stride;
+    uint32_t rows, vocab, dtype, flags, n_top, mask_words;
+    const lcs_params* params;
+    const uint32_t* hist_off;
+    const int32_t* hist_ids;
+    const double* u;
+    const uint32_t* mask;
+    const uint8_t* has_mask;
+    int32_t* ids;
+    float* chosen_lp;
+    int32_t* top_ids;
+    float* top_lp;
+    lcs_row_diag* diag;
+    // workspace
+    uint32_t* recs;          // rows x slices x rec::kWords
+    uint32_t* counters;      // rows
+    uint32_t* d_ids;         // rows x max_hist (distinct penalised ids)
+    float* d_raw;
+    float* d_pen;
+    uint32_t max_hist;
+    uint32_t* status;        // device error word (sticky bits)
+    uint32_t slices;         // workgroups per row on the sliced path
+    uint32_t slice_len;      // elements per slice (multiple of 8)
+};
+
+struct VerifyArgs {
+    const void* logits;
+    uint64_t row_stride;
+    uint32_t n_seq, rows_per_seq, vocab, dtype;
+    const int32_t* draft;
+    int32_t* argmax_ids;
+    float* draft_lp;
+    uint32_t* accept_len;
+    uint32_t* counters;      // n_seq
+};
+
+// status bits
+constexpr uint32_t kStatusHistCap = 1u;   // a penalty window exceeded the capacity
+constexpr uint32_t kStatusBinCap = 2u;    // selection could not narrow a bin (unexpected)
+
+}  // namespace lcs

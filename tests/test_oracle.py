@@ -1,0 +1,238 @@
+"""Pins the CPU oracle (oracle/oracle.cpp) before any GPU result is judged
+against it: golden vectors of the compiled reference, the reference's own
+known-answer tests (tests/test_sampling.cpp), the C++ standard's RNG check
+value, and independent closed forms (numpy float64)."""
+import math
+
+import numpy as np
+import pytest
+
+from locus_amd import workloads as W
+from oracle import pyoracle as O
+from tests.util import load
+
+U_LAST = math.nextafter(1.0, 0.0)
+
+
+def test_mt19937_64_standard_check_value():
+    # C++ [rand.predef]: 10000th output of a default-constructed mt19937_64
+    g = W.MT19937_64()
+    for _ in range(9999):
+        g()
+    assert g() == 9981545732273789042
+    assert O.lib().orc_mt_raw(5489, 9999) == 9981545732273789042
+
+
+def test_uniform_transform_matches_generate_canonical():
+    for s in [0, 1, 42, 20261202 * 1000003 + 7, (1 << 64) - 1]:
+        s &= (1 << 64) - 1
+        assert W.MT19937_64(s).canonical() == O.lib().orc_mt_u(s, 0)
+
+
+@pytest.mark.parametrize("idx", range(5))
+def test_oracle_matches_reference_configs(idx):
+    fx = load("configs.json")["sampling"][idx]
+    w = W.make(fx["workload"], rows=fx["rows"] if fx["workload"] not in ("c1g", "c1s") else None)
+    assert w.input_checksum() == fx["checksum"], "generator drift"
+    res = O.sample_batch(w, threads=8)
+    assert res.ids.tolist() == fx["ids"]
+    assert W.checksum(res.penalized) == fx["penalized_checksum"]
+    stoch = w.params["temperature"] > 0
+    hi = O.sample_batch(w, threads=8, u=np.where(stoch, U_LAST, 0.0))
+    assert [int(x) if s else -1 for x, s in zip(hi.ids, stoch)] == fx["last_survivor_ids"]
+    # the u -> 1 draw lands on the last survivor (pins the survivor count)
+    for r in np.nonzero(stoch)[0]:
+        assert hi.diag[r]["pos"] == hi.diag[r]["keep"] - 1 or hi.diag[r]["tie_flags"]
+    if w.want_logprobs:
+        assert np.array_equal(res.chosen_lp, np.array(fx["chosen_lp"], np.float32))
+        assert res.top_ids[:, :w.n_top].tolist() == fx["top_ids"]
+        assert np.array_equal(res.top_lp[:, :w.n_top], np.array(fx["top_lp"], np.float32))
+
+
+def test_oracle_matches_reference_edge_cases():
+    from tests.golden.make_golden import edge_workloads
+    fx = load("edge.json")
+    wls = edge_workloads()
+    assert len(wls) == len(fx)
+    for w, f in zip(wls, fx):
+        assert w.input_checksum() == f["checksum"]
+        res = O.sample_batch(w)
+        assert res.ids.tolist() == f["ids"], w.name
+        if w.want_logprobs:
+            assert np.array_equal(res.chosen_lp, np.array(f["chosen_lp"], np.float32)), w.name
+            assert res.top_ids[:, :w.n_top].tolist() == f["top_ids"], w.name
+
+
+def test_oracle_verify_matches_reference():
+    fx = load("configs.json")["verify"]
+    w = W.make("c5", rows=fx["rows"])
+    assert w.input_checksum() == fx["checksum"]
+    am, lp, acc = O.verify(w, threads=8)
+    assert am.tolist() == fx["argmax"]
+    assert np.array_equal(lp, np.array(fx["draft_lp"], np.float32))
+    assert acc.tolist() == fx["accept_len"]
+
+
+# ---- the reference's own known answers (tests/test_sampling.cpp) ----
+def P(**kw):
+    p = W.default_params(1)
+    for k, v in kw.items():
+        p[k] = v
+    return p
+
+
+def rng_u(g, p):
+    """u for one sample() call: one mt19937_64 output when stochastic."""
+    return g.canonical() if p["temperature"][0] > 0 else 0.0
+
+
+def test_kat_default_is_greedy():
+    assert O.sample_row([1.0, 3.0, 2.0, 0.5], P())[0] == 1
+
+
+def test_kat_repeat_penalty_shifts_argmax():
+    rid, pen, _ = O.sample_row([5.0, 4.9], P(repeat_penalty=10.0), hist=[0])
+    assert rid == 1 and pen[0] == np.float32(0.5)
+
+
+def test_kat_frequency_penalty_counts_history():
+    assert O.sample_row([5.0, 4.0], P(frequency_penalty=1.0), hist=[0, 0, 0])[0] == 1
+
+
+def test_kat_top_k_one_selects_max():
+    g = W.MT19937_64(123)
+    p = P(temperature=1.5, top_k=1)
+    for _ in range(20):
+        assert O.sample_row([0.1, 0.2, 5.0, 0.3], p, u=rng_u(g, p))[0] == 2
+
+
+def test_kat_same_seed_reproducible():
+    a, b = W.MT19937_64(42), W.MT19937_64(42)
+    p = P(temperature=1.0)
+    for _ in range(16):
+        assert O.sample_row([1.0] * 4, p, u=rng_u(a, p))[0] == O.sample_row([1.0] * 4, p, u=rng_u(b, p))[0]
+
+
+def test_kat_constraint_restricts_choice():
+    mask = W.pack_mask(np.array([False, False, True, True, False]))
+    assert O.sample_row([5.0, 4.0, 3.0, 2.0, 1.0], P(), mask=mask)[0] == 2
+    g = W.MT19937_64(123)
+    p = P(temperature=1.0)
+    for _ in range(30):
+        assert O.sample_row([5.0, 4.0, 3.0, 2.0, 1.0], p, u=rng_u(g, p), mask=mask)[0] in (2, 3)
+
+
+def test_kat_dominant_logit_always_chosen():
+    g = W.MT19937_64(123)
+    p = P(temperature=1.0)
+    for _ in range(50):
+        assert O.sample_row([0.0, 40.0, 0.0], p, u=rng_u(g, p))[0] == 1
+
+
+def test_kat_logprobs_normalized():
+    lp2, top, tlp, _ = O.logprobs(np.array([1.0, 2.0, 3.0]), 2, 3)
+    assert abs(np.exp(tlp.astype(np.float64)).sum() - 1.0) < 1e-5
+    assert top.tolist() == [2, 1, 0]
+    assert tlp[0] == pytest.approx(lp2) and (tlp <= 0).all()
+    lp0, one, _, _ = O.logprobs(np.array([1.0, 2.0, 3.0]), 0, 1)
+    assert one.tolist() == [2] and lp0 < lp2
+
+
+# ---- closed forms (numpy float64), independent of the oracle's code ----
+def test_logprobs_match_float64_log_softmax():
+    g = np.random.default_rng(5)
+    for V in (1, 7, 1000, 50000):
+        l = (g.standard_normal(V) * 3).astype(np.float32)
+        c = int(g.integers(0, V))
+        lp, top, tlp, _ = O.logprobs(l, c, min(5, V))
+        x = l.astype(np.float64)
+        ref = x - (np.log(np.exp(x - x.max()).sum()) + x.max())
+        assert abs(lp - ref[c]) < 1e-6
+        order = np.argsort(-x, kind="stable")[:min(5, V)]
+        assert top.tolist() == order.tolist()
+        assert np.allclose(tlp, ref[order], atol=1e-6)
+        assert O.lib().orc_argmax(l.ctypes.data_as(O.C.c_void_p), V) == int(np.argmax(l))
+
+
+def _np_survivors(l, p):
+    """Survivor count by a vectorised float64 restatement of the filters."""
+    srt = np.sort(l)[::-1]
+    if 0 < p["top_k"] < len(srt):
+        srt = srt[:p["top_k"]]
+    x = ((srt - srt[0]).astype(np.float32) * np.float32(1.0 / np.float32(p["temperature"]))).astype(np.float64)
+    w = np.exp(x)
+    s = w.sum()
+    keep = len(srt)
+    if p["top_p"] < 1:
+        cum = np.cumsum(w / s)
+        hit = np.nonzero(cum >= np.float64(np.float32(p["top_p"])))[0]
+        if len(hit):
+            keep = hit[0] + 1
+    if p["min_p"] > 0:
+        ok = w / s >= np.float64(np.float32(p["min_p"])) * (w[0] / s)
+        ok[0] = True
+        bad = np.nonzero(~ok[:keep])[0]
+        if len(bad):
+            keep = bad[0]
+    return keep, w, srt
+
+
+def test_survivor_sets_match_vectorised_closed_form():
+    g = np.random.default_rng(9)
+    checked = 0
+    for trial in range(60):
+        V = int(g.integers(2, 3000))
+        l = (g.standard_normal(V) * g.uniform(0.5, 4)).astype(np.float32)
+        p = P(temperature=float(g.uniform(0.3, 2.0)), top_k=int(g.choice([0, 5, 50])),
+              top_p=float(g.choice([1.0, 0.9, 0.5])), min_p=float(g.choice([0.0, 0.05, 0.3])))[0]
+        rid, _, d = O.sample_row(l, np.array([p]), u=float(g.random()))
+        keep, w, srt = _np_survivors(l, p)
+        if min(d["margin_p"], d["margin_m"]) < 1e-9:
+            continue
+        assert d["keep"] == keep
+        assert l[rid] >= srt[keep - 1]  # drawn id is a survivor
+        checked += 1
+    assert checked > 40
+
+
+def test_draw_position_monotone_in_u_and_frequencies():
+    l = np.array([2.0, 1.0, 0.5, -1.0, 0.0], np.float32)
+    p = P(temperature=1.0)
+    order = np.argsort(-l, kind="stable")
+    prev = -1
+    for u in np.linspace(0, U_LAST, 200):
+        rid = O.sample_row(l, p, u=float(u))[0]
+        pos = int(np.nonzero(order == rid)[0][0])
+        assert pos >= prev
+        prev = pos
+    # chi-square over many uniform draws against the softmax
+    g = W.MT19937_64(2024)
+    n = 20000
+    counts = np.zeros(5)
+    for _ in range(n):
+        counts[O.sample_row(l, p, u=g.canonical())[0]] += 1
+    prob = np.exp(l.astype(np.float64))
+    prob /= prob.sum()
+    chi2 = ((counts - n * prob) ** 2 / (n * prob)).sum()
+    assert chi2 < 20.0  # 4 dof, p ~ 5e-4
+
+
+def test_checks_have_teeth_against_planted_mistake():
+    """A plausibly wrong filter order (min-p before top-p) must be caught by
+    the vectorised closed form used above."""
+    g = np.random.default_rng(3)
+    caught = False
+    for _ in range(200):
+        V = 200
+        l = (g.standard_normal(V) * 2).astype(np.float32)
+        p = P(temperature=0.7, top_p=0.5, min_p=0.3)[0]
+        keep, w, _ = _np_survivors(l, p)
+        s = w.sum()
+        ok = w / s >= np.float64(np.float32(p["min_p"])) * (w[0] / s)
+        wrong = int(np.argmin(ok)) if not ok.all() else len(w)  # min-p first
+        cum = np.cumsum(w[:wrong] / w[:wrong].sum())
+        wrong_keep = int(np.nonzero(cum >= 0.5)[0][0]) + 1
+        if wrong_keep != keep:
+            caught = True
+            break
+    assert caught
