@@ -1,0 +1,193 @@
+"""Benchmark of the HIP sampler on one MI355X.
+
+Default workload: BASELINE.json configs[1] ("c2"): B=64, V=128256 f32
+logits ~ N(0, 3^2), 2048-id Zipf history, repeat 1.1 / frequency 0.5 /
+presence 0.3, T=0.7, min-p 0.05, top-p 0.9, seeded draw, top-5 logprobs.
+A step is one lcs_sample call over one batch with inputs already resident in
+HBM; the timed loop rotates through enough distinct input sets (> 2x the
+256 MB Infinity Cache) that each call reads its logits from HBM.
+
+Prints one JSON line: rows/s (value), HBM roofline of the sampling kernel,
+and the reference CPU sampler timed on this host (cpu_baseline).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from locus_amd import workloads as W  # noqa: E402
+
+METRIC = "sampled rows/sec + achieved HBM GB/s (B=64, V=128256, full sampling chain)"
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+
+CONFIG_TEXT = {
+    "c1g": "B=1 V=128256 f32 greedy",
+    "c1s": "B=1 V=128256 f32 T0.8 top-k40 top-p0.95",
+    "c2": "B=64 V=128256 f32 pen(1.1,0.5,0.3,last2048) T0.7 min-p0.05 top-p0.9 top-5 logprobs",
+    "c3": "B=256 V=151936 f32 T1.5 top-p0.98",
+    "c4": "B=32 V=128256 f32 JSON-mask T1.0 top-p0.95 top-1 logprob",
+    "c5": "4096 rows (512x8) V=163840 bf16 verify: argmax + lp(draft) + accept length",
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gpu_bench(name, steps, warmup):
+    import torch
+
+    from locus_amd.sampler import Sampler
+
+    w0 = W.make(name)
+    set_bytes = w0.logits.nbytes
+    nsets = max(1, min(32, -(-2 * MALL_BYTES // set_bytes) + 1)) if set_bytes < MALL_BYTES else 1
+    log(f"[bench] {name}: {nsets} input sets of {set_bytes / 1e6:.1f} MB")
+    s = Sampler(device=0, max_rows=max(w0.rows, w0.n_seq or 1), max_vocab=w0.vocab,
+                max_hist=4096, max_top=20)
+    sets = []
+    for k in range(nsets):
+        w = w0 if k == 0 else W.make(name, set_index=k)
+        d = s.upload(w)
+        out = s.alloc_verify_out(w) if w.n_seq else s.alloc_out(w.rows, w.n_top, w.want_logprobs, diag=False)
+        sets.append((d, out))
+    verify = bool(w0.n_seq)
+    stream = torch.cuda.current_stream()
+
+    def call(i):
+        d, out = sets[i % nsets]
+        if verify:
+            s.verify_dev(d, out, stream=stream)
+        else:
+            s.sample_dev(d, out, stream=stream)
+
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize()
+    # (1) whole-job timing: events bracket the K calls on the launch stream
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(steps):
+        call(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = e0.elapsed_time(e1)
+    # (2) per-launch duration: events around each launch on the same stream
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for i in range(steps):
+        starts[i].record(stream)
+        call(i)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    per = np.array([a.elapsed_time(b) for a, b in zip(starts, ends)])
+    assert s.status() == 0, "device status set"
+    s.close()
+    return w0, ev_ms / steps, wall / steps * 1e3, float(np.median(per)), nsets
+
+
+def cpu_baseline(name, budget_s=10.0):
+    """The reference sampler (compiled from the reference's own sources,
+    oracle/_ref) on this host, one thread, rows in order as the reference
+    engine samples them (engine.cpp:541-557); the C++ restatement when the
+    reference build is absent."""
+    from oracle import pyoracle as O
+    kind = "reference" if O.ref_available() else "port"
+    w = W.make(name)
+    rows_done = 0
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        if w.n_seq:
+            O.verify(w, threads=1)
+        elif kind == "reference":
+            O.ref_sample_batch(w, threads=1)
+        else:
+            O.sample_batch(w, threads=1)
+        rows_done += w.rows
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 50:
+            break
+    if w.n_seq:
+        kind = "port"  # the reference has no batched verify; the oracle restates its loop
+    return {"value": rows_done / el, "unit": "rows/s", "cores": 1, "kind": kind,
+            "sample": f"{reps} x {name} batch ({w.rows} rows, V={w.vocab}), single thread, "
+                      f"{el:.1f} s"}
+
+
+def copy_calibration(mib: int, reps: int = 20):
+    """A plain device copy of known size (for scaling FETCH_SIZE/WRITE_SIZE:
+    each dispatch must read and write exactly `mib` MiB)."""
+    import torch
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n * 4, "dispatches": reps}), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c2", choices=sorted(CONFIG_TEXT))
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="only run a plain copy of MIB MiB (counter calibration)")
+    args = ap.parse_args()
+    if args.copy_calib:
+        copy_calibration(args.copy_calib)
+        return
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); "
+              "rows shard across GPUs with no exchange, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+    w, ms_step, wall_ms, ms_launch, nsets = gpu_bench(args.workload, args.steps, args.warmup)
+    rows = w.rows
+    alg = w.algorithmic_bytes()
+    achieved = alg / (ms_launch * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": rows / (ms_step * 1e-3),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if w.dtype == "bf16" else "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{args.workload}: {CONFIG_TEXT[args.workload]}",
+                   "rows": rows, "vocab": w.vocab, "input_sets": nsets},
+        "hbm_gbps": alg / (ms_step * 1e-3) / 1e9,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes": alg, "ms_per_launch": ms_launch},
+        "wall_ms_per_step": wall_ms,
+    }
+    if not args.no_cpu:
+        cb = cpu_baseline(args.workload, args.cpu_seconds)
+        line["cpu_baseline"] = cb
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -66,42 +66,125 @@ __device__ __forceinline__ float tempered(float p, float maxl, float inv_t) {
 }
 
 // ------------------------------------------------------ wave reductions ----
+// Wave64 reductions and scans on DPP lane moves (VALU, no LDS round trip):
+// quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror and row_mirror give every
+// lane its 16-lane row total; row_bcast:15 (rows 1,3) and row_bcast:31
+// (rows 2,3) fold the rows so lane 63 holds the wave total, which readlane
+// broadcasts. Lanes a DPP move does not feed receive the identity `old`.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ int dpp_i(int old, int x) {
+    return __builtin_amdgcn_update_dpp(old, x, CTRL, ROWS, 0xF, false);
+}
+__device__ __forceinline__ float dpp_f_dummy(float x) { return x; }
+
+#define LCS_WAVE_REDUCE_32(T, x, ident, COMBINE)                                  \
+    do {                                                                          \
+        const int id_ = __builtin_bit_cast(int, (T)(ident));                      \
+        int v_ = __builtin_bit_cast(int, (x));                                    \
+        T o_;                                                                     \
+        o_ = __builtin_bit_cast(T, dpp_i<0xB1>(id_, v_)); x = COMBINE(x, o_); v_ = __builtin_bit_cast(int, (x)); \
+        o_ = __builtin_bit_cast(T, dpp_i<0x4E>(id_, v_)); x = COMBINE(x, o_); v_ = __builtin_bit_cast(int, (x)); \
+        o_ = __builtin_bit_cast(T, dpp_i<0x141>(id_, v_)); x = COMBINE(x, o_); v_ = __builtin_bit_cast(int, (x)); \
+        o_ = __builtin_bit_cast(T, dpp_i<0x140>(id_, v_)); x = COMBINE(x, o_); v_ = __builtin_bit_cast(int, (x)); \
+        o_ = __builtin_bit_cast(T, dpp_i<0x142, 0xA>(id_, v_)); x = COMBINE(x, o_); v_ = __builtin_bit_cast(int, (x)); \
+        o_ = __builtin_bit_cast(T, dpp_i<0x143, 0xC>(id_, v_)); x = COMBINE(x, o_); v_ = __builtin_bit_cast(int, (x)); \
+        x = __builtin_bit_cast(T, __builtin_amdgcn_readlane(v_, 63));             \
+    } while (0)
+
+__device__ __forceinline__ float f_max(float a, float b) { return fmaxf(a, b); }
+__device__ __forceinline__ float f_min(float a, float b) { return fminf(a, b); }
+__device__ __forceinline__ uint32_t u_add(uint32_t a, uint32_t b) { return a + b; }
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    LCS_WAVE_REDUCE_32(float, v, -__builtin_huge_valf(), f_max);
     return v;
 }
 __device__ __forceinline__ float wave_min(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, kWave));
-    return v;
-}
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    LCS_WAVE_REDUCE_32(float, v, __builtin_huge_valf(), f_min);
     return v;
 }
 __device__ __forceinline__ uint32_t wave_sum_u(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    LCS_WAVE_REDUCE_32(uint32_t, v, 0u, u_add);
     return v;
 }
-// argmax with first-index tie rule
-__device__ __forceinline__ void wave_argmax(float& v, uint32_t& i) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(v, o, kWave);
-        const uint32_t oi = __shfl_xor(i, o, kWave);
-        if (vi_better(ov, oi, v, i)) { v = ov; i = oi; }
-    }
+
+// 64-bit payloads move as two 32-bit DPP halves with the same control.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t old, uint64_t x) {
+    const int lo = dpp_i<CTRL, ROWS>((int)(uint32_t)old, (int)(uint32_t)x);
+    const int hi = dpp_i<CTRL, ROWS>((int)(uint32_t)(old >> 32), (int)(uint32_t)(x >> 32));
+    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t x, int lane) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), lane);
+    return ((uint64_t)hi << 32) | lo;
+}
+#define LCS_WAVE_REDUCE_64(x, ident, COMBINE)                                     \
+    do {                                                                          \
+        const uint64_t id_ = (ident);                                             \
+        x = COMBINE(x, dpp_u64<0xB1>(id_, x));                                    \
+        x = COMBINE(x, dpp_u64<0x4E>(id_, x));                                    \
+        x = COMBINE(x, dpp_u64<0x141>(id_, x));                                   \
+        x = COMBINE(x, dpp_u64<0x140>(id_, x));                                   \
+        x = COMBINE(x, dpp_u64<0x142, 0xA>(id_, x));                              \
+        x = COMBINE(x, dpp_u64<0x143, 0xC>(id_, x));                              \
+        x = readlane_u64(x, 63);                                                  \
+    } while (0)
+
+__device__ __forceinline__ uint64_t u64_min(uint64_t a, uint64_t b) { return b < a ? b : a; }
+__device__ __forceinline__ uint64_t d_add_bits(uint64_t a, uint64_t b) {
+    return (uint64_t)__double_as_longlong(__longlong_as_double((long long)a) +
+                                          __longlong_as_double((long long)b));
 }
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint64_t w = __shfl_xor(v, o, kWave);
-        v = w < v ? w : v;
-    }
+    LCS_WAVE_REDUCE_64(v, ~0ull, u64_min);
     return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+    uint64_t b = (uint64_t)__double_as_longlong(v);
+    LCS_WAVE_REDUCE_64(b, 0ull, d_add_bits);  // +0.0 identity
+    return __longlong_as_double((long long)b);
+}
+// argmax with the first-index tie rule: the pair travels as a 64-bit rank
+// key (descending value, ascending index; -0 and +0 equal), so the wave min
+// of rank keys is the argmax.
+__device__ __forceinline__ void wave_argmax(float& v, uint32_t& i) {
+    const uint32_t k = (v == 0.0f ? 0x80000000u
+                                  : ((__float_as_uint(v) & 0x80000000u) ? ~__float_as_uint(v)
+                                                                        : (__float_as_uint(v) | 0x80000000u)));
+    uint64_t r = ((uint64_t)(~k) << 32) | i;
+    r = wave_min_u64(r);
+    i = (uint32_t)r;
+    const uint32_t kk = ~(uint32_t)(r >> 32);
+    v = __uint_as_float((kk & 0x80000000u) ? (kk & 0x7fffffffu) : ~kk);
+}
+// Inclusive wave scan of doubles (row_shr 1,2,4,8 then the two row folds).
+__device__ __forceinline__ double wave_scan_incl(double v) {
+    uint64_t b = (uint64_t)__double_as_longlong(v);
+    b = d_add_bits(b, dpp_u64<0x111>(0ull, b));
+    b = d_add_bits(b, dpp_u64<0x112>(0ull, b));
+    b = d_add_bits(b, dpp_u64<0x114>(0ull, b));
+    b = d_add_bits(b, dpp_u64<0x118>(0ull, b));
+    b = d_add_bits(b, dpp_u64<0x142, 0xA>(0ull, b));
+    b = d_add_bits(b, dpp_u64<0x143, 0xC>(0ull, b));
+    return __longlong_as_double((long long)b);
+}
+__device__ __forceinline__ uint32_t wave_scan_incl_u(uint32_t v) {
+    v += (uint32_t)dpp_i<0x111>(0, (int)v);
+    v += (uint32_t)dpp_i<0x112>(0, (int)v);
+    v += (uint32_t)dpp_i<0x114>(0, (int)v);
+    v += (uint32_t)dpp_i<0x118>(0, (int)v);
+    v += (uint32_t)dpp_i<0x142, 0xA>(0, (int)v);
+    v += (uint32_t)dpp_i<0x143, 0xC>(0, (int)v);
+    return v;
+}
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
+// Orders LDS traffic between lanes of one wave (no cross-wave barrier).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
 }
 
 // ----------------------------------------------------- block reductions ----
@@ -188,12 +271,7 @@ __device__ __forceinline__ uint64_t block_min_u64(uint64_t v, uint64_t* red) {
 template <int NT>
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t& excl, uint32_t* red) {
     const int lane = threadIdx.x & 63, w = threadIdx.x / kWave;
-    uint32_t inc = v;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const uint32_t t = __shfl_up(inc, o, kWave);
-        if (lane >= o) inc += t;
-    }
+    const uint32_t inc = wave_scan_incl_u(v);
     if (lane == 63) red[w] = inc;
     __syncthreads();
     uint32_t base = 0, total = 0;

@@ -32,8 +32,9 @@ constexpr uint32_t kOverflow = 10;
 constexpr uint32_t kNTop = 11;
 constexpr uint32_t kBulk = 12;      // f64 sum over non-window ids of exp((p - kMAll)/T)
 constexpr uint32_t kBulkErr = 14;   // f64 error bound of kBulk
-constexpr uint32_t kTop = 16;       // kTopMax x (f32 value, u32 idx)
-constexpr uint32_t kWin = kTop + 2 * kTopMax;   // kWinCap x (f32 value, u32 idx)
+constexpr uint32_t kHeader = 16;    // words before the entry arrays
+constexpr uint32_t kTop = 16;       // kTopMax x 64-bit rank key (value, idx)
+constexpr uint32_t kWin = kTop + 2 * kTopMax;   // kWinCap x 64-bit rank key
 constexpr uint32_t kWords = ((kWin + 2 * kWinCap) + 63) / 64 * 64;
 }  // namespace rec
 

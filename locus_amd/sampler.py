@@ -178,6 +178,70 @@ class Sampler:
         return o
 
     # ---------------------------------------------------------------- calls
+    def prepare(self, d, out, n_top: int | None = None, want_lp: bool | None = None,
+                has_mask=None, flags_extra: int = 0, use_host_params: bool = True):
+        """Builds the C structs of one lcs_sample call once; returns a
+        zero-argument launcher (for tight benchmark loops)."""
+        w = d["w"]
+        want_lp = w.want_logprobs if want_lp is None else want_lp
+        n_top = w.n_top if n_top is None else n_top
+        b = _Batch()
+        b.rows, b.vocab = w.rows, w.vocab
+        b.dtype = LCS_BF16 if w.dtype == "bf16" else LCS_F32
+        b.flags = (LCS_WANT_LOGPROBS if want_lp else 0) | flags_extra
+        b.row_stride = d["stride"]
+        b.logits = _dptr(d["logits"])
+        b.params = _dptr(d["params"])
+        ph = d["params_host"] if use_host_params else None
+        b.params_host = None if ph is None else ph.ctypes.data_as(C.c_void_p)
+        b.hist_off = _dptr(d.get("hist_off"))
+        b.hist_ids = _dptr(d.get("hist_ids"))
+        b.u = _dptr(d.get("u"))
+        b.mask = _dptr(d.get("mask"))
+        b.has_mask = _dptr(has_mask)
+        b.mask_words = w.mask_words
+        b.n_top = n_top if want_lp else 0
+        o = _Out()
+        o.ids = _dptr(out["ids"])
+        o.chosen_lp = _dptr(out.get("chosen_lp"))
+        o.top_ids = _dptr(out.get("top_ids"))
+        o.top_lp = _dptr(out.get("top_lp"))
+        o.diag = _dptr(out.get("diag"))
+        fn, ctx, bp, op = lib().lcs_sample, self.ctx, C.byref(b), C.byref(o)
+        keep = (ph, b, o, d, out)
+
+        def launch(stream_handle):
+            _ = keep
+            rc = fn(ctx, bp, op, stream_handle)
+            if rc != LCS_OK:
+                self._check(rc)
+        return launch
+
+    def prepare_verify(self, d, out):
+        w = d["w"]
+        b = _VBatch()
+        b.n_seq, b.rows_per_seq, b.vocab = w.n_seq, w.rows_per_seq, w.vocab
+        b.dtype = LCS_BF16 if w.dtype == "bf16" else LCS_F32
+        b.row_stride = d["stride"]
+        b.logits = _dptr(d["logits"])
+        b.draft = _dptr(d["draft"])
+        o = _VOut()
+        o.argmax_ids = _dptr(out["argmax_ids"])
+        o.draft_lp = _dptr(out["draft_lp"])
+        o.accept_len = _dptr(out["accept_len"])
+        fn, ctx, bp, op = lib().lcs_verify, self.ctx, C.byref(b), C.byref(o)
+        keep = (b, o, d, out)
+
+        def launch(stream_handle):
+            _ = keep
+            rc = fn(ctx, bp, op, stream_handle)
+            if rc != LCS_OK:
+                self._check(rc)
+        return launch
+
+    def stream_handle(self, stream=None):
+        return _stream_handle(self.torch, stream)
+
     def sample_dev(self, d, out, n_top: int | None = None, want_lp: bool | None = None,
                    has_mask=None, flags_extra: int = 0, use_host_params: bool = True, stream=None):
         """Enqueues lcs_sample on device buffers from upload()/alloc_out()."""

@@ -117,8 +117,6 @@ def test_full_size_c3(sampler):
 def test_edge_cases(sampler):
     from tests.golden.make_golden import edge_workloads
     for w in edge_workloads():
-        if w.vocab % 4:
-            continue  # covered with padded strides below
         say("edge", w.name, w.vocab)
         compare(w, run(sampler, w), O.sample_batch(w), f"edge-{w.name}")
 
