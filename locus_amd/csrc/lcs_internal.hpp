@@ -17,25 +17,26 @@ constexpr uint32_t kTopMax = 20;        // logprob alternatives per row
 constexpr uint32_t kWinCap = 64;        // min-p window entries per slice
 constexpr uint32_t kFastHistMax = 4096; // penalty window handled by the sliced path
 
-// Slice record (uint32 words), written with device-scope stores and read by
-// the row's last-arriving workgroup.
+// Slice record (64-bit words), written with device-scope stores by each
+// slice workgroup and read by the row's last-arriving workgroup.
 namespace rec {
-constexpr uint32_t kMRaw = 0;       // f32 raw max of the slice
-constexpr uint32_t kSRaw = 2;       // f64 sum exp(raw - kMRaw)
-constexpr uint32_t kMAll = 4;       // f32 penalised max over all ids, then idx
-constexpr uint32_t kIAll = 5;
-constexpr uint32_t kMMsk = 6;       // f32 penalised max over allowed ids, then idx
-constexpr uint32_t kIMsk = 7;
-constexpr uint32_t kNAllowed = 8;
-constexpr uint32_t kNWin = 9;
-constexpr uint32_t kOverflow = 10;
-constexpr uint32_t kNTop = 11;
-constexpr uint32_t kBulk = 12;      // f64 sum over non-window ids of exp((p - kMAll)/T)
-constexpr uint32_t kBulkErr = 14;   // f64 error bound of kBulk
-constexpr uint32_t kHeader = 16;    // words before the entry arrays
-constexpr uint32_t kTop = 16;       // kTopMax x 64-bit rank key (value, idx)
-constexpr uint32_t kWin = kTop + 2 * kTopMax;   // kWinCap x 64-bit rank key
-constexpr uint32_t kWords = ((kWin + 2 * kWinCap) + 63) / 64 * 64;
+constexpr uint32_t kHdr = 8;         // header words:
+// 0: f32 raw max | u16 window entries << 32 | u16 flags << 48
+// 1: f64 sum exp(raw - raw max)
+// 2: f32 penalised max | u32 its index (first index of the max)
+// 3: f32 penalised max over allowed ids | u32 its index
+// 4: u32 allowed ids | u32 top-n entries
+// 5: f64 bulk: sum over the slice of exp((p - penalised max) / T), f32 terms
+// 6: f64 error bound of word 5 (against the reference's own f64 weights)
+// 7: f32 raw logit at word 2's index | f32 raw logit at word 3's index
+constexpr uint32_t kTop = kHdr;                    // kTopMax rank keys, ascending
+constexpr uint32_t kWin = kTop + kTopMax;          // kWinCap rank keys, ascending
+constexpr uint32_t kWinRaw = kWin + kWinCap;       // kWinCap raw logits (f32 in the low half)
+constexpr uint32_t kWords64 = (kWinRaw + kWinCap + 7) / 8 * 8;
+constexpr uint32_t kWords = 2 * kWords64;          // in uint32 units (workspace sizing)
+constexpr uint32_t kFlagWinTrunc = 1u;             // more window entries than kWinCap (top kWinCap kept)
+constexpr uint32_t kFlagCandOverflow = 2u;         // more top-n candidates than the slice holds
+constexpr uint32_t kFlagWinLost = 4u;              // more window entries than the slice could rank
 }  // namespace rec
 
 // ---- single-workgroup exact path ----

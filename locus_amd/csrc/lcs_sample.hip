@@ -134,6 +134,7 @@ struct ExactSmem {
     float out_boundary;
     double out_kept_sum;
     double out_S;
+    SampleArgs args;   // the launch arguments, for the out-of-line call (no private copy)
 };
 
 struct MassPrefix {
@@ -907,6 +908,16 @@ write_back:
 }
 
 // ================================================================ kernels ==
+// Copies the launch arguments into LDS for the out-of-line exact path, one
+// dword per lane straight from the kernel argument segment (a reference to
+// the by-value argument would give every lane a private copy in scratch).
+__device__ __forceinline__ void stage_args(SampleArgs* dst) {
+    static_assert(sizeof(SampleArgs) % 4 == 0 && sizeof(SampleArgs) / 4 <= 64, "args size");
+    const uint32_t* src = (const uint32_t*)__builtin_amdgcn_kernarg_segment_ptr();
+    if (threadIdx.x < sizeof(SampleArgs) / 4) reinterpret_cast<uint32_t*>(dst)[threadIdx.x] = src[threadIdx.x];
+    __syncthreads();
+}
+
 template <int G>
 __global__ __launch_bounds__(kGenThreads) void general_kernel(SampleArgs a) {
     __shared__ ExactSmem<kGenThreads, kGenBins, kGenCap, kGenHistCap> sm;
@@ -916,7 +927,8 @@ __global__ __launch_bounds__(kGenThreads) void general_kernel(SampleArgs a) {
     const bool masked = a.mask != nullptr && (a.has_mask == nullptr || a.has_mask[row] != 0);
     const bool force = (a.flags & LCS_WRITE_PENALIZED) != 0;
     if (!force && row_mode(P, masked, a.vocab) != kModeGeneral) return;
-    exact_row<kGenThreads, kGenBins, kGenCap, kGenHistCap, G>(a, row, sm);
+    stage_args(&sm.args);
+    exact_row<kGenThreads, kGenBins, kGenCap, kGenHistCap, G>(sm.args, row, sm);
 }
 
 // ============================================================ sliced path ==
@@ -934,48 +946,91 @@ __device__ uint64_t g_prof[16384 * 16];
     } while (0)
 #endif
 
-constexpr uint32_t kFinWinCap = 512;   // window entries the finalize can rank
 constexpr int kSliceWaves = kSliceThreads / kWave;
+constexpr uint32_t kCandCap = 128;   // top-n candidates one slice can hold
+constexpr uint32_t kWinLds = 256;    // window entries one slice can rank
+constexpr uint32_t kSpecWin = 8;     // window entries fetched with each slice header
+constexpr uint32_t kRowWin = 4 * kWave;  // row-window entries the finalize can rank
+constexpr float kLog2E = 1.4426950408889634f;
 
 // cross-wave partials of a slice's local phase
 struct SliceLocal {
     float mraw[kSliceWaves];
-    double se[kSliceWaves];
-    float mall[kSliceWaves];
-    uint32_t iall[kSliceWaves];
+    float mpen[kSliceWaves];
+    uint32_t ipen[kSliceWaves];
+    float rpen[kSliceWaves];
     float mmsk[kSliceWaves];
     uint32_t imsk[kSliceWaves];
+    float rmsk[kSliceWaves];
     uint32_t nall[kSliceWaves];
+    double sraw[kSliceWaves];
     double bulk[kSliceWaves];
-    double berr[kSliceWaves];
-    uint64_t wtop[kSliceWaves][kTopMax];
-    uint64_t win[kWinCap];
-    uint32_t nwin;
+    double bterm[kSliceWaves];
+    uint32_t ncand, nwin, last, fallback;
+    uint64_t cand[kCandCap];
+    uint64_t win[kWinLds];
+    float winraw[kWinLds];
 };
 // the row's finalize (wave 0 of the last-arriving workgroup)
 struct SliceFin {
-    uint64_t top[kMaxSlices * kTopMax];
-    uint64_t ent[kFinWinCap];
-    uint64_t sorted[kFinWinCap];
-    uint32_t base[kMaxSlices + 1];
+    uint64_t top[kWave * kTopMax];
+    uint64_t ent[kRowWin];
+    float entraw[kRowWin];
+    uint64_t sorted[kRowWin];
+    float sortedraw[kRowWin];
+    double sw[kRowWin];
 };
 struct SliceSmem {
     union {
-        uint32_t cnt[kSliceMax / 2];     // packed u16 penalty counts of the slice
+        uint32_t ovr[kSliceMax];      // penalised-logit bits per slice position (0 = none)
+        uint4 ovr4[kSliceMax / 4];
         SliceFin f;
         ExactSmem<kSliceThreads, kFbBins, kFbCap, kFbHistCap> ex;
     } u;
     SliceLocal l;
-    uint32_t last;
-    uint32_t fallback;
 };
 
-// Finalize of a row by wave 0 of its last-arriving workgroup: merges the
-// slice records with wave-parallel DPP reductions/scans and ballots.
-// Returns true when the row needs the exact single-workgroup walk.
-template <int G>
-__device__ __noinline__ bool slice_finalize(const SampleArgs& a, uint32_t row, uint32_t mode,
-                                            SliceSmem& sm) {
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ double bits_d(uint64_t b) { return __longlong_as_double((long long)b); }
+__device__ __forceinline__ uint64_t d_bits(double d) { return (uint64_t)__double_as_longlong(d); }
+__device__ __forceinline__ uint64_t pack2(uint32_t lo, uint32_t hi) { return ((uint64_t)hi << 32) | lo; }
+
+// Ranks n <= 4*64 unique keys held in LDS by one wave: lane l owns entries
+// l, l+64, l+128, l+192 (k[c], ~0 past n) and gets their ascending ranks.
+__device__ __forceinline__ void wave_rank4(const uint64_t* keys, uint32_t n, uint64_t (&k)[4],
+                                           uint32_t (&rk)[4]) {
+    const uint32_t lane = (uint32_t)lane_id();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t e = lane + (uint32_t)c * kWave;
+        k[c] = e < n ? keys[e] : ~0ull;
+        rk[c] = 0;
+    }
+    if (n <= (uint32_t)kWave) {
+        for (uint32_t f = 0; f < n; ++f) rk[0] += readlane_u64(k[0], (int)f) < k[0] ? 1u : 0u;
+        return;
+    }
+    const uint32_t nch = (n + kWave - 1) / kWave;
+    for (uint32_t c2 = 0; c2 < nch; ++c2) {
+        const uint64_t src = c2 == 0 ? k[0] : c2 == 1 ? k[1] : c2 == 2 ? k[2] : k[3];
+        const uint32_t cnt = min((uint32_t)kWave, n - c2 * kWave);
+        for (uint32_t f = 0; f < cnt; ++f) {
+            const uint64_t o = readlane_u64(src, (int)f);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) rk[c] += o < k[c] ? 1u : 0u;
+        }
+    }
+}
+
+// Finalize of a row by wave 0 of its last-arriving workgroup. One round trip
+// brings every slice's header, top-n list and leading window entries; the
+// row window (entries within delta of the row max) is ranked in registers and
+// the reference's top-p / min-p / draw walk runs as wave scans. Returns true
+// when the row needs the exact single-workgroup path: a window or candidate
+// list overflowed, the row window holds more than kRowWin entries, or a
+// top-p / min-p decision lies within the normaliser's error bound.
+__device__ __forceinline__ bool slice_finalize(const SampleArgs& a, uint32_t row, uint32_t mode,
+                                               SliceSmem& sm) {
     const int lane = lane_id();
     const uint32_t S = a.slices, V = a.vocab;
     const lcs_params P = a.params[row];
@@ -984,72 +1039,85 @@ __device__ __noinline__ bool slice_finalize(const SampleArgs& a, uint32_t row, u
     const bool masked = a.mask != nullptr && (a.has_mask == nullptr || a.has_mask[row] != 0);
     const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
     const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
-    const uint32_t* recs = a.recs + (uint64_t)row * S * rec::kWords;
+    const uint64_t* recs = reinterpret_cast<const uint64_t*>(a.recs) + (uint64_t)row * S * rec::kWords64;
     const bool mine = (uint32_t)lane < S;
-    const uint32_t* myrec = recs + (uint64_t)(mine ? lane : 0) * rec::kWords;
+    const uint64_t* my = recs + (uint64_t)(mine ? lane : 0) * rec::kWords64;
+    const float NEG = -__builtin_huge_valf();
 
-    // round trip 1: headers and top-n entries (counts are known: min(n, slice))
-    uint32_t h[rec::kHeader];
+    // ---- one round trip: headers, top-n lists, leading window entries ----
+    uint64_t h[rec::kHdr];
 #pragma unroll
-    for (int k = 0; k < (int)rec::kHeader; ++k) h[k] = ld_dev(myrec + k);
-    const uint32_t slice_len_s = mine ? min(a.slice_len, V - lane * a.slice_len) : 0u;
-    const uint32_t nts = mine ? min(ntop, slice_len_s) : 0u;
+    for (int k = 0; k < (int)rec::kHdr; ++k) h[k] = ld_dev_u64(my + k);
     uint64_t tk[kTopMax];
 #pragma unroll
-    for (int j = 0; j < (int)kTopMax; ++j) {
-        tk[j] = (j < (int)nts) ? ld_dev_u64(reinterpret_cast<const uint64_t*>(myrec + rec::kTop + 2 * j))
-                               : ~0ull;
-    }
-    auto f32 = [](uint32_t x) { return __uint_as_float(x); };
-    auto f64 = [&](int w) { return __longlong_as_double((long long)(((uint64_t)h[w + 1] << 32) | h[w])); };
-    const float NEG = -__builtin_huge_valf();
-    const float m_raw = mine ? f32(h[rec::kMRaw]) : NEG;
-    const double s_raw = mine ? f64(rec::kSRaw) : 0.0;
-    const float m_all = mine ? f32(h[rec::kMAll]) : NEG;
-    const uint32_t i_all = mine ? h[rec::kIAll] : 0xfffffffeu;
-    const float m_msk = mine ? f32(h[rec::kMMsk]) : NEG;
-    const uint32_t i_msk = mine ? h[rec::kIMsk] : 0xfffffffeu;
-    const uint32_t n_allowed = mine ? h[rec::kNAllowed] : 0u;
-    const uint32_t n_win = mine ? h[rec::kNWin] : 0u;
-    const uint32_t ovf = mine ? h[rec::kOverflow] : 0u;
-    const double bulk = mine ? f64(rec::kBulk) : 0.0;
-    const double berr = mine ? f64(rec::kBulkErr) : 0.0;
-
-    // raw log-normaliser (logprobs_from over the whole row)
-    const float M = wave_max(m_raw);
-    const double z = wave_sum(mine ? s_raw * exp((double)m_raw - (double)M) : 0.0);
-    const double log_z = log(z) + (double)M;
-
-    // top-n: k-way merge of the slices' sorted lists (lane s holds list s)
-    uint64_t topk[kTopMax];
-    if (ntop) {
+    for (int j = 0; j < (int)kTopMax; ++j) tk[j] = (uint32_t)j < ntop ? ld_dev_u64(my + rec::kTop + j) : ~0ull;
+    const bool stoch = mode == kModeWindow;
+    uint64_t wk[kSpecWin];
+    uint32_t wr[kSpecWin];
+    if (stoch) {
 #pragma unroll
-        for (int j = 0; j < (int)kTopMax; ++j) sm.u.f.top[lane * kTopMax + j] = mine ? tk[j] : ~0ull;
-        wave_sync();
-        uint32_t p = 0;
-        for (uint32_t r = 0; r < ntop; ++r) {
-            const uint64_t head = (mine && p < nts) ? sm.u.f.top[lane * kTopMax + p] : ~0ull;
-            const uint64_t best = wave_min_u64(head);
-            topk[r < kTopMax ? r : 0] = best;
-            if (head == best && best != ~0ull) ++p;
-            if (lane == 0) {
-                a.top_ids[(uint64_t)row * a.n_top + r] = (int32_t)rank_idx(best);
-                a.top_lp[(uint64_t)row * a.n_top + r] = (float)((double)rank_val(best) - log_z);
-            }
+        for (int j = 0; j < (int)kSpecWin; ++j) {
+            wk[j] = ld_dev_u64(my + rec::kWin + j);
+            wr[j] = (uint32_t)ld_dev_u64(my + rec::kWinRaw + j);
         }
     }
-    (void)topk;
+    const float m_raw = mine ? __uint_as_float((uint32_t)h[0]) : NEG;
+    const uint32_t n_win = mine ? (uint32_t)(h[0] >> 32) & 0xffffu : 0u;
+    const uint32_t flags = mine ? (uint32_t)(h[0] >> 48) : 0u;
+    const double s_raw = mine ? bits_d(h[1]) : 0.0;
+    const float m_pen = mine ? __uint_as_float((uint32_t)h[2]) : NEG;
+    const uint32_t i_pen = mine ? (uint32_t)(h[2] >> 32) : kNoIdx;
+    const float m_msk = mine ? __uint_as_float((uint32_t)h[3]) : NEG;
+    const uint32_t i_msk = mine ? (uint32_t)(h[3] >> 32) : kNoIdx;
+    const uint32_t n_allowed = mine ? (uint32_t)h[4] : 0u;
+    const uint32_t nts = mine ? (uint32_t)(h[4] >> 32) : 0u;
+    const double bulk = mine ? bits_d(h[5]) : 0.0;
+    const double berr = mine ? bits_d(h[6]) : 0.0;
+
+    // ---- raw log-normaliser (logprobs_from over the whole row) ----
+    const float M = wave_max(m_raw);
+    double log_z = 0.0;
+    if (want_lp) {
+        const double z = wave_sum(mine && m_raw != NEG ? s_raw * exp((double)m_raw - (double)M) : 0.0);
+        log_z = log(z) + (double)M;
+    }
+    // ---- top-n: k-way merge of the slices' ascending rank-key lists ----
+    if (ntop) {
+        if (ballot(mine && (flags & rec::kFlagCandOverflow))) return true;
+#pragma unroll
+        for (int j = 0; j < (int)kTopMax; ++j) {
+            if ((uint32_t)j < ntop) sm.u.f.top[lane * kTopMax + j] = (mine && (uint32_t)j < nts) ? tk[j] : ~0ull;
+        }
+        wave_sync();
+        uint32_t p = 0;
+        uint64_t myk = ~0ull;
+        for (uint32_t r = 0; r < ntop; ++r) {
+            const uint64_t head = p < ntop ? sm.u.f.top[lane * kTopMax + p] : ~0ull;
+            const uint64_t best = wave_min_u64(head);
+            if (head == best && best != ~0ull) ++p;
+            if ((uint32_t)lane == r) myk = best;
+        }
+        if ((uint32_t)lane < ntop) {
+            a.top_ids[(uint64_t)row * a.n_top + lane] = (int32_t)rank_idx(myk);
+            a.top_lp[(uint64_t)row * a.n_top + lane] = (float)((double)rank_val(myk) - log_z);
+        }
+    }
     const uint32_t tot_allowed = wave_sum_u(n_allowed);
 
     if (mode == kModeGreedy) {
         const bool use_mask = masked && tot_allowed > 0;
-        float bv = use_mask ? m_msk : m_all;
-        uint32_t bi = use_mask ? i_msk : i_all;
-        if (bi >= V) { bv = NEG; bi = 0xfffffffeu; }
+        float bv = use_mask ? m_msk : m_pen;
+        uint32_t bi = use_mask ? i_msk : i_pen;
+        float braw = use_mask ? __uint_as_float((uint32_t)(h[7] >> 32)) : __uint_as_float((uint32_t)h[7]);
+        if (bi >= V) { bv = NEG; bi = kNoIdx; }
+        const float bv0 = bv;
+        const uint32_t bi0 = bi;
         wave_argmax(bv, bi);
+        const uint64_t own = ballot(bi0 == bi && bv0 == bv && bi < V);
+        braw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(braw), own ? __builtin_ctzll(own) : 0));
         if (lane == 0) {
             a.ids[row] = (int32_t)bi;
-            if (want_lp) a.chosen_lp[row] = (float)((double)load_elem(rowp, a.dtype, bi) - log_z);
+            if (want_lp) a.chosen_lp[row] = (float)((double)braw - log_z);
             if (a.diag) {
                 lcs_row_diag dg{};
                 dg.n_cand = use_mask ? tot_allowed : V; dg.maxl = bv; dg.boundary = bv;
@@ -1060,128 +1128,141 @@ __device__ __noinline__ bool slice_finalize(const SampleArgs& a, uint32_t row, u
         return false;
     }
 
-    // ---- min-p window ----
+    // ---- the row window: entries with p >= maxl - delta ----
     const float inv_t = fdiv(1.0f, P.temperature);
     const double delta = (double)P.temperature * (-log((double)P.min_p) + 1e-3);
-    const float maxl = wave_max(m_all);
-    uint32_t base_s = wave_scan_incl_u(n_win) - n_win;
-    const uint32_t nw = wave_sum_u(n_win);
-    if (wave_sum_u(ovf) != 0 || nw > kFinWinCap || nw == 0) return true;
-    // round trip 2: window entries (entry e of slice s goes to ent[base_s + e])
-    if (mine) sm.u.f.base[lane] = base_s;
-    if (lane == 0) sm.u.f.base[S] = nw;
-    wave_sync();
-    constexpr int kPer = kFinWinCap / kWave;  // 8
-    uint64_t ek[kPer];
+    const float maxl = wave_max(m_pen);
+    const double thr = (double)maxl - delta;
+    // a slice that could hold row-window entries must not have lost any
+    if (ballot(mine && (flags & rec::kFlagWinLost) && (double)m_pen >= thr)) return true;
+    uint32_t q = 0;
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-        const uint32_t e = (uint32_t)lane + (uint32_t)k * kWave;
-        const uint32_t ee = e < nw ? e : 0u;
-        uint32_t s = 0;
-        while (s + 1 < S && sm.u.f.base[s + 1] <= ee) ++s;
-        const uint32_t j = ee - sm.u.f.base[s];
-        ek[k] = ld_dev_u64(reinterpret_cast<const uint64_t*>(recs + (uint64_t)s * rec::kWords + rec::kWin + 2 * j));
+    for (int j = 0; j < (int)kSpecWin; ++j)
+        q += ((uint32_t)j < n_win && (double)rank_val(wk[j]) >= thr) ? 1u : 0u;
+    const uint32_t base = wave_scan_incl_u(q) - q;
+    uint32_t L0 = wave_sum_u(q);
+    if (L0 > kRowWin) return true;
+#pragma unroll
+    for (int j = 0; j < (int)kSpecWin; ++j) {
+        if ((uint32_t)j < q) {
+            sm.u.f.ent[base + j] = wk[j];
+            sm.u.f.entraw[base + j] = __uint_as_float(wr[j]);
+        }
     }
+    // slices whose leading entries all qualify and that hold more (rare);
+    // entries are in ascending rank order, so the qualifying ones lead
+    uint32_t qtot = q;
+    bool more = mine && q == kSpecWin && n_win > kSpecWin;
+    for (uint32_t j0 = kSpecWin; ballot(more); j0 += kSpecWin) {
+        uint64_t ek[kSpecWin];
+        uint32_t er[kSpecWin];
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-        const uint32_t e = (uint32_t)lane + (uint32_t)k * kWave;
-        if (e < nw) sm.u.f.ent[e] = ek[k];
+        for (int j = 0; j < (int)kSpecWin; ++j) {
+            const uint32_t jj = min(j0 + j, kWinCap - 1);
+            ek[j] = more ? ld_dev_u64(my + rec::kWin + jj) : ~0ull;
+            er[j] = more ? (uint32_t)ld_dev_u64(my + rec::kWinRaw + jj) : 0u;
+        }
+        uint32_t qq = 0;
+#pragma unroll
+        for (int j = 0; j < (int)kSpecWin; ++j)
+            qq += (more && j0 + j < n_win && (double)rank_val(ek[j]) >= thr) ? 1u : 0u;
+        const uint32_t b2 = L0 + wave_scan_incl_u(qq) - qq;
+        L0 += wave_sum_u(qq);
+        if (L0 > kRowWin) return true;
+#pragma unroll
+        for (int j = 0; j < (int)kSpecWin; ++j) {
+            if ((uint32_t)j < qq) {
+                sm.u.f.ent[b2 + j] = ek[j];
+                sm.u.f.entraw[b2 + j] = __uint_as_float(er[j]);
+            }
+        }
+        qtot += qq;
+        more = more && qq == kSpecWin && j0 + kSpecWin < n_win;
     }
+    // a truncated slice whose every kept entry qualifies may hold more
+    if (ballot(mine && (flags & rec::kFlagWinTrunc) && qtot == n_win)) return true;
     wave_sync();
-    // rank each entry among all (keys are unique), scatter into order
+    // rank the row window (keys are unique)
+    {
+        uint64_t k[4];
+        uint32_t rk[4];
+        wave_rank4(sm.u.f.ent, L0, k, rk);
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-        const uint32_t e = (uint32_t)lane + (uint32_t)k * kWave;
-        if (e < nw) {
-            uint32_t rk = 0;
-            for (uint32_t f = 0; f < nw; ++f) rk += sm.u.f.ent[f] < ek[k] ? 1u : 0u;
-            sm.u.f.sorted[rk] = ek[k];
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
+            if (e < L0) { sm.u.f.sorted[rk[c]] = k[c]; sm.u.f.sortedraw[rk[c]] = sm.u.f.entraw[e]; }
         }
     }
     wave_sync();
-    // normaliser: exact window part + rescaled slice tails with their bound
-    double sw = 0.0;
-    for (uint32_t e = lane; e < nw; e += kWave) sw += exp((double)tempered(rank_val(sm.u.f.sorted[e]), maxl, inv_t));
-    const double d_s = mine ? ((double)m_all - (double)maxl) * (double)inv_t : 0.0;
-    const double es = mine ? exp(d_s) : 0.0;
-    const double S_win = wave_sum(sw);
-    const double S_tail = wave_sum(mine ? bulk * es : 0.0);
-    const double eps = wave_sum(mine ? es * (berr + fabs(d_s) * 0x1p-23 * bulk) : 0.0);
-    const double Sf = S_win + S_tail;
+
+    // ---- normaliser: slice bulks rescaled to the row max, with their bound ----
+    const double d_s = mine ? ((double)m_pen - (double)maxl) * (double)inv_t : 0.0;
+    const double es = mine && m_pen != NEG ? exp(d_s) : 0.0;
+    const double Sf = wave_sum(es * bulk);
+    const double eps = wave_sum(es * (berr + fabs(d_s) * 0x1p-50 * bulk));
     const double rel = 2.0 * eps / Sf + 0x1p-50;
-    // L0: the sorted prefix within delta of the row max
-    uint32_t L0 = 0;
-    for (uint32_t c = 0; c < nw; c += kWave) {
-        const uint32_t i = c + lane;
-        const bool in = i < nw && (double)rank_val(sm.u.f.sorted[i]) >= (double)maxl - delta;
-        L0 += wave_sum_u(in ? 1u : 0u);
-    }
-    // walk the prefix in chunks of 64 (scans replace the reference's sequential sums)
+
+    // ---- top-p, then min-p (sampling.cpp order), 64 ranked entries at a time ----
     bool uncertain = false;
-    uint32_t keep_p = 0xffffffffu;
+    uint32_t keep_p = 0xffffffffu, keep = 0;
     const double tp = (double)P.top_p;
-    const double w0 = 1.0;  // exp(0): the max candidate
-    const double thresh = (double)P.min_p * (w0 / Sf);
-    uint32_t keep = 0;
+    const double thresh = (double)P.min_p * (1.0 / Sf);
     double cum_c = 0.0;
-    for (uint32_t c = 0; c < L0 && keep == 0; c += kWave) {
-        const uint32_t i = c + lane;
+    for (uint32_t c0 = 0; c0 < L0 && keep == 0; c0 += kWave) {
+        const uint32_t i = c0 + (uint32_t)lane;
         const bool in = i < L0;
-        const double wi = in ? exp((double)tempered(rank_val(sm.u.f.sorted[i]), maxl, inv_t)) : 0.0;
-        const double qi = in ? wi / Sf : 0.0;
+        const double w = in ? exp((double)tempered(rank_val(sm.u.f.sorted[i]), maxl, inv_t)) : 0.0;
+        if (in) sm.u.f.sw[i] = w;
+        const double qi = w / Sf;
         const double cum = cum_c + wave_scan_incl(qi);
         if (P.top_p < 1.0f && keep_p == 0xffffffffu) {
             const uint64_t hit = ballot(in && cum >= tp);
             if (hit) {
                 const int hl = __builtin_ctzll(hit);
-                const double ch = __longlong_as_double((long long)readlane_u64((uint64_t)__double_as_longlong(cum), hl));
-                const double cp = hl > 0 ? __longlong_as_double((long long)readlane_u64((uint64_t)__double_as_longlong(cum), hl - 1)) : cum_c;
+                const double ch = bits_d(readlane_u64(d_bits(cum), hl));
+                const double cp = hl > 0 ? bits_d(readlane_u64(d_bits(cum), hl - 1)) : cum_c;
                 if (ch - tp <= rel * ch + 1e-13) uncertain = true;
-                if ((c + hl) > 0 && tp - cp <= rel * cp + 1e-13) uncertain = true;
-                keep_p = c + hl + 1;
+                if (c0 + (uint32_t)hl > 0 && tp - cp <= rel * cp + 1e-13) uncertain = true;
+                keep_p = c0 + (uint32_t)hl + 1u;
             }
         }
-        // min-p: first i in [1, min(keep_p, L0)) with w_i/S < thresh
+        // min-p: first i in [1, min(keep_p, L0)) with w_i/S < thresh; the
+        // entry after the row window fails it by construction (margin 1e-3 in ln w)
         const uint32_t lim = min(keep_p, L0);
         const bool cmp = in && i >= 1 && i < lim;
-        if (cmp && fabs(wi / ((double)P.min_p * w0) - 1.0) <= 1e-12) uncertain = true;
+        if (ballot(cmp && fabs(w / (double)P.min_p - 1.0) <= 1e-12)) uncertain = true;
         const uint64_t fail = ballot(cmp && qi < thresh);
-        if (fail) {
-            keep = c + __builtin_ctzll(fail);
-        } else if (lim <= c + kWave) {
-            keep = lim;
-        }
-        cum_c = __longlong_as_double((long long)readlane_u64((uint64_t)__double_as_longlong(cum), 63));
+        if (fail) keep = c0 + (uint32_t)__builtin_ctzll(fail);
+        else if (lim <= c0 + kWave) keep = lim;
+        cum_c = bits_d(readlane_u64(d_bits(cum), kWave - 1));
     }
     if (P.top_p < 1.0f && keep_p == 0xffffffffu && tp - cum_c <= rel * cum_c + 1e-13) uncertain = true;
-    uncertain = ballot(uncertain) != 0;
     if (uncertain) return true;
     if (keep < 1) keep = 1;
-    // kept mass and the draw (r -= w_i walk) over the first `keep`
-    const double u = a.u[row];
-    double wc = 0.0, kept_sum = 0.0;
-    for (uint32_t c = 0; c < keep; c += kWave) {
-        const uint32_t i = c + lane;
-        const double wi = i < keep ? exp((double)tempered(rank_val(sm.u.f.sorted[i]), maxl, inv_t)) : 0.0;
-        wc += wave_sum(wi);
+    wave_sync();
+
+    // ---- kept mass and the draw (r -= w_i walk) ----
+    double kept_sum = 0.0;
+    for (uint32_t c0 = 0; c0 < keep; c0 += kWave) {
+        const uint32_t i = c0 + (uint32_t)lane;
+        kept_sum += wave_sum(i < keep ? sm.u.f.sw[i] : 0.0);
     }
-    kept_sum = wc;
-    const double r0 = u * (kept_sum - 0.0) + 0.0;
-    int32_t chosen = -1;
+    const double r0 = a.u[row] * (kept_sum - 0.0) + 0.0;
+    uint32_t pos = 0xffffffffu;
     double Wc = 0.0;
-    for (uint32_t c = 0; c < keep && chosen < 0; c += kWave) {
-        const uint32_t i = c + lane;
-        const bool in = i < keep;
-        const double wi = in ? exp((double)tempered(rank_val(sm.u.f.sorted[i]), maxl, inv_t)) : 0.0;
-        const double W = Wc + wave_scan_incl(wi);
-        const uint64_t hit = ballot(in && r0 - W <= 0.0);
-        if (hit) chosen = (int32_t)rank_idx(sm.u.f.sorted[c + __builtin_ctzll(hit)]);
-        Wc = __longlong_as_double((long long)readlane_u64((uint64_t)__double_as_longlong(W), 63));
+    for (uint32_t c0 = 0; c0 < keep && pos == 0xffffffffu; c0 += kWave) {
+        const uint32_t i = c0 + (uint32_t)lane;
+        const bool kept = i < keep;
+        const double W = Wc + wave_scan_incl(kept ? sm.u.f.sw[i] : 0.0);
+        const uint64_t hit = ballot(kept && r0 - W <= 0.0);
+        if (hit) pos = c0 + (uint32_t)__builtin_ctzll(hit);
+        Wc = bits_d(readlane_u64(d_bits(W), kWave - 1));
     }
-    if (chosen < 0) chosen = (int32_t)rank_idx(sm.u.f.sorted[keep - 1]);  // reference fallback
+    if (pos == 0xffffffffu) pos = keep - 1;  // reference fallback: cand[keep-1]
     if (lane == 0) {
-        a.ids[row] = chosen;
-        if (want_lp) a.chosen_lp[row] = (float)((double)load_elem(rowp, a.dtype, (uint32_t)chosen) - log_z);
+        const uint64_t ck = sm.u.f.sorted[pos];
+        a.ids[row] = (int32_t)rank_idx(ck);
+        if (want_lp) a.chosen_lp[row] = (float)((double)sm.u.f.sortedraw[pos] - log_z);
         if (a.diag) {
             lcs_row_diag dg{};
             dg.n_cand = V; dg.keep = keep; dg.maxl = maxl;
@@ -1193,10 +1274,16 @@ __device__ __noinline__ bool slice_finalize(const SampleArgs& a, uint32_t row, u
     return false;
 }
 
+// One workgroup per (row, slice of <= 8192 logits); 32 logits per thread in
+// registers. Penalised logits reach the slice through an LDS table of
+// override bits written once per distinct history id. Every slice publishes a
+// record; the row's last arrival finalizes it.
 template <int G>
-__global__ __launch_bounds__(kSliceThreads) void slice_kernel(SampleArgs a) {
+__global__ __launch_bounds__(kSliceThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void slice_kernel(SampleArgs a) {
     constexpr int NT = kSliceThreads;
     constexpr int NG = kSliceElems / G;   // 16-byte groups per thread
+    constexpr int HC = 8;                 // history ids per thread per chunk
     __shared__ SliceSmem sm;
     const uint32_t tid = threadIdx.x;
     const int lane = lane_id(), wv = (int)(tid / kWave);
@@ -1218,10 +1305,31 @@ __global__ __launch_bounds__(kSliceThreads) void slice_kernel(SampleArgs a) {
     const uint32_t* mrow = masked ? a.mask + (uint64_t)row * a.mask_words : nullptr;
     const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
     const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
-    uint32_t* myrec = a.recs + ((uint64_t)row * S + slice) * rec::kWords;
+    uint64_t* myrec = reinterpret_cast<uint64_t*>(a.recs) + ((uint64_t)row * S + slice) * rec::kWords64;
     const float NEG = -__builtin_huge_valf();
+    const bool stoch = mode == kModeWindow;
 
-    // ---- every load of the slice first (branch-free, clamped) ----
+    // ---- loads: history window ids first, then the slice's logits ----
+    const bool pen = penalties_active(P) && a.hist_off != nullptr;
+    uint32_t hn = 0, hstart = 0, hoff = 0;
+    if (pen) {
+        hoff = a.hist_off[row];
+        hn = a.hist_off[row + 1] - hoff;
+        hstart = hn > P.repeat_last_n ? hn - P.repeat_last_n : 0u;
+    }
+    const bool hany = pen && hn > hstart;
+    const bool htwo = hany && hn - hstart > (uint32_t)(NT * HC);
+    uint32_t hA[HC], hB[HC];
+    auto load_ids = [&](uint32_t (&h)[HC], uint32_t c0) {
+#pragma unroll
+        for (int k = 0; k < HC; ++k) {
+            const uint32_t i = hstart + c0 + (uint32_t)k * NT + tid;
+            h[k] = (uint32_t)a.hist_ids[hoff + (i < hn ? i : hn - 1)];
+            h[k] = i < hn ? h[k] : 0xffffffffu;
+        }
+    };
+    if (hany) load_ids(hA, 0);
+    if (htwo) load_ids(hB, NT * HC);
     uint4 raw[NG];
 #pragma unroll
     for (int j = 0; j < NG; ++j) {
@@ -1235,254 +1343,342 @@ __global__ __launch_bounds__(kSliceThreads) void slice_kernel(SampleArgs a) {
         const uint32_t ee = e0 < hi ? e0 : lo;
         mw[j] = mrow ? (mrow[ee >> 5] >> (ee & 31u)) : 0xffffffffu;
     }
-    const bool pen = penalties_active(P) && a.hist_off != nullptr;
-    constexpr int HPT = (int)(kFastHistMax / kSliceThreads);  // 16 window ids per thread
-    uint32_t hid[HPT];
-    uint32_t hoff = 0, hn = 0, hstart = 0;
-    if (pen) {
-        hoff = a.hist_off[row];
-        hn = a.hist_off[row + 1] - hoff;
-        hstart = hn > P.repeat_last_n ? hn - P.repeat_last_n : 0u;
-#pragma unroll
-        for (int k = 0; k < HPT; ++k) {
-            const uint32_t i = hstart + (uint32_t)k * NT + tid;
-            hid[k] = (uint32_t)a.hist_ids[hoff + (i < hn ? i : (hn > 0 ? hn - 1 : 0u))];
-        }
-        for (uint32_t i = tid; i < (len + 1) / 2; i += NT) sm.u.cnt[i] = 0;
-    }
-    if (tid == 0) sm.l.nwin = 0;
-    PROF_MARK(1);
-    if (pen) {
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < HPT; ++k) {
-            const uint32_t i = hstart + (uint32_t)k * NT + tid;
-            const uint32_t d = hid[k] - lo;
-            if (i < hn && hid[k] < V && d < len) atomicAdd(&sm.u.cnt[d >> 1], 1u << ((d & 1u) * 16u));
-        }
-        __syncthreads();
-    }
-    PROF_MARK(2);
+    if (tid == 0) { sm.l.ncand = 0; sm.l.nwin = 0; }
 
+    // ---- penalties: one override per distinct history id in this slice ----
+    if (hany) {
+#pragma unroll
+        for (int i = 0; i < (int)(kSliceMax / 4 / NT); ++i) sm.u.ovr4[i * NT + tid] = make_uint4(0, 0, 0, 0);
+        __syncthreads();
+        auto count = [&](const uint32_t (&h)[HC]) {
+#pragma unroll
+            for (int k = 0; k < HC; ++k) {
+                const uint32_t d = h[k] - lo;
+                if (h[k] < V && d < len) atomicAdd(&sm.u.ovr[d], 1u);
+            }
+        };
+        count(hA);
+        if (htwo) count(hB);
+        __syncthreads();
+        // the first exchange of each id takes its count; it alone writes the override
+        uint32_t cA[HC], cB[HC];
+        float rA[HC], rB[HC];
+        auto claim = [&](const uint32_t (&h)[HC], uint32_t (&c)[HC], float (&r)[HC]) {
+#pragma unroll
+            for (int k = 0; k < HC; ++k) {
+                const uint32_t d = h[k] - lo;
+                c[k] = (h[k] < V && d < len) ? atomicExch(&sm.u.ovr[d], 0u) : 0u;
+            }
+#pragma unroll
+            for (int k = 0; k < HC; ++k) r[k] = load_elem(rowp, a.dtype, c[k] ? h[k] : lo);
+        };
+        claim(hA, cA, rA);
+        if (htwo) claim(hB, cB, rB);
+        __syncthreads();
+        auto put = [&](const uint32_t (&h)[HC], const uint32_t (&c)[HC], const float (&r)[HC]) {
+#pragma unroll
+            for (int k = 0; k < HC; ++k) {
+                if (c[k]) {
+                    const uint32_t b = __float_as_uint(penalize(r[k], c[k], P));
+                    sm.u.ovr[h[k] - lo] = b ? b : 0x80000000u;   // +0 travels as -0
+                }
+            }
+        };
+        put(hA, cA, rA);
+        if (htwo) put(hB, cB, rB);
+    }
+    __syncthreads();
+    PROF_MARK(1);
+
+    // ---- values; positions past the slice read as -inf ----
     float v[kSliceElems];
-    bool vld[NG];
 #pragma unroll
     for (int j = 0; j < NG; ++j) {
-        vld[j] = lo + (j * NT + tid) * G < hi;
         float t[G];
         decode<G>(raw[j], t);
+        const uint32_t e0 = lo + (j * NT + tid) * G;
+        const bool full = lo + (j * NT + (uint32_t)wv * kWave + kWave) * G <= hi;  // wave-uniform
 #pragma unroll
-        for (int k = 0; k < G; ++k) v[j * G + k] = t[k];
+        for (int k = 0; k < G; ++k) v[j * G + k] = (full || e0 + k < hi) ? t[k] : NEG;
     }
-    auto elem_ok = [&](int j, int k) { return vld[j] && (lo + (j * NT + tid) * G + k) < hi; };
-    auto elem_id = [&](int j, int k) { return lo + (j * NT + tid) * G + (uint32_t)k; };
+    auto eid = [&](int q) { return lo + ((q / G) * NT + tid) * G + (uint32_t)(q % G); };
 
-    // ---- raw statistics per wave (logprob normaliser, top-n) ----
-    float m_raw = NEG;
+    // ---- raw statistics: max, top-n candidates, sum of exp ----
+    float lm = NEG;
 #pragma unroll
-    for (int j = 0; j < NG; ++j)
+    for (int q = 0; q < kSliceElems; ++q) lm = fmaxf(lm, v[q]);
+    const float Mw = wave_max(lm);
+    if (ntop) {
+        // the ntop-th largest lane max bounds the wave's top-n from below
+        float cur = lm, t = NEG;
+        for (uint32_t r = 0; r < ntop; ++r) {
+            t = wave_max(cur);
+            const uint64_t hit = ballot(cur == t);
+            if (lane == __builtin_ctzll(hit)) cur = NEG;
+        }
+        if (lm >= t) {
 #pragma unroll
-        for (int k = 0; k < G; ++k)
-            if (elem_ok(j, k)) m_raw = fmaxf(m_raw, v[j * G + k]);
-    m_raw = wave_max(m_raw);
-    double se = 0.0;
-    if (want_lp) {
+            for (int q = 0; q < kSliceElems; ++q) {
+                const uint32_t e = eid(q);
+                if (v[q] >= t && e < hi) {
+                    const uint32_t s = atomicAdd(&sm.l.ncand, 1u);
+                    if (s < kCandCap) sm.l.cand[s] = rank_key(v[q], e);
+                }
+            }
+        }
+    }
+    double sw = 0.0;
+    if (want_lp && Mw != NEG) {
+        const float b = -Mw * kLog2E;
+        float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < NG; ++j) {
-            float gs = 0.0f;
+            float c[G];
 #pragma unroll
-            for (int k = 0; k < G; ++k)
-                if (elem_ok(j, k)) gs += expf(fsub(v[j * G + k], m_raw));
-            se += (double)gs;
+            for (int k = 0; k < G; ++k) c[k] = fast_exp2(fmaf(v[j * G + k], kLog2E, b));
+#pragma unroll
+            for (int w = G / 2; w >= 1; w /= 2)
+#pragma unroll
+                for (int k = 0; k < w; ++k) c[k] += c[k + w];
+            s += c[0];
         }
-        se = wave_sum(se);
+        sw = wave_sum((double)s);
     }
-    if (lane == 0) { sm.l.mraw[wv] = m_raw; sm.l.se[wv] = se; }
-    PROF_MARK(3);
-    if (ntop) {
-        // each lane keeps its best remaining (value, id); the wave's winner
-        // marks it taken and rescans its own elements
-        uint32_t taken = 0;
-        float lv = NEG;
-        uint32_t li = 0xfffffffeu;
-        auto rescan = [&]() {
-            lv = NEG;
-            li = 0xfffffffeu;
-#pragma unroll
-            for (int j = 0; j < NG; ++j)
-#pragma unroll
-                for (int k = 0; k < G; ++k) {
-                    const int q = j * G + k;
-                    if (elem_ok(j, k) && !((taken >> q) & 1u)) {
-                        const uint32_t e = elem_id(j, k);
-                        if (li == 0xfffffffeu || vi_better(v[q], e, lv, li)) { lv = v[q]; li = e; }
-                    }
-                }
-        };
-        rescan();
-        for (uint32_t r = 0; r < kTopMax; ++r) {
-            if (r >= ntop) {
-                if (lane == 0) sm.l.wtop[wv][r] = ~0ull;
-                continue;
-            }
-            float bv = lv;
-            uint32_t bi = li;
-            wave_argmax(bv, bi);
-            if (lane == 0) sm.l.wtop[wv][r] = bi < V ? rank_key(bv, bi) : ~0ull;
-            if (bi < V && li == bi) {
-                const uint32_t off = li - lo;
-                const uint32_t jj = off / (NT * G);
-                taken |= 1u << (jj * G + (off - jj * NT * G - tid * G));
-                rescan();
-            }
-        }
-    }
-    PROF_MARK(4);
+    if (lane == 0) { sm.l.mraw[wv] = Mw; sm.l.sraw[wv] = sw; }
+    PROF_MARK(2);
 
-    // ---- penalties in registers, penalised maxima per wave ----
-    if (pen) {
+    // ---- penalised values ----
+    if (hany) {
 #pragma unroll
-        for (int j = 0; j < NG; ++j)
+        for (int j = 0; j < NG; ++j) {
+#pragma unroll
+            for (int h4 = 0; h4 < G / 4; ++h4) {
+                const uint4 o = sm.u.ovr4[((j * NT + tid) * G) / 4 + h4];
+                const uint32_t ob[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int qq = j * G + h4 * 4 + k;
+                    v[qq] = ob[k] ? __uint_as_float(ob[k]) : v[qq];
+                }
+            }
+        }
+    }
+    float lpm = NEG;   // lane max of the penalised values (sampled rows)
+    if (mode == kModeGreedy) {
+        // first index of the max, over all ids and over the allowed ids;
+        // the raw logit of each winner rides along for its logprob
+        float bv = NEG, mv = NEG, br = 0.0f, mr = 0.0f;
+        uint32_t bi = kNoIdx, mi = kNoIdx, na = 0;
+#pragma unroll
+        for (int q = 0; q < kSliceElems; ++q) {
+            const uint32_t e = eid(q);
+            const bool ok = e < hi;
+            const float x = v[q];
+            if (ok && (x > bv || bi == kNoIdx)) { bv = x; bi = e; }
+            if (mrow) {
+                const bool al = ok && ((mw[q / G] >> (q % G)) & 1u);
+                na += al ? 1u : 0u;
+                if (al && (x > mv || mi == kNoIdx)) { mv = x; mi = e; }
+            }
+        }
+        // raw logits of the lane winners (re-read: the registers hold penalised values)
+        if (want_lp && hany) {
+            br = bi < V ? load_elem(rowp, a.dtype, bi) : 0.0f;
+            mr = mi < V ? load_elem(rowp, a.dtype, mi) : 0.0f;
+        } else {
+            br = bv;
+            mr = mv;
+        }
+        const float bv0 = bv, mv0 = mv;
+        const uint32_t bi0 = bi, mi0 = mi;
+        wave_argmax(bv, bi);
+        const uint64_t ob = ballot(bi0 == bi && bi < V);
+        br = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(br), ob ? __builtin_ctzll(ob) : 0));
+        (void)bv0;
+        if (mrow) {
+            wave_argmax(mv, mi);
+            const uint64_t om = ballot(mi0 == mi && mi < V);
+            mr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mr), om ? __builtin_ctzll(om) : 0));
+            na = wave_sum_u(na);
+        }
+        (void)mv0;
+        if (lane == 0) {
+            sm.l.mpen[wv] = bv; sm.l.ipen[wv] = bi; sm.l.rpen[wv] = br;
+            sm.l.mmsk[wv] = mv; sm.l.imsk[wv] = mi; sm.l.rmsk[wv] = mr; sm.l.nall[wv] = na;
+            sm.l.bulk[wv] = 0.0; sm.l.bterm[wv] = 0.0;
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < kSliceElems; ++q) lpm = fmaxf(lpm, v[q]);
+        const float pm = wave_max(lpm);
+        if (lane == 0) { sm.l.mpen[wv] = pm; sm.l.ipen[wv] = kNoIdx; sm.l.nall[wv] = 0; }
+    }
+    PROF_MARK(3);
+
+    // ---- min-p window entries and the normaliser's bulk, against the slice max ----
+    if (stoch) {
+        __syncthreads();
+        float ms = sm.l.mpen[0];
+#pragma unroll
+        for (int w = 1; w < kSliceWaves; ++w) ms = fmaxf(ms, sm.l.mpen[w]);
+        const float inv_t = fdiv(1.0f, P.temperature);
+        const float kk = fmul(inv_t, kLog2E);
+        // bulk term c = 2^t, t = (p - ms) * inv_t * log2(e) <= 0; sum of c|t| bounds
+        // the effect of the rounding of t here and in the reference's tempered offsets
+        float bs = 0.0f, bt = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            float c[G];
 #pragma unroll
             for (int k = 0; k < G; ++k) {
-                if (!elem_ok(j, k)) continue;
-                const uint32_t d = elem_id(j, k) - lo;
-                const uint32_t c = (sm.u.cnt[d >> 1] >> ((d & 1u) * 16u)) & 0xffffu;
-                if (c) v[j * G + k] = penalize(v[j * G + k], c, P);
+                const float t = fmaxf(fmul(fsub(v[j * G + k], ms), kk), -250.0f);
+                c[k] = fast_exp2(t);
+                bt = fmaf(c[k], -t, bt);
             }
-    }
-    float m_all = NEG, m_msk = NEG;
-    uint32_t i_all = 0xfffffffeu, i_msk = 0xfffffffeu, n_allowed = 0;
 #pragma unroll
-    for (int j = 0; j < NG; ++j)
+            for (int w = G / 2; w >= 1; w /= 2)
 #pragma unroll
-        for (int k = 0; k < G; ++k) {
-            if (!elem_ok(j, k)) continue;
-            const float x = v[j * G + k];
-            const uint32_t e = elem_id(j, k);
-            if (i_all == 0xfffffffeu || vi_better(x, e, m_all, i_all)) { m_all = x; i_all = e; }
-            if (mrow && ((mw[j] >> k) & 1u)) {
-                ++n_allowed;
-                if (i_msk == 0xfffffffeu || vi_better(x, e, m_msk, i_msk)) { m_msk = x; i_msk = e; }
-            }
+                for (int k = 0; k < w; ++k) c[k] += c[k + w];
+            bs += c[0];
         }
-    wave_argmax(m_all, i_all);
-    if (mrow) {
-        wave_argmax(m_msk, i_msk);
-        n_allowed = wave_sum_u(n_allowed);
-    }
-    if (lane == 0) {
-        sm.l.mall[wv] = m_all; sm.l.iall[wv] = i_all;
-        sm.l.mmsk[wv] = m_msk; sm.l.imsk[wv] = i_msk; sm.l.nall[wv] = n_allowed;
-        sm.l.bulk[wv] = 0.0; sm.l.berr[wv] = 0.0;
-    }
-    PROF_MARK(5);
-
-    // ---- min-p window (exact entries) and tail of the normaliser ----
-    if (mode == kModeWindow) {
-        __syncthreads();
-        float ms = sm.l.mall[0];
-#pragma unroll
-        for (int w = 1; w < kSliceWaves; ++w) ms = fmaxf(ms, sm.l.mall[w]);
-        const float inv_t = fdiv(1.0f, P.temperature);
         const double delta = (double)P.temperature * (-log((double)P.min_p) + 1e-3);
         const double thr = (double)ms - delta;
-        double bulk = 0.0, berr = 0.0;
+        if ((double)lpm >= thr) {
 #pragma unroll
-        for (int j = 0; j < NG; ++j)
-#pragma unroll
-            for (int k = 0; k < G; ++k) {
-                if (!elem_ok(j, k)) continue;
-                const float x = v[j * G + k];
-                if ((double)x >= thr) {
+            for (int q = 0; q < kSliceElems; ++q) {
+                if ((double)v[q] >= thr) {
                     const uint32_t s = atomicAdd(&sm.l.nwin, 1u);
-                    if (s < kWinCap) sm.l.win[s] = rank_key(x, elem_id(j, k));
-                } else {
-                    const float xl = tempered(x, ms, inv_t);
-                    const float c = expf(xl);
-                    bulk += (double)c;
-                    berr += (double)c * ((double)fabsf(xl) * 0x1p-22 + 0x1p-21);
+                    if (s < kWinLds) {
+                        const uint32_t e = eid(q);
+                        sm.l.win[s] = rank_key(v[q], e);
+                        // raw logit: the value itself unless penalised (then fetched at publish)
+                        const uint32_t ob = hany ? sm.u.ovr[e - lo] : 0u;
+                        sm.l.winraw[s] = ob ? __uint_as_float(0x7fffffffu) : v[q];
+                    }
                 }
             }
-        bulk = wave_sum(bulk);
-        berr = wave_sum(berr);
-        if (lane == 0) { sm.l.bulk[wv] = bulk; sm.l.berr[wv] = berr; }
+        }
+        const double bsum = wave_sum((double)bs);
+        const double btsum = wave_sum((double)bt);
+        if (lane == 0) { sm.l.bulk[wv] = bsum; sm.l.bterm[wv] = btsum; }
     }
-    PROF_MARK(6);
+    PROF_MARK(4);
     __syncthreads();
 
     // ---- wave 0 combines the waves and publishes the slice record ----
     if (wv == 0) {
         const bool lw = lane < kSliceWaves;
         const int wl = lw ? lane : 0;
-        float mr = lw ? sm.l.mraw[wl] : NEG;
-        const float mrs = wave_max(mr);
-        const double ses = wave_sum(lw && want_lp ? sm.l.se[wl] * exp((double)mr - (double)mrs) : 0.0);
-        float ma = lw ? sm.l.mall[wl] : NEG;
-        uint32_t ia = lw ? sm.l.iall[wl] : 0xfffffffeu;
-        wave_argmax(ma, ia);
+        const float mrw = lw ? sm.l.mraw[wl] : NEG;
+        const float mrs = wave_max(mrw);
+        const double ses = wave_sum(lw && want_lp && mrw != NEG
+                                        ? sm.l.sraw[wl] * (double)fast_exp2((mrw - mrs) * kLog2E) : 0.0);
+        float ma = lw ? sm.l.mpen[wl] : NEG;
+        uint32_t ia = lw ? sm.l.ipen[wl] : kNoIdx;
+        float ra = lw ? sm.l.rpen[wl] : 0.0f;
         float mm = lw ? sm.l.mmsk[wl] : NEG;
-        uint32_t im = lw ? sm.l.imsk[wl] : 0xfffffffeu;
-        wave_argmax(mm, im);
-        const uint32_t na = wave_sum_u(lw ? sm.l.nall[wl] : 0u);
-        const double bk = wave_sum(lw ? sm.l.bulk[wl] : 0.0);
-        const double be = wave_sum(lw ? sm.l.berr[wl] : 0.0);
-        const uint32_t nwin = sm.l.nwin;
-        // slice top-n: merge the wave lists (lane w < 4 holds list w)
-        const uint32_t nts = min(ntop, len);
-        uint32_t p = 0;
-        for (uint32_t r = 0; r < nts; ++r) {
-            const uint64_t head = (lw && p < kTopMax) ? sm.l.wtop[wl][p] : ~0ull;
-            const uint64_t best = wave_min_u64(head);
-            if (lw && head == best) ++p;
-            if (lane == 0) st_dev_u64(reinterpret_cast<uint64_t*>(myrec + rec::kTop + 2 * r), best);
+        uint32_t im = lw ? sm.l.imsk[wl] : kNoIdx;
+        float rm = lw ? sm.l.rmsk[wl] : 0.0f;
+        uint32_t na = 0;
+        double bk = 0.0, be = 0.0;
+        if (stoch) {
+            ma = wave_max(ma);
+            ia = kNoIdx;
+            bk = wave_sum(lw ? sm.l.bulk[wl] : 0.0);
+            be = wave_sum(lw ? sm.l.bterm[wl] : 0.0) * 0x1p-22 + bk * 0x1p-20 + (double)len * 0x1p-120;
+        } else {
+            const uint32_t ia0 = ia, im0 = im;
+            wave_argmax(ma, ia);
+            const uint64_t oa = ballot(lw && ia0 == ia && ia < V);
+            ra = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ra), oa ? __builtin_ctzll(oa) : 0));
+            if (mrow) {
+                wave_argmax(mm, im);
+                const uint64_t om = ballot(lw && im0 == im && im < V);
+                rm = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), om ? __builtin_ctzll(om) : 0));
+                na = wave_sum_u(lw ? sm.l.nall[wl] : 0u);
+            }
         }
-        uint32_t hw = 0;
+        // slice top-n: ntop rounds over the candidates (<= 4 per lane)
+        const uint32_t nc = sm.l.ncand;
+        const uint32_t ncc = min(nc, kCandCap);
+        const uint32_t nts = min(ntop, len);
+        if (nts) {
+            uint64_t ck[kCandCap / kWave];
+#pragma unroll
+            for (int i = 0; i < (int)(kCandCap / kWave); ++i) {
+                const uint32_t s = (uint32_t)lane + (uint32_t)i * kWave;
+                ck[i] = s < ncc ? sm.l.cand[s] : ~0ull;
+            }
+            uint64_t myk = ~0ull;
+            for (uint32_t r = 0; r < nts; ++r) {
+                uint64_t m = ck[0];
+#pragma unroll
+                for (int i = 1; i < (int)(kCandCap / kWave); ++i) m = ck[i] < m ? ck[i] : m;
+                const uint64_t best = wave_min_u64(m);
+#pragma unroll
+                for (int i = 0; i < (int)(kCandCap / kWave); ++i) ck[i] = ck[i] == best ? ~0ull : ck[i];
+                if ((uint32_t)lane == r) myk = best;
+            }
+            if ((uint32_t)lane < nts) st_dev_u64(myrec + rec::kTop + lane, myk);
+        }
+        // window entries: the top kWinCap by rank, in ascending rank order
+        const uint32_t nwr = stoch ? sm.l.nwin : 0u;
+        const uint32_t nwl = min(nwr, kWinLds);
+        const uint32_t nw = min(nwl, kWinCap);
+        if (nwl) {
+            uint64_t k[4];
+            uint32_t rk[4];
+            wave_rank4(sm.l.win, nwl, k, rk);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
+                if (e < nwl && rk[c] < kWinCap) {
+                    float kr = sm.l.winraw[e];
+                    if (__float_as_uint(kr) == 0x7fffffffu) kr = load_elem(rowp, a.dtype, rank_idx(k[c]));
+                    st_dev_u64(myrec + rec::kWin + rk[c], k[c]);
+                    st_dev_u64(myrec + rec::kWinRaw + rk[c], (uint64_t)__float_as_uint(kr));
+                }
+            }
+        }
+        const uint32_t fl = (nwr > kWinCap ? rec::kFlagWinTrunc : 0u) |
+                            (nwr > kWinLds ? rec::kFlagWinLost : 0u) |
+                            (nts && nc > kCandCap ? rec::kFlagCandOverflow : 0u);
+        uint64_t hw = 0;
         switch (lane) {
-            case rec::kMRaw: hw = __float_as_uint(mrs); break;
-            case rec::kSRaw: hw = (uint32_t)(uint64_t)__double_as_longlong(ses); break;
-            case rec::kSRaw + 1: hw = (uint32_t)((uint64_t)__double_as_longlong(ses) >> 32); break;
-            case rec::kMAll: hw = __float_as_uint(ma); break;
-            case rec::kIAll: hw = ia; break;
-            case rec::kMMsk: hw = __float_as_uint(mm); break;
-            case rec::kIMsk: hw = im; break;
-            case rec::kNAllowed: hw = na; break;
-            case rec::kNWin: hw = min(nwin, kWinCap); break;
-            case rec::kOverflow: hw = nwin > kWinCap ? 1u : 0u; break;
-            case rec::kNTop: hw = nts; break;
-            case rec::kBulk: hw = (uint32_t)(uint64_t)__double_as_longlong(bk); break;
-            case rec::kBulk + 1: hw = (uint32_t)((uint64_t)__double_as_longlong(bk) >> 32); break;
-            case rec::kBulkErr: hw = (uint32_t)(uint64_t)__double_as_longlong(be); break;
-            case rec::kBulkErr + 1: hw = (uint32_t)((uint64_t)__double_as_longlong(be) >> 32); break;
+            case 0: hw = (uint64_t)__float_as_uint(mrs) | ((uint64_t)nw << 32) | ((uint64_t)fl << 48); break;
+            case 1: hw = d_bits(ses); break;
+            case 2: hw = pack2(__float_as_uint(ma), ia); break;
+            case 3: hw = pack2(__float_as_uint(mm), im); break;
+            case 4: hw = pack2(na, nts); break;
+            case 5: hw = d_bits(bk); break;
+            case 6: hw = d_bits(be); break;
+            case 7: hw = pack2(__float_as_uint(ra), __float_as_uint(rm)); break;
             default: break;
         }
-        if (lane < (int)rec::kHeader) st_dev(myrec + lane, hw);
-        for (uint32_t j = lane; j < min(nwin, kWinCap); j += kWave) {
-            st_dev_u64(reinterpret_cast<uint64_t*>(myrec + rec::kWin + 2 * j), sm.l.win[j]);
-        }
+        if (lane < (int)rec::kHdr) st_dev_u64(myrec + lane, hw);
         wait_all_memory();
         if (lane == 0) {
             const uint32_t prev = __hip_atomic_fetch_add(a.counters + row, 1u, __ATOMIC_RELAXED,
                                                          __HIP_MEMORY_SCOPE_AGENT);
             const bool last = prev == S - 1;
             if (last) st_dev(a.counters + row, 0u);
-            sm.last = last ? 1u : 0u;
-            sm.fallback = 0u;
+            sm.l.last = last ? 1u : 0u;
+            sm.l.fallback = 0u;
         }
     }
-    PROF_MARK(7);
+    PROF_MARK(5);
     __syncthreads();
-    if (!sm.last) return;
-    PROF_MARK(8);
+    if (!sm.l.last) return;
     // =============== last-arriving workgroup finishes the row ===============
     if (wv == 0) {
-        const bool fb = slice_finalize<G>(a, row, mode, sm);
-        if (lane == 0) sm.fallback = fb ? 1u : 0u;
+        const bool fb = slice_finalize(a, row, mode, sm);
+        if (lane == 0) sm.l.fallback = fb ? 1u : 0u;
     }
     __syncthreads();
-    PROF_MARK(9);
-    if (sm.fallback) {
-        exact_row<kSliceThreads, kFbBins, kFbCap, kFbHistCap, G>(a, row, sm.u.ex);
+    PROF_MARK(6);
+    if (sm.l.fallback) {
+        stage_args(&sm.u.ex.args);
+        exact_row<kSliceThreads, kFbBins, kFbCap, kFbHistCap, G>(sm.u.ex.args, row, sm.u.ex);
     }
 }
 
