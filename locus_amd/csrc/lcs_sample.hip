@@ -934,15 +934,23 @@ __global__ __launch_bounds__(kGenThreads) void general_kernel(SampleArgs a) {
 // ============================================================ sliced path ==
 #ifdef LCS_PROFILE
 // Phase timestamps per workgroup (wall clock, 100 MHz) for performance work.
-__device__ uint64_t g_prof[16384 * 16];
+__device__ uint64_t g_prof[16384 * 32];
 #define PROF_MARK(k)                                                              \
     do {                                                                          \
         __syncthreads();                                                          \
-        if (threadIdx.x == 0 && blockIdx.x < 16384) g_prof[blockIdx.x * 16 + (k)] = wall_clock64(); \
+        if (threadIdx.x == 0 && blockIdx.x < 16384) g_prof[blockIdx.x * 32 + (k)] = wall_clock64(); \
+    } while (0)
+// wave-level mark (no barrier), for the single-wave publish and finalize
+#define PROF_WMARK(k)                                                             \
+    do {                                                                          \
+        if ((threadIdx.x & 63) == 0 && blockIdx.x < 16384) g_prof[blockIdx.x * 32 + (k)] = wall_clock64(); \
     } while (0)
 #else
 #define PROF_MARK(k) \
     do {             \
+    } while (0)
+#define PROF_WMARK(k) \
+    do {              \
     } while (0)
 #endif
 
@@ -966,12 +974,15 @@ struct SliceLocal {
     double sraw[kSliceWaves];
     double bulk[kSliceWaves];
     double bterm[kSliceWaves];
-    uint32_t ncand, nwin, last, fallback;
-    uint64_t cand[kCandCap];
-    uint64_t win[kWinLds];
-    float winraw[kWinLds];
+    uint32_t ncand, nwin, last;
+    // finalize hand-off between its waves
+    double log_z, fin_S, fin_rel;
+    float chosen_raw, fin_maxl;
+    uint32_t fin_fb, fin_L0;
+    uint64_t ck[kCandCap];               // top-n candidates (rank keys)
+    uint64_t wk[kWinLds];                // window entries (rank keys)
 };
-// the row's finalize (wave 0 of the last-arriving workgroup)
+// the row's finalize (two waves of the last-arriving workgroup)
 struct SliceFin {
     uint64_t top[kWave * kTopMax];
     uint64_t ent[kRowWin];
@@ -991,14 +1002,20 @@ struct SliceSmem {
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+// The next float below a finite x.
+__device__ __forceinline__ float next_down(float x) {
+    const uint32_t b = __float_as_uint(x);
+    if (x == 0.0f) return -__uint_as_float(1u);
+    return __uint_as_float(x > 0.0f ? b - 1u : b + 1u);
+}
 __device__ __forceinline__ double bits_d(uint64_t b) { return __longlong_as_double((long long)b); }
 __device__ __forceinline__ uint64_t d_bits(double d) { return (uint64_t)__double_as_longlong(d); }
 __device__ __forceinline__ uint64_t pack2(uint32_t lo, uint32_t hi) { return ((uint64_t)hi << 32) | lo; }
 
-// Ranks n <= 4*64 unique keys held in LDS by one wave: lane l owns entries
-// l, l+64, l+128, l+192 (k[c], ~0 past n) and gets their ascending ranks.
-__device__ __forceinline__ void wave_rank4(const uint64_t* keys, uint32_t n, uint64_t (&k)[4],
-                                           uint32_t (&rk)[4]) {
+// Ascending ranks of n <= 4*64 unique keys in LDS, by one wave: lane l takes
+// entries l, l+64, l+128, l+192 (k[c], ~0 past n) and counts the smaller keys
+// with broadcast reads, 8 per batch.
+__device__ __forceinline__ void lds_rank4(const uint64_t* keys, uint32_t n, uint64_t (&k)[4], uint32_t (&rk)[4]) {
     const uint32_t lane = (uint32_t)lane_id();
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -1007,51 +1024,139 @@ __device__ __forceinline__ void wave_rank4(const uint64_t* keys, uint32_t n, uin
         rk[c] = 0;
     }
     if (n <= (uint32_t)kWave) {
-        for (uint32_t f = 0; f < n; ++f) rk[0] += readlane_u64(k[0], (int)f) < k[0] ? 1u : 0u;
+        uint32_t f = 0;
+        for (; f + 8 <= n; f += 8) {
+            uint64_t o[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) o[u] = keys[f + u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) rk[0] += o[u] < k[0] ? 1u : 0u;
+        }
+        for (; f < n; ++f) rk[0] += keys[f] < k[0] ? 1u : 0u;
         return;
     }
-    const uint32_t nch = (n + kWave - 1) / kWave;
-    for (uint32_t c2 = 0; c2 < nch; ++c2) {
-        const uint64_t src = c2 == 0 ? k[0] : c2 == 1 ? k[1] : c2 == 2 ? k[2] : k[3];
-        const uint32_t cnt = min((uint32_t)kWave, n - c2 * kWave);
-        for (uint32_t f = 0; f < cnt; ++f) {
-            const uint64_t o = readlane_u64(src, (int)f);
+    uint32_t f = 0;
+    for (; f + 8 <= n; f += 8) {
+        uint64_t o[8];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) rk[c] += o < k[c] ? 1u : 0u;
-        }
+        for (int u = 0; u < 8; ++u) o[u] = keys[f + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) rk[c] += o[u] < k[c] ? 1u : 0u;
+    }
+    for (; f < n; ++f) {
+        const uint64_t o = keys[f];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rk[c] += o < k[c] ? 1u : 0u;
     }
 }
 
-// Finalize of a row by wave 0 of its last-arriving workgroup. One round trip
-// brings every slice's header, top-n list and leading window entries; the
-// row window (entries within delta of the row max) is ranked in registers and
-// the reference's top-p / min-p / draw walk runs as wave scans. Returns true
-// when the row needs the exact single-workgroup path: a window or candidate
-// list overflowed, the row window holds more than kRowWin entries, or a
-// top-p / min-p decision lies within the normaliser's error bound.
-__device__ __forceinline__ bool slice_finalize(const SampleArgs& a, uint32_t row, uint32_t mode,
-                                               SliceSmem& sm) {
+// ---- the row's finalize, spread over the waves of the last-arriving workgroup ----
+// wave 0: headers, the row window gathered and ranked (greedy rows finish here)
+// wave 1: raw log-normaliser and the top-n merge (logprob rows)
+// wave 2: the sampling normaliser S and its error bound
+// then, after one barrier, wave 0 walks top-p / min-p / the draw.
+
+// Raw log-normaliser over the slices and the k-way merge of their top-n lists
+// (logprobs_from, sampling.cpp:150-190). Returns true when a slice's candidate
+// list overflowed.
+__device__ __forceinline__ bool fin_logprobs(const SampleArgs& a, uint32_t row, SliceSmem& sm) {
     const int lane = lane_id();
-    const uint32_t S = a.slices, V = a.vocab;
-    const lcs_params P = a.params[row];
-    const uint32_t esz = a.dtype == LCS_BF16 ? 2u : 4u;
-    const void* rowp = static_cast<const char*>(a.logits) + (uint64_t)row * a.row_stride * esz;
-    const bool masked = a.mask != nullptr && (a.has_mask == nullptr || a.has_mask[row] != 0);
-    const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
-    const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
+    const uint32_t S = a.slices;
+    const uint32_t ntop = min(a.n_top, kTopMax);
     const uint64_t* recs = reinterpret_cast<const uint64_t*>(a.recs) + (uint64_t)row * S * rec::kWords64;
     const bool mine = (uint32_t)lane < S;
     const uint64_t* my = recs + (uint64_t)(mine ? lane : 0) * rec::kWords64;
     const float NEG = -__builtin_huge_valf();
-
-    // ---- one round trip: headers, top-n lists, leading window entries ----
-    uint64_t h[rec::kHdr];
-#pragma unroll
-    for (int k = 0; k < (int)rec::kHdr; ++k) h[k] = ld_dev_u64(my + k);
+    const uint64_t h0 = ld_dev_u64(my + 0), h1 = ld_dev_u64(my + 1), h4 = ld_dev_u64(my + 4);
     uint64_t tk[kTopMax];
 #pragma unroll
     for (int j = 0; j < (int)kTopMax; ++j) tk[j] = (uint32_t)j < ntop ? ld_dev_u64(my + rec::kTop + j) : ~0ull;
+    const float m_raw = mine ? __uint_as_float((uint32_t)h0) : NEG;
+    const uint32_t flags = mine ? (uint32_t)(h0 >> 48) : 0u;
+    const double s_raw = mine ? bits_d(h1) : 0.0;
+    const uint32_t nts = mine ? (uint32_t)(h4 >> 32) : 0u;
+    const float M = wave_max(m_raw);
+    const double z = wave_sum(mine && m_raw != NEG ? s_raw * exp((double)m_raw - (double)M) : 0.0);
+    const double log_z = log(z) + (double)M;
+    if (lane == 0) sm.l.log_z = log_z;
+    if (ntop == 0) return false;
+    if (ballot(mine && (flags & rec::kFlagCandOverflow))) return true;
+#pragma unroll
+    for (int j = 0; j < (int)kTopMax; ++j) {
+        if ((uint32_t)j < ntop) sm.u.f.top[lane * kTopMax + j] = (mine && (uint32_t)j < nts) ? tk[j] : ~0ull;
+    }
+    wave_sync();
+    uint32_t p = 0;
+    uint64_t myk = ~0ull;
+    for (uint32_t r = 0; r < ntop; ++r) {
+        const uint64_t head = p < ntop ? sm.u.f.top[lane * kTopMax + p] : ~0ull;
+        const uint64_t best = wave_min_u64(head);
+        if (head == best && best != ~0ull) ++p;
+        if ((uint32_t)lane == r) myk = best;
+    }
+    if ((uint32_t)lane < ntop) {
+        a.top_ids[(uint64_t)row * a.n_top + lane] = (int32_t)rank_idx(myk);
+        a.top_lp[(uint64_t)row * a.n_top + lane] = (float)((double)rank_val(myk) - log_z);
+    }
+    PROF_WMARK(21);
+    return false;
+}
+
+// The sampling normaliser: slice bulks rescaled to the row max, with the
+// bound that certifies top-p decisions (sampled rows).
+__device__ __forceinline__ void fin_norm(const SampleArgs& a, uint32_t row, SliceSmem& sm) {
+    const int lane = lane_id();
+    const uint32_t S = a.slices;
+    const lcs_params P = a.params[row];
+    const uint64_t* recs = reinterpret_cast<const uint64_t*>(a.recs) + (uint64_t)row * S * rec::kWords64;
+    const bool mine = (uint32_t)lane < S;
+    const uint64_t* my = recs + (uint64_t)(mine ? lane : 0) * rec::kWords64;
+    const float NEG = -__builtin_huge_valf();
+    const uint64_t h2 = ld_dev_u64(my + 2), h5 = ld_dev_u64(my + 5), h6 = ld_dev_u64(my + 6);
+    const float m_pen = mine ? __uint_as_float((uint32_t)h2) : NEG;
+    const double bulk = mine ? bits_d(h5) : 0.0;
+    const double berr = mine ? bits_d(h6) : 0.0;
+    const float inv_t = fdiv(1.0f, P.temperature);
+    const float maxl = wave_max(m_pen);
+    const double d_s = mine ? ((double)m_pen - (double)maxl) * (double)inv_t : 0.0;
+    const double es = mine && m_pen != NEG ? exp(d_s) : 0.0;
+    const double Sf = wave_sum(es * bulk);
+    const double eps = wave_sum(es * (berr + fabs(d_s) * 0x1p-50 * bulk));
+    if (lane == 0) {
+        sm.l.fin_S = Sf;
+        sm.l.fin_rel = 2.0 * eps / Sf + 0x1p-50;
+    }
+    PROF_WMARK(22);
+}
+
+__device__ __forceinline__ float next_up(float x) {
+    const uint32_t b = __float_as_uint(x);
+    if (x == 0.0f) return __uint_as_float(1u);
+    return __uint_as_float(x > 0.0f ? b + 1u : b - 1u);
+}
+
+// Headers and the row window. Greedy rows: the argmax over the slices
+// (sampling.cpp:52-67), written out here. Sampled rows: every entry with
+// p >= maxl - delta gathered from the slices' rank-ordered lists and ranked in
+// LDS (sorted / sortedraw, count in fin_L0). Returns true when the row needs
+// the exact single-workgroup path (a slice dropped window entries, or the
+// row window holds more than kRowWin entries).
+__device__ __forceinline__ bool fin_gather(const SampleArgs& a, uint32_t row, uint32_t mode, SliceSmem& sm) {
+    const int lane = lane_id();
+    const uint32_t S = a.slices, V = a.vocab;
+    const lcs_params P = a.params[row];
+    const bool masked = a.mask != nullptr && (a.has_mask == nullptr || a.has_mask[row] != 0);
+    const uint64_t* recs = reinterpret_cast<const uint64_t*>(a.recs) + (uint64_t)row * S * rec::kWords64;
+    const bool mine = (uint32_t)lane < S;
+    const uint64_t* my = recs + (uint64_t)(mine ? lane : 0) * rec::kWords64;
+    const float NEG = -__builtin_huge_valf();
     const bool stoch = mode == kModeWindow;
+
+    uint64_t h[rec::kHdr];
+#pragma unroll
+    for (int k = 0; k < (int)rec::kHdr; ++k) h[k] = ld_dev_u64(my + k);
     uint64_t wk[kSpecWin];
     uint32_t wr[kSpecWin];
     if (stoch) {
@@ -1061,63 +1166,29 @@ __device__ __forceinline__ bool slice_finalize(const SampleArgs& a, uint32_t row
             wr[j] = (uint32_t)ld_dev_u64(my + rec::kWinRaw + j);
         }
     }
-    const float m_raw = mine ? __uint_as_float((uint32_t)h[0]) : NEG;
+    PROF_WMARK(7);
     const uint32_t n_win = mine ? (uint32_t)(h[0] >> 32) & 0xffffu : 0u;
     const uint32_t flags = mine ? (uint32_t)(h[0] >> 48) : 0u;
-    const double s_raw = mine ? bits_d(h[1]) : 0.0;
     const float m_pen = mine ? __uint_as_float((uint32_t)h[2]) : NEG;
     const uint32_t i_pen = mine ? (uint32_t)(h[2] >> 32) : kNoIdx;
     const float m_msk = mine ? __uint_as_float((uint32_t)h[3]) : NEG;
     const uint32_t i_msk = mine ? (uint32_t)(h[3] >> 32) : kNoIdx;
     const uint32_t n_allowed = mine ? (uint32_t)h[4] : 0u;
-    const uint32_t nts = mine ? (uint32_t)(h[4] >> 32) : 0u;
-    const double bulk = mine ? bits_d(h[5]) : 0.0;
-    const double berr = mine ? bits_d(h[6]) : 0.0;
 
-    // ---- raw log-normaliser (logprobs_from over the whole row) ----
-    const float M = wave_max(m_raw);
-    double log_z = 0.0;
-    if (want_lp) {
-        const double z = wave_sum(mine && m_raw != NEG ? s_raw * exp((double)m_raw - (double)M) : 0.0);
-        log_z = log(z) + (double)M;
-    }
-    // ---- top-n: k-way merge of the slices' ascending rank-key lists ----
-    if (ntop) {
-        if (ballot(mine && (flags & rec::kFlagCandOverflow))) return true;
-#pragma unroll
-        for (int j = 0; j < (int)kTopMax; ++j) {
-            if ((uint32_t)j < ntop) sm.u.f.top[lane * kTopMax + j] = (mine && (uint32_t)j < nts) ? tk[j] : ~0ull;
-        }
-        wave_sync();
-        uint32_t p = 0;
-        uint64_t myk = ~0ull;
-        for (uint32_t r = 0; r < ntop; ++r) {
-            const uint64_t head = p < ntop ? sm.u.f.top[lane * kTopMax + p] : ~0ull;
-            const uint64_t best = wave_min_u64(head);
-            if (head == best && best != ~0ull) ++p;
-            if ((uint32_t)lane == r) myk = best;
-        }
-        if ((uint32_t)lane < ntop) {
-            a.top_ids[(uint64_t)row * a.n_top + lane] = (int32_t)rank_idx(myk);
-            a.top_lp[(uint64_t)row * a.n_top + lane] = (float)((double)rank_val(myk) - log_z);
-        }
-    }
-    const uint32_t tot_allowed = wave_sum_u(n_allowed);
-
-    if (mode == kModeGreedy) {
+    if (!stoch) {
+        const uint32_t tot_allowed = wave_sum_u(n_allowed);
         const bool use_mask = masked && tot_allowed > 0;
         float bv = use_mask ? m_msk : m_pen;
         uint32_t bi = use_mask ? i_msk : i_pen;
         float braw = use_mask ? __uint_as_float((uint32_t)(h[7] >> 32)) : __uint_as_float((uint32_t)h[7]);
         if (bi >= V) { bv = NEG; bi = kNoIdx; }
-        const float bv0 = bv;
         const uint32_t bi0 = bi;
         wave_argmax(bv, bi);
-        const uint64_t own = ballot(bi0 == bi && bv0 == bv && bi < V);
+        const uint64_t own = ballot(bi0 == bi && bi < V);
         braw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(braw), own ? __builtin_ctzll(own) : 0));
         if (lane == 0) {
             a.ids[row] = (int32_t)bi;
-            if (want_lp) a.chosen_lp[row] = (float)((double)braw - log_z);
+            sm.l.chosen_raw = braw;
             if (a.diag) {
                 lcs_row_diag dg{};
                 dg.n_cand = use_mask ? tot_allowed : V; dg.maxl = bv; dg.boundary = bv;
@@ -1128,17 +1199,17 @@ __device__ __forceinline__ bool slice_finalize(const SampleArgs& a, uint32_t row
         return false;
     }
 
-    // ---- the row window: entries with p >= maxl - delta ----
-    const float inv_t = fdiv(1.0f, P.temperature);
+    // row window threshold maxl - delta, as the smallest float at or above it
     const double delta = (double)P.temperature * (-log((double)P.min_p) + 1e-3);
     const float maxl = wave_max(m_pen);
     const double thr = (double)maxl - delta;
+    float thr_up = (float)thr;
+    if ((double)thr_up < thr) thr_up = next_up(thr_up);
     // a slice that could hold row-window entries must not have lost any
-    if (ballot(mine && (flags & rec::kFlagWinLost) && (double)m_pen >= thr)) return true;
+    if (ballot(mine && (flags & rec::kFlagWinLost) && m_pen >= thr_up)) return true;
     uint32_t q = 0;
 #pragma unroll
-    for (int j = 0; j < (int)kSpecWin; ++j)
-        q += ((uint32_t)j < n_win && (double)rank_val(wk[j]) >= thr) ? 1u : 0u;
+    for (int j = 0; j < (int)kSpecWin; ++j) q += ((uint32_t)j < n_win && rank_val(wk[j]) >= thr_up) ? 1u : 0u;
     const uint32_t base = wave_scan_incl_u(q) - q;
     uint32_t L0 = wave_sum_u(q);
     if (L0 > kRowWin) return true;
@@ -1165,7 +1236,7 @@ __device__ __forceinline__ bool slice_finalize(const SampleArgs& a, uint32_t row
         uint32_t qq = 0;
 #pragma unroll
         for (int j = 0; j < (int)kSpecWin; ++j)
-            qq += (more && j0 + j < n_win && (double)rank_val(ek[j]) >= thr) ? 1u : 0u;
+            qq += (more && j0 + j < n_win && rank_val(ek[j]) >= thr_up) ? 1u : 0u;
         const uint32_t b2 = L0 + wave_scan_incl_u(qq) - qq;
         L0 += wave_sum_u(qq);
         if (L0 > kRowWin) return true;
@@ -1182,38 +1253,44 @@ __device__ __forceinline__ bool slice_finalize(const SampleArgs& a, uint32_t row
     // a truncated slice whose every kept entry qualifies may hold more
     if (ballot(mine && (flags & rec::kFlagWinTrunc) && qtot == n_win)) return true;
     wave_sync();
-    // rank the row window (keys are unique)
-    {
-        uint64_t k[4];
-        uint32_t rk[4];
-        wave_rank4(sm.u.f.ent, L0, k, rk);
+    PROF_WMARK(10);
+    uint64_t k[4];
+    uint32_t rk[4];
+    lds_rank4(sm.u.f.ent, L0, k, rk);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
-            if (e < L0) { sm.u.f.sorted[rk[c]] = k[c]; sm.u.f.sortedraw[rk[c]] = sm.u.f.entraw[e]; }
-        }
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
+        if (e < L0) { sm.u.f.sorted[rk[c]] = k[c]; sm.u.f.sortedraw[rk[c]] = sm.u.f.entraw[e]; }
     }
-    wave_sync();
+    if (lane == 0) { sm.l.fin_L0 = L0; sm.l.fin_maxl = maxl; }
+    PROF_WMARK(11);
+    return false;
+}
 
-    // ---- normaliser: slice bulks rescaled to the row max, with their bound ----
-    const double d_s = mine ? ((double)m_pen - (double)maxl) * (double)inv_t : 0.0;
-    const double es = mine && m_pen != NEG ? exp(d_s) : 0.0;
-    const double Sf = wave_sum(es * bulk);
-    const double eps = wave_sum(es * (berr + fabs(d_s) * 0x1p-50 * bulk));
-    const double rel = 2.0 * eps / Sf + 0x1p-50;
-
-    // ---- top-p, then min-p (sampling.cpp order), 64 ranked entries at a time ----
+// Top-p, then min-p (sampling.cpp order), then the draw, 64 ranked row-window
+// entries at a time; weights exp((double)((p - maxl) * inv_t)) as the
+// reference's. Returns true when a top-p / min-p decision lies within the
+// normaliser's error bound.
+__device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, SliceSmem& sm) {
+    const int lane = lane_id();
+    PROF_WMARK(12);
+    const lcs_params P = a.params[row];
+    const uint32_t L0 = sm.l.fin_L0;
+    const float maxl = sm.l.fin_maxl;
+    const double Sf = sm.l.fin_S, rel = sm.l.fin_rel;
+    const float inv_t = fdiv(1.0f, P.temperature);
     bool uncertain = false;
     uint32_t keep_p = 0xffffffffu, keep = 0;
     const double tp = (double)P.top_p;
-    const double thresh = (double)P.min_p * (1.0 / Sf);
+    const double inv_S = 1.0 / Sf;
+    const double mp = (double)P.min_p;
     double cum_c = 0.0;
     for (uint32_t c0 = 0; c0 < L0 && keep == 0; c0 += kWave) {
         const uint32_t i = c0 + (uint32_t)lane;
         const bool in = i < L0;
         const double w = in ? exp((double)tempered(rank_val(sm.u.f.sorted[i]), maxl, inv_t)) : 0.0;
         if (in) sm.u.f.sw[i] = w;
-        const double qi = w / Sf;
+        const double qi = w * inv_S;
         const double cum = cum_c + wave_scan_incl(qi);
         if (P.top_p < 1.0f && keep_p == 0xffffffffu) {
             const uint64_t hit = ballot(in && cum >= tp);
@@ -1226,12 +1303,14 @@ __device__ __forceinline__ bool slice_finalize(const SampleArgs& a, uint32_t row
                 keep_p = c0 + (uint32_t)hl + 1u;
             }
         }
-        // min-p: first i in [1, min(keep_p, L0)) with w_i/S < thresh; the
-        // entry after the row window fails it by construction (margin 1e-3 in ln w)
+        // min-p: first i in [1, min(keep_p, L0)) with w_i/S < min_p * (w_0/S),
+        // i.e. w_i < min_p (w_0 = 1) away from a 1e-12 band where the
+        // reference's roundings decide; the entry after the row window fails
+        // it by construction (margin 1e-3 in ln w)
         const uint32_t lim = min(keep_p, L0);
         const bool cmp = in && i >= 1 && i < lim;
-        if (ballot(cmp && fabs(w / (double)P.min_p - 1.0) <= 1e-12)) uncertain = true;
-        const uint64_t fail = ballot(cmp && qi < thresh);
+        if (ballot(cmp && fabs(w - mp) <= 1e-12 * mp)) uncertain = true;
+        const uint64_t fail = ballot(cmp && w < mp);
         if (fail) keep = c0 + (uint32_t)__builtin_ctzll(fail);
         else if (lim <= c0 + kWave) keep = lim;
         cum_c = bits_d(readlane_u64(d_bits(cum), kWave - 1));
@@ -1240,8 +1319,8 @@ __device__ __forceinline__ bool slice_finalize(const SampleArgs& a, uint32_t row
     if (uncertain) return true;
     if (keep < 1) keep = 1;
     wave_sync();
-
-    // ---- kept mass and the draw (r -= w_i walk) ----
+    PROF_WMARK(13);
+    // kept mass and the draw (r -= w_i walk, sampling.cpp:135-147)
     double kept_sum = 0.0;
     for (uint32_t c0 = 0; c0 < keep; c0 += kWave) {
         const uint32_t i = c0 + (uint32_t)lane;
@@ -1259,13 +1338,14 @@ __device__ __forceinline__ bool slice_finalize(const SampleArgs& a, uint32_t row
         Wc = bits_d(readlane_u64(d_bits(W), kWave - 1));
     }
     if (pos == 0xffffffffu) pos = keep - 1;  // reference fallback: cand[keep-1]
+    PROF_WMARK(14);
     if (lane == 0) {
         const uint64_t ck = sm.u.f.sorted[pos];
         a.ids[row] = (int32_t)rank_idx(ck);
-        if (want_lp) a.chosen_lp[row] = (float)((double)sm.u.f.sortedraw[pos] - log_z);
+        sm.l.chosen_raw = sm.u.f.sortedraw[pos];
         if (a.diag) {
             lcs_row_diag dg{};
-            dg.n_cand = V; dg.keep = keep; dg.maxl = maxl;
+            dg.n_cand = a.vocab; dg.keep = keep; dg.maxl = maxl;
             dg.boundary = rank_val(sm.u.f.sorted[keep - 1]);
             dg.path = LCS_PATH_WINDOW; dg.sum = Sf; dg.kept_sum = kept_sum;
             a.diag[row] = dg;
@@ -1337,55 +1417,57 @@ void slice_kernel(SampleArgs a) {
         raw[j] = load16(rowp, (e0 < hi ? e0 : lo) / G);
     }
     uint32_t mw[NG];
+    if (mrow) {
 #pragma unroll
-    for (int j = 0; j < NG; ++j) {
-        const uint32_t e0 = lo + (j * NT + tid) * G;
-        const uint32_t ee = e0 < hi ? e0 : lo;
-        mw[j] = mrow ? (mrow[ee >> 5] >> (ee & 31u)) : 0xffffffffu;
+        for (int j = 0; j < NG; ++j) {
+            const uint32_t e0 = lo + (j * NT + tid) * G;
+            const uint32_t ee = e0 < hi ? e0 : lo;
+            mw[j] = mrow[ee >> 5] >> (ee & 31u);
+        }
     }
     if (tid == 0) { sm.l.ncand = 0; sm.l.nwin = 0; }
 
-    // ---- penalties: one override per distinct history id in this slice ----
+    // ---- penalties: LDS table of (penalised ^ raw) bits per slice position,
+    // 0 where no history id falls (sampling.cpp:16-41 applied once per id) ----
     if (hany) {
 #pragma unroll
         for (int i = 0; i < (int)(kSliceMax / 4 / NT); ++i) sm.u.ovr4[i * NT + tid] = make_uint4(0, 0, 0, 0);
-        __syncthreads();
-        auto count = [&](const uint32_t (&h)[HC]) {
-#pragma unroll
-            for (int k = 0; k < HC; ++k) {
-                const uint32_t d = h[k] - lo;
-                if (h[k] < V && d < len) atomicAdd(&sm.u.ovr[d], 1u);
-            }
-        };
-        count(hA);
-        if (htwo) count(hB);
-        __syncthreads();
-        // the first exchange of each id takes its count; it alone writes the override
-        uint32_t cA[HC], cB[HC];
+        // raw logits of the in-slice history ids, fetched while the table clears
         float rA[HC], rB[HC];
-        auto claim = [&](const uint32_t (&h)[HC], uint32_t (&c)[HC], float (&r)[HC]) {
+        auto gather = [&](const uint32_t (&h)[HC], float (&r)[HC]) {
 #pragma unroll
             for (int k = 0; k < HC; ++k) {
                 const uint32_t d = h[k] - lo;
-                c[k] = (h[k] < V && d < len) ? atomicExch(&sm.u.ovr[d], 0u) : 0u;
+                r[k] = load_elem(rowp, a.dtype, (h[k] < V && d < len) ? h[k] : lo);
             }
-#pragma unroll
-            for (int k = 0; k < HC; ++k) r[k] = load_elem(rowp, a.dtype, c[k] ? h[k] : lo);
         };
-        claim(hA, cA, rA);
-        if (htwo) claim(hB, cB, rB);
+        gather(hA, rA);
+        if (htwo) gather(hB, rB);
         __syncthreads();
-        auto put = [&](const uint32_t (&h)[HC], const uint32_t (&c)[HC], const float (&r)[HC]) {
+        // counts; the lane whose increment finds 0 owns the id
+        uint32_t oA = 0, oB = 0;
+        auto count = [&](const uint32_t (&h)[HC], uint32_t& own) {
 #pragma unroll
             for (int k = 0; k < HC; ++k) {
-                if (c[k]) {
-                    const uint32_t b = __float_as_uint(penalize(r[k], c[k], P));
-                    sm.u.ovr[h[k] - lo] = b ? b : 0x80000000u;   // +0 travels as -0
+                const uint32_t d = h[k] - lo;
+                if (h[k] < V && d < len && atomicAdd(&sm.u.ovr[d], 1u) == 0u) own |= 1u << k;
+            }
+        };
+        count(hA, oA);
+        if (htwo) count(hB, oB);
+        __syncthreads();
+        auto put = [&](const uint32_t (&h)[HC], const float (&r)[HC], uint32_t own) {
+#pragma unroll
+            for (int k = 0; k < HC; ++k) {
+                if ((own >> k) & 1u) {
+                    const uint32_t d = h[k] - lo;
+                    const float p = penalize(r[k], sm.u.ovr[d], P);
+                    sm.u.ovr[d] = __float_as_uint(p) ^ __float_as_uint(r[k]);
                 }
             }
         };
-        put(hA, cA, rA);
-        if (htwo) put(hB, cB, rB);
+        put(hA, rA, oA);
+        if (htwo) put(hB, rB, oB);
     }
     __syncthreads();
     PROF_MARK(1);
@@ -1396,10 +1478,14 @@ void slice_kernel(SampleArgs a) {
     for (int j = 0; j < NG; ++j) {
         float t[G];
         decode<G>(raw[j], t);
-        const uint32_t e0 = lo + (j * NT + tid) * G;
-        const bool full = lo + (j * NT + (uint32_t)wv * kWave + kWave) * G <= hi;  // wave-uniform
 #pragma unroll
-        for (int k = 0; k < G; ++k) v[j * G + k] = (full || e0 + k < hi) ? t[k] : NEG;
+        for (int k = 0; k < G; ++k) v[j * G + k] = t[k];
+        // wave-uniform: does this group row run past the slice for any lane?
+        if (lo + (j * NT + (uint32_t)wv * kWave + kWave) * G > hi) {
+            const uint32_t e0 = lo + (j * NT + tid) * G;
+#pragma unroll
+            for (int k = 0; k < G; ++k) v[j * G + k] = e0 + k < hi ? v[j * G + k] : NEG;
+        }
     }
     auto eid = [&](int q) { return lo + ((q / G) * NT + tid) * G + (uint32_t)(q % G); };
 
@@ -1419,10 +1505,12 @@ void slice_kernel(SampleArgs a) {
         if (lm >= t) {
 #pragma unroll
             for (int q = 0; q < kSliceElems; ++q) {
-                const uint32_t e = eid(q);
-                if (v[q] >= t && e < hi) {
-                    const uint32_t s = atomicAdd(&sm.l.ncand, 1u);
-                    if (s < kCandCap) sm.l.cand[s] = rank_key(v[q], e);
+                if (v[q] >= t) {
+                    const uint32_t e = eid(q);
+                    if (e < hi) {
+                        const uint32_t s = atomicAdd(&sm.l.ncand, 1u);
+                        if (s < kCandCap) sm.l.ck[s] = rank_key(v[q], e);
+                    }
                 }
             }
         }
@@ -1458,7 +1546,7 @@ void slice_kernel(SampleArgs a) {
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     const int qq = j * G + h4 * 4 + k;
-                    v[qq] = ob[k] ? __uint_as_float(ob[k]) : v[qq];
+                    v[qq] = __uint_as_float(__float_as_uint(v[qq]) ^ ob[k]);
                 }
             }
         }
@@ -1481,27 +1569,23 @@ void slice_kernel(SampleArgs a) {
                 if (al && (x > mv || mi == kNoIdx)) { mv = x; mi = e; }
             }
         }
-        // raw logits of the lane winners (re-read: the registers hold penalised values)
+        // raw logits of the lane winners: penalised ^ table bits
+        br = bv;
+        mr = mv;
         if (want_lp && hany) {
-            br = bi < V ? load_elem(rowp, a.dtype, bi) : 0.0f;
-            mr = mi < V ? load_elem(rowp, a.dtype, mi) : 0.0f;
-        } else {
-            br = bv;
-            mr = mv;
+            if (bi < V) br = __uint_as_float(__float_as_uint(bv) ^ sm.u.ovr[bi - lo]);
+            if (mi < V) mr = __uint_as_float(__float_as_uint(mv) ^ sm.u.ovr[mi - lo]);
         }
-        const float bv0 = bv, mv0 = mv;
         const uint32_t bi0 = bi, mi0 = mi;
         wave_argmax(bv, bi);
         const uint64_t ob = ballot(bi0 == bi && bi < V);
         br = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(br), ob ? __builtin_ctzll(ob) : 0));
-        (void)bv0;
         if (mrow) {
             wave_argmax(mv, mi);
             const uint64_t om = ballot(mi0 == mi && mi < V);
             mr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mr), om ? __builtin_ctzll(om) : 0));
             na = wave_sum_u(na);
         }
-        (void)mv0;
         if (lane == 0) {
             sm.l.mpen[wv] = bv; sm.l.ipen[wv] = bi; sm.l.rpen[wv] = br;
             sm.l.mmsk[wv] = mv; sm.l.imsk[wv] = mi; sm.l.rmsk[wv] = mr; sm.l.nall[wv] = na;
@@ -1541,20 +1625,17 @@ void slice_kernel(SampleArgs a) {
                 for (int k = 0; k < w; ++k) c[k] += c[k + w];
             bs += c[0];
         }
+        // window test in float, rounded down from the exact threshold (a superset)
         const double delta = (double)P.temperature * (-log((double)P.min_p) + 1e-3);
         const double thr = (double)ms - delta;
-        if ((double)lpm >= thr) {
+        float thr_f = (float)thr;
+        if ((double)thr_f > thr) thr_f = next_down(thr_f);
+        if (lpm >= thr_f) {
 #pragma unroll
             for (int q = 0; q < kSliceElems; ++q) {
-                if ((double)v[q] >= thr) {
+                if (v[q] >= thr_f) {
                     const uint32_t s = atomicAdd(&sm.l.nwin, 1u);
-                    if (s < kWinLds) {
-                        const uint32_t e = eid(q);
-                        sm.l.win[s] = rank_key(v[q], e);
-                        // raw logit: the value itself unless penalised (then fetched at publish)
-                        const uint32_t ob = hany ? sm.u.ovr[e - lo] : 0u;
-                        sm.l.winraw[s] = ob ? __uint_as_float(0x7fffffffu) : v[q];
-                    }
+                    if (s < kWinLds) sm.l.wk[s] = rank_key(v[q], eid(q));
                 }
             }
         }
@@ -1565,7 +1646,8 @@ void slice_kernel(SampleArgs a) {
     PROF_MARK(4);
     __syncthreads();
 
-    // ---- wave 0 combines the waves and publishes the slice record ----
+    // ---- publish: header (wave 0), top-n (wave 1), window entries (wave 2) ----
+    __builtin_amdgcn_s_setprio(3);
     if (wv == 0) {
         const bool lw = lane < kSliceWaves;
         const int wl = lw ? lane : 0;
@@ -1598,51 +1680,12 @@ void slice_kernel(SampleArgs a) {
                 na = wave_sum_u(lw ? sm.l.nall[wl] : 0u);
             }
         }
-        // slice top-n: ntop rounds over the candidates (<= 4 per lane)
-        const uint32_t nc = sm.l.ncand;
-        const uint32_t ncc = min(nc, kCandCap);
-        const uint32_t nts = min(ntop, len);
-        if (nts) {
-            uint64_t ck[kCandCap / kWave];
-#pragma unroll
-            for (int i = 0; i < (int)(kCandCap / kWave); ++i) {
-                const uint32_t s = (uint32_t)lane + (uint32_t)i * kWave;
-                ck[i] = s < ncc ? sm.l.cand[s] : ~0ull;
-            }
-            uint64_t myk = ~0ull;
-            for (uint32_t r = 0; r < nts; ++r) {
-                uint64_t m = ck[0];
-#pragma unroll
-                for (int i = 1; i < (int)(kCandCap / kWave); ++i) m = ck[i] < m ? ck[i] : m;
-                const uint64_t best = wave_min_u64(m);
-#pragma unroll
-                for (int i = 0; i < (int)(kCandCap / kWave); ++i) ck[i] = ck[i] == best ? ~0ull : ck[i];
-                if ((uint32_t)lane == r) myk = best;
-            }
-            if ((uint32_t)lane < nts) st_dev_u64(myrec + rec::kTop + lane, myk);
-        }
-        // window entries: the top kWinCap by rank, in ascending rank order
         const uint32_t nwr = stoch ? sm.l.nwin : 0u;
-        const uint32_t nwl = min(nwr, kWinLds);
-        const uint32_t nw = min(nwl, kWinCap);
-        if (nwl) {
-            uint64_t k[4];
-            uint32_t rk[4];
-            wave_rank4(sm.l.win, nwl, k, rk);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
-                if (e < nwl && rk[c] < kWinCap) {
-                    float kr = sm.l.winraw[e];
-                    if (__float_as_uint(kr) == 0x7fffffffu) kr = load_elem(rowp, a.dtype, rank_idx(k[c]));
-                    st_dev_u64(myrec + rec::kWin + rk[c], k[c]);
-                    st_dev_u64(myrec + rec::kWinRaw + rk[c], (uint64_t)__float_as_uint(kr));
-                }
-            }
-        }
+        const uint32_t nw = min(min(nwr, kWinLds), kWinCap);
+        const uint32_t nts = min(ntop, len);
         const uint32_t fl = (nwr > kWinCap ? rec::kFlagWinTrunc : 0u) |
                             (nwr > kWinLds ? rec::kFlagWinLost : 0u) |
-                            (nts && nc > kCandCap ? rec::kFlagCandOverflow : 0u);
+                            (nts && sm.l.ncand > kCandCap ? rec::kFlagCandOverflow : 0u);
         uint64_t hw = 0;
         switch (lane) {
             case 0: hw = (uint64_t)__float_as_uint(mrs) | ((uint64_t)nw << 32) | ((uint64_t)fl << 48); break;
@@ -1656,29 +1699,76 @@ void slice_kernel(SampleArgs a) {
             default: break;
         }
         if (lane < (int)rec::kHdr) st_dev_u64(myrec + lane, hw);
-        wait_all_memory();
-        if (lane == 0) {
-            const uint32_t prev = __hip_atomic_fetch_add(a.counters + row, 1u, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-            const bool last = prev == S - 1;
-            if (last) st_dev(a.counters + row, 0u);
-            sm.l.last = last ? 1u : 0u;
-            sm.l.fallback = 0u;
+    } else if (wv == 1) {
+        // slice top-n: rank the candidates, store the first nts
+        const uint32_t nts = min(ntop, len);
+        const uint32_t ncc = min(sm.l.ncand, kCandCap);
+        if (nts) {
+            uint64_t k[4];
+            uint32_t rk[4];
+            lds_rank4(sm.l.ck, ncc, k, rk);
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
+                if (e < ncc && rk[c] < nts) st_dev_u64(myrec + rec::kTop + rk[c], k[c]);
+            }
+        }
+    } else if (wv == 2 && stoch) {
+        // window entries: the top kWinCap by rank, in ascending rank order,
+        // each with its raw logit (the value itself unless penalised)
+        const uint32_t nwl = min(sm.l.nwin, kWinLds);
+        if (nwl) {
+            uint64_t k[4];
+            uint32_t rk[4];
+            lds_rank4(sm.l.wk, nwl, k, rk);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
+                if (e < nwl && rk[c] < kWinCap) {
+                    const uint32_t id = rank_idx(k[c]);
+                    const uint32_t kr = __float_as_uint(rank_val(k[c])) ^ (hany ? sm.u.ovr[id - lo] : 0u);
+                    st_dev_u64(myrec + rec::kWin + rk[c], k[c]);
+                    st_dev_u64(myrec + rec::kWinRaw + rk[c], (uint64_t)kr);
+                }
+            }
         }
     }
-    PROF_MARK(5);
+    wait_all_memory();
+    PROF_WMARK(19);
     __syncthreads();
+    if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(a.counters + row, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = prev == S - 1;
+        if (last) st_dev(a.counters + row, 0u);
+        sm.l.last = last ? 1u : 0u;
+        sm.l.fin_fb = 0u;
+    }
+    __syncthreads();
+    PROF_MARK(5);
     if (!sm.l.last) return;
     // =============== last-arriving workgroup finishes the row ===============
+    bool fb = false;
     if (wv == 0) {
-        const bool fb = slice_finalize(a, row, mode, sm);
-        if (lane == 0) sm.l.fallback = fb ? 1u : 0u;
+        fb = fin_gather(a, row, mode, sm);
+    } else if (wv == 1) {
+        if (want_lp) fb = fin_logprobs(a, row, sm);
+    } else if (wv == 2) {
+        if (stoch) fin_norm(a, row, sm);
+    }
+    if (fb && lane == 0) sm.l.fin_fb = 1u;
+    __syncthreads();
+    if (wv == 0 && stoch && !sm.l.fin_fb) {
+        fb = fin_decide(a, row, sm);
+        if (fb && lane == 0) sm.l.fin_fb = 1u;
     }
     __syncthreads();
     PROF_MARK(6);
-    if (sm.l.fallback) {
+    if (sm.l.fin_fb) {
         stage_args(&sm.u.ex.args);
         exact_row<kSliceThreads, kFbBins, kFbCap, kFbHistCap, G>(sm.u.ex.args, row, sm.u.ex);
+    } else if (tid == 0 && want_lp) {
+        a.chosen_lp[row] = (float)((double)sm.l.chosen_raw - sm.l.log_z);
     }
 }
 
