@@ -1284,20 +1284,24 @@ __device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, Sl
     const double tp = (double)P.top_p;
     const double inv_S = 1.0 / Sf;
     const double mp = (double)P.min_p;
-    double cum_c = 0.0;
+    const double u = a.u[row];
+    // one inclusive scan of the weights per 64 entries serves the top-p sums
+    // (cum = W / S), the kept mass and the draw
+    double Wc = 0.0, kept_sum = 0.0;
+    uint32_t pos = 0xffffffffu;
     for (uint32_t c0 = 0; c0 < L0 && keep == 0; c0 += kWave) {
         const uint32_t i = c0 + (uint32_t)lane;
         const bool in = i < L0;
         const double w = in ? exp((double)tempered(rank_val(sm.u.f.sorted[i]), maxl, inv_t)) : 0.0;
         if (in) sm.u.f.sw[i] = w;
-        const double qi = w * inv_S;
-        const double cum = cum_c + wave_scan_incl(qi);
+        const double W = Wc + wave_scan_incl(w);
+        const double cum = W * inv_S;
         if (P.top_p < 1.0f && keep_p == 0xffffffffu) {
             const uint64_t hit = ballot(in && cum >= tp);
             if (hit) {
                 const int hl = __builtin_ctzll(hit);
                 const double ch = bits_d(readlane_u64(d_bits(cum), hl));
-                const double cp = hl > 0 ? bits_d(readlane_u64(d_bits(cum), hl - 1)) : cum_c;
+                const double cp = hl > 0 ? bits_d(readlane_u64(d_bits(cum), hl - 1)) : Wc * inv_S;
                 if (ch - tp <= rel * ch + 1e-13) uncertain = true;
                 if (c0 + (uint32_t)hl > 0 && tp - cp <= rel * cp + 1e-13) uncertain = true;
                 keep_p = c0 + (uint32_t)hl + 1u;
@@ -1313,31 +1317,40 @@ __device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, Sl
         const uint64_t fail = ballot(cmp && w < mp);
         if (fail) keep = c0 + (uint32_t)__builtin_ctzll(fail);
         else if (lim <= c0 + kWave) keep = lim;
-        cum_c = bits_d(readlane_u64(d_bits(cum), kWave - 1));
-    }
-    if (P.top_p < 1.0f && keep_p == 0xffffffffu && tp - cum_c <= rel * cum_c + 1e-13) uncertain = true;
-    if (uncertain) return true;
-    if (keep < 1) keep = 1;
-    wave_sync();
-    PROF_WMARK(13);
-    // kept mass and the draw (r -= w_i walk, sampling.cpp:135-147)
-    double kept_sum = 0.0;
-    for (uint32_t c0 = 0; c0 < keep; c0 += kWave) {
-        const uint32_t i = c0 + (uint32_t)lane;
-        kept_sum += wave_sum(i < keep ? sm.u.f.sw[i] : 0.0);
-    }
-    const double r0 = a.u[row] * (kept_sum - 0.0) + 0.0;
-    uint32_t pos = 0xffffffffu;
-    double Wc = 0.0;
-    for (uint32_t c0 = 0; c0 < keep && pos == 0xffffffffu; c0 += kWave) {
-        const uint32_t i = c0 + (uint32_t)lane;
-        const bool kept = i < keep;
-        const double W = Wc + wave_scan_incl(kept ? sm.u.f.sw[i] : 0.0);
-        const uint64_t hit = ballot(kept && r0 - W <= 0.0);
-        if (hit) pos = c0 + (uint32_t)__builtin_ctzll(hit);
+        if (keep != 0 && c0 == 0) {
+            // kept set inside the first 64: kept mass and the draw from this scan
+            const uint32_t kk = keep < 1 ? 1u : keep;
+            kept_sum = bits_d(readlane_u64(d_bits(W), (int)kk - 1));
+            const double r0 = u * (kept_sum - 0.0) + 0.0;
+            const uint64_t h2 = ballot(i < kk && r0 - W <= 0.0);
+            pos = h2 ? (uint32_t)__builtin_ctzll(h2) : kk - 1;
+        }
         Wc = bits_d(readlane_u64(d_bits(W), kWave - 1));
     }
-    if (pos == 0xffffffffu) pos = keep - 1;  // reference fallback: cand[keep-1]
+    if (P.top_p < 1.0f && keep_p == 0xffffffffu && tp - Wc * inv_S <= rel * Wc * inv_S + 1e-13) uncertain = true;
+    if (uncertain) return true;
+    if (keep < 1) keep = 1;
+    PROF_WMARK(13);
+    if (pos == 0xffffffffu) {
+        // kept set past the first 64 entries (r -= w_i walk, sampling.cpp:135-147)
+        wave_sync();
+        kept_sum = 0.0;
+        for (uint32_t c0 = 0; c0 < keep; c0 += kWave) {
+            const uint32_t i = c0 + (uint32_t)lane;
+            kept_sum += wave_sum(i < keep ? sm.u.f.sw[i] : 0.0);
+        }
+        const double r0 = u * (kept_sum - 0.0) + 0.0;
+        double Wd = 0.0;
+        for (uint32_t c0 = 0; c0 < keep && pos == 0xffffffffu; c0 += kWave) {
+            const uint32_t i = c0 + (uint32_t)lane;
+            const bool kept = i < keep;
+            const double W = Wd + wave_scan_incl(kept ? sm.u.f.sw[i] : 0.0);
+            const uint64_t hit = ballot(kept && r0 - W <= 0.0);
+            if (hit) pos = c0 + (uint32_t)__builtin_ctzll(hit);
+            Wd = bits_d(readlane_u64(d_bits(W), kWave - 1));
+        }
+        if (pos == 0xffffffffu) pos = keep - 1;  // reference fallback: cand[keep-1]
+    }
     PROF_WMARK(14);
     if (lane == 0) {
         const uint64_t ck = sm.u.f.sorted[pos];

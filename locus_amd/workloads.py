@@ -150,7 +150,7 @@ class Workload:
         if self.n_seq:
             return b + 4 * self.rows + 4 * self.rows + 4 * self.rows + 4 * self.n_seq
         if self.hist_ids is not None:
-            b += 4 * (len(self.hist_ids) + self.rows + 1)
+            b += 4 * len(self.hist_ids)   # history ids (the CSR offsets are not counted)
         if self.mask is not None:
             b += 4 * self.mask.size
         b += 32 * self.rows
