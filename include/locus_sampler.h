@@ -78,6 +78,10 @@ typedef struct lcs_batch {
                                   constrained when mask != NULL */
     uint32_t mask_words;       /* >= ceil(V/32) when mask != NULL */
     uint32_t n_top;            /* alternatives per row (<= the context's max_top) */
+    const int32_t* lp_ids;     /* rows, or NULL: with LCS_WANT_LOGPROBS, chosen_lp
+                                  reports the logprob of lp_ids[row] instead of the
+                                  sampled id (logprobs_from's `chosen` argument,
+                                  sampling.hpp:86-89); ids outside [0, V) give 0 */
 } lcs_batch;
 
 /* Per-row diagnostics (optional output): the survivor set of the reference's

@@ -3,6 +3,10 @@ with the tree to the GPU box).
 
 * liblocus_sampler.so - HIP kernels for gfx950 + the C ABI
   (include/locus_sampler.h), compiled with hipcc.
+* liblocus_host.so - the C++ host layer (include/locus/...: the reference's
+  sampling API over the C ABI, JSON grammar and mask builder, n-gram draft,
+  backend registry) and its C ABI (include/locus_host.h).
+* tests/cpp/test_host - the host layer's C++ test program.
 """
 from __future__ import annotations
 
@@ -27,6 +31,10 @@ HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contra
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I" + INCLUDE]
 HIP_SOURCES = ["lcs_api.hip", "lcs_sample.hip", "lcs_verify.hip"]
 SAMPLER_SO = os.path.join(HERE, "liblocus_sampler.so")
+HOST_SO = os.path.join(HERE, "liblocus_host.so")
+HOST_SOURCES = ["grammar.cpp", "speculative.cpp", "sampler_registry.cpp", "host_capi.cpp", "sampling.cpp"]
+HOST_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-Wall", "-I" + INCLUDE]
+TEST_HOST = os.path.join(ROOT, "tests", "cpp", "test_host")
 
 
 def _run(cmd):
@@ -53,8 +61,31 @@ def build_sampler(jobs: int = 4) -> str:
     return SAMPLER_SO
 
 
+def build_host(jobs: int = 4) -> str:
+    """The C++ host layer, linked against liblocus_sampler.so (found next to
+    it at run time), and its test program."""
+    os.makedirs(BUILD, exist_ok=True)
+    objs, cmds = [], []
+    for src in HOST_SOURCES:
+        obj = os.path.join(BUILD, "host_" + src.replace(".cpp", ".o"))
+        objs.append(obj)
+        cmds.append([HIPCC, *HOST_FLAGS, "-c", os.path.join(HERE, "host", src), "-o", obj])
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(_run, cmds))
+    tmp = HOST_SO + ".tmp"
+    _run([HIPCC, "-shared", "-o", tmp, *objs, "-L" + HERE, "-llocus_sampler", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, HOST_SO)
+    tobj = os.path.join(BUILD, "test_host.o")
+    _run([HIPCC, *HOST_FLAGS, "-c", os.path.join(ROOT, "tests", "cpp", "test_host.cpp"), "-o", tobj])
+    _run([HIPCC, "-o", TEST_HOST + ".tmp", tobj, "-L" + HERE, "-llocus_host", "-llocus_sampler",
+          "-Wl,-rpath," + os.path.relpath(HERE, os.path.dirname(TEST_HOST)).join(["$ORIGIN/", ""])])
+    os.replace(TEST_HOST + ".tmp", TEST_HOST)
+    return HOST_SO
+
+
 def build_all() -> None:
     build_sampler()
+    build_host()
 
 
 if __name__ == "__main__":

@@ -211,6 +211,7 @@ int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
     a.u = b->u;
     a.mask = b->mask;
     a.has_mask = b->has_mask;
+    a.lp_ids = b->lp_ids;
     a.ids = o->ids;
     a.chosen_lp = o->chosen_lp;
     a.top_ids = o->top_ids;

@@ -73,6 +73,7 @@ struct SampleArgs {
     const double* u;
     const uint32_t* mask;
     const uint8_t* has_mask;
+    const int32_t* lp_ids;
     int32_t* ids;
     float* chosen_lp;
     int32_t* top_ids;

@@ -369,10 +369,11 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
             const int32_t id = (int32_t)maxi;
             a.ids[row] = id;
             if (want_lp) {
-                const float raw = (nD > 0 && d_find(d_ids, nD, maxi) >= 0)
-                                      ? d_raw[d_find(d_ids, nD, maxi)]
-                                      : load_elem(rowp, a.dtype, maxi);
-                write_logprobs(a, row, id, raw, log_z, sm.topbuf, ntop);
+                const int32_t lid = a.lp_ids ? a.lp_ids[row] : id;
+                const bool inr = lid >= 0 && (uint32_t)lid < V;
+                const int j = inr && nD > 0 ? d_find(d_ids, nD, (uint32_t)lid) : -1;
+                const float raw = j >= 0 ? d_raw[j] : (inr ? load_elem(rowp, a.dtype, (uint32_t)lid) : 0.0f);
+                write_logprobs(a, row, lid, raw, log_z, sm.topbuf, ntop);
             }
             if (a.diag) {
                 lcs_row_diag dg{};
@@ -885,9 +886,11 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
         if (tid == 0) {
             a.ids[row] = chosen;
             if (want_lp) {
-                const int j = nD > 0 ? d_find(d_ids, nD, (uint32_t)chosen) : -1;
-                const float raw = j >= 0 ? d_raw[j] : load_elem(rowp, a.dtype, (uint32_t)chosen);
-                write_logprobs(a, row, chosen, raw, log_z, sm.topbuf, ntop);
+                const int32_t lid = a.lp_ids ? a.lp_ids[row] : chosen;
+                const bool inr = lid >= 0 && (uint32_t)lid < V;
+                const int j = inr && nD > 0 ? d_find(d_ids, nD, (uint32_t)lid) : -1;
+                const float raw = j >= 0 ? d_raw[j] : (inr ? load_elem(rowp, a.dtype, (uint32_t)lid) : 0.0f);
+                write_logprobs(a, row, lid, raw, log_z, sm.topbuf, ntop);
             }
             if (a.diag) {
                 lcs_row_diag dg{};
@@ -1781,7 +1784,14 @@ void slice_kernel(SampleArgs a) {
         stage_args(&sm.u.ex.args);
         exact_row<kSliceThreads, kFbBins, kFbCap, kFbHistCap, G>(sm.u.ex.args, row, sm.u.ex);
     } else if (tid == 0 && want_lp) {
-        a.chosen_lp[row] = (float)((double)sm.l.chosen_raw - sm.l.log_z);
+        float raw = sm.l.chosen_raw;
+        bool inr = true;
+        if (a.lp_ids) {
+            const int32_t lid = a.lp_ids[row];
+            inr = lid >= 0 && (uint32_t)lid < V;
+            raw = inr ? load_elem(rowp, a.dtype, (uint32_t)lid) : 0.0f;
+        }
+        a.chosen_lp[row] = inr ? (float)((double)raw - sm.l.log_z) : 0.0f;
     }
 }
 

@@ -21,6 +21,8 @@ constexpr int kVerifyThreads = 256;
 template <int G>
 __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     constexpr int NT = kVerifyThreads;
+    constexpr int U = 8;                   // 16-byte groups in flight per thread
+    constexpr float kL2E = 1.4426950408889634f;
     __shared__ float redf[NT / kWave];
     __shared__ uint32_t redu[NT / kWave];
     __shared__ double redd[NT / kWave];
@@ -31,31 +33,65 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     const uint32_t V = a.vocab;
     const uint32_t esz = a.dtype == LCS_BF16 ? 2u : 4u;
     const void* rowp = static_cast<const char*>(a.logits) + (uint64_t)row * a.row_stride * esz;
+    const float NEG = -__builtin_huge_valf();
 
-    float bm = -__builtin_huge_valf();
-    uint32_t bi = 0xffffffffu;
-    float om = -__builtin_huge_valf();
+    // per lane: running max om, the first group bg that reached it, and
+    // os = sum exp(v - om) (f32 group sums of exp2 accumulated in f64)
+    const uint32_t ng = (V + G - 1) / G;
+    float om = NEG;
     double os = 0.0;
-    stream_groups<NT, G>(rowp, V, [&](uint32_t gi, const float (&v)[G], uint32_t nv) {
-        float gm = -__builtin_huge_valf();
-        uint32_t gidx = 0xffffffffu;
-        for (uint32_t k = 0; k < nv; ++k) {
-            if (gidx == 0xffffffffu || v[k] > gm) { gm = v[k]; gidx = gi * G + k; }
+    uint32_t bg = 0xffffffffu;
+    for (uint32_t g0 = 0; g0 < ng; g0 += NT * U) {
+        uint4 r[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t gi = g0 + u * NT + threadIdx.x;
+            r[u] = load16(rowp, gi < ng ? gi : 0u);
         }
-        if (bi == 0xffffffffu || gm > bm) { bm = gm; bi = gidx; }
-        if (gm > om) {
-            os = (om == -__builtin_huge_valf()) ? 0.0 : os * exp((double)om - (double)gm);
-            om = gm;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t gi = g0 + u * NT + threadIdx.x;
+            if (gi >= ng) continue;
+            float v[G];
+            decode<G>(r[u], v);
+            if (gi * G + G > V) {
+#pragma unroll
+                for (int k = 0; k < G; ++k) v[k] = gi * G + k < V ? v[k] : NEG;
+            }
+            float gm = v[0];
+#pragma unroll
+            for (int k = 1; k < G; ++k) gm = fmaxf(gm, v[k]);
+            if (gm > om) {
+                os = om == NEG ? 0.0 : os * (double)__builtin_amdgcn_exp2f((om - gm) * kL2E);
+                om = gm;
+                bg = gi;
+            }
+            if (om != NEG) {
+                const float b = -om * kL2E;
+                float c[G];
+#pragma unroll
+                for (int k = 0; k < G; ++k) c[k] = __builtin_amdgcn_exp2f(fmaf(v[k], kL2E, b));
+#pragma unroll
+                for (int w = G / 2; w >= 1; w /= 2)
+#pragma unroll
+                    for (int k = 0; k < w; ++k) c[k] += c[k + w];
+                os += (double)c[0];
+            }
         }
-        if (om != -__builtin_huge_valf()) {
-            float gs = 0.0f;
-            for (uint32_t k = 0; k < nv; ++k) gs += expf(fsub(v[k], om));
-            os += (double)gs;
-        }
-    });
-    uint32_t idx = bi == 0xffffffffu ? 0xfffffffeu : bi;
+    }
+    // first index of the lane max inside its first group
+    uint32_t idx = 0xfffffffeu;
+    if (bg != 0xffffffffu) {
+        float v[G];
+        decode<G>(load16(rowp, bg), v);
+        uint32_t k = G;
+#pragma unroll
+        for (int j = G - 1; j >= 0; --j) k = (bg * G + j < V && v[j] == om) ? (uint32_t)j : k;
+        idx = bg * G + k;
+    }
+    float bm = om;
     block_argmax<NT>(bm, idx, redf, redu);
-    const double sc = (om == -__builtin_huge_valf()) ? 0.0 : os * exp((double)om - (double)bm);
+    const double sc = om == NEG ? 0.0 : os * exp((double)om - (double)bm);
     const double z = block_sum<NT>(sc, redd);
     if (threadIdx.x == 0) {
         const double log_z = log(z) + (double)bm;
@@ -63,7 +99,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
         float lp = 0.0f;
         if (d >= 0 && (uint32_t)d < V) lp = (float)((double)load_elem(rowp, a.dtype, (uint32_t)d) - log_z);
         a.draft_lp[row] = lp;
-        st_dev(reinterpret_cast<uint32_t*>(a.argmax_ids + row), idx);
+        st_dev(reinterpret_cast<uint32_t*>(a.argmax_ids + row), idx < V ? idx : 0u);
     }
     if (!arrive_last(a.counters + row / a.rows_per_seq, a.rows_per_seq, &last)) return;
     if (threadIdx.x == 0) {

@@ -34,7 +34,7 @@ class _Batch(C.Structure):
                 ("flags", C.c_uint32), ("row_stride", C.c_uint64), ("logits", _P),
                 ("params", _P), ("params_host", _P), ("hist_off", _P), ("hist_ids", _P),
                 ("u", _P), ("mask", _P), ("has_mask", _P), ("mask_words", C.c_uint32),
-                ("n_top", C.c_uint32)]
+                ("n_top", C.c_uint32), ("lp_ids", _P)]
 
 
 class _Out(C.Structure):
@@ -243,8 +243,10 @@ class Sampler:
         return _stream_handle(self.torch, stream)
 
     def sample_dev(self, d, out, n_top: int | None = None, want_lp: bool | None = None,
-                   has_mask=None, flags_extra: int = 0, use_host_params: bool = True, stream=None):
-        """Enqueues lcs_sample on device buffers from upload()/alloc_out()."""
+                   has_mask=None, flags_extra: int = 0, use_host_params: bool = True, stream=None,
+                   lp_ids=None):
+        """Enqueues lcs_sample on device buffers from upload()/alloc_out();
+        `lp_ids` (device int32 per row) makes chosen_lp report those ids."""
         w = d["w"]
         want_lp = w.want_logprobs if want_lp is None else want_lp
         n_top = w.n_top if n_top is None else n_top
@@ -264,13 +266,14 @@ class Sampler:
         b.has_mask = _dptr(has_mask)
         b.mask_words = w.mask_words
         b.n_top = n_top if want_lp else 0
+        b.lp_ids = _dptr(lp_ids)
         o = _Out()
         o.ids = _dptr(out["ids"])
         o.chosen_lp = _dptr(out.get("chosen_lp"))
         o.top_ids = _dptr(out.get("top_ids"))
         o.top_lp = _dptr(out.get("top_lp"))
         o.diag = _dptr(out.get("diag"))
-        self._keep = (ph, b, o)
+        self._keep = (ph, b, o, lp_ids)
         self._check(lib().lcs_sample(self.ctx, C.byref(b), C.byref(o),
                                      _stream_handle(self.torch, stream)))
 

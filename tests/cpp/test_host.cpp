@@ -1,0 +1,313 @@
+// Host-layer tests in C++ against the public headers (include/locus/...):
+// the reference's own known-answer tests for sampling, the JSON grammar and
+// the n-gram draft (tests/test_sampling.cpp, test_grammar.cpp,
+// test_speculative.cpp), restated with a minimal harness, plus the mask
+// builder against per-token allows() and the backend-resolution rules.
+//   test_host cpu   grammar, mask builder, n-gram draft, registry (no device)
+//   test_host gpu   sampling API on the device, registry with a device
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <random>
+#include <set>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "locus/backend/sampler_registry.hpp"
+#include "locus/model/grammar.hpp"
+#include "locus/model/sampling.hpp"
+#include "locus/model/speculative.hpp"
+
+using namespace locus::model;
+using locus::tok::TokenId;
+
+static int g_fail = 0, g_pass = 0;
+#define CHECK(cond)                                                                   \
+    do {                                                                              \
+        if (cond) {                                                                   \
+            ++g_pass;                                                                 \
+        } else {                                                                      \
+            ++g_fail;                                                                 \
+            std::fprintf(stderr, "FAIL %s:%d: %s\n", __FILE__, __LINE__, #cond);      \
+        }                                                                             \
+    } while (0)
+
+template <class E, class F>
+static bool throws(F&& f) {
+    try {
+        f();
+    } catch (const E&) {
+        return true;
+    } catch (...) {
+        return false;
+    }
+    return false;
+}
+
+static bool feed_all(JsonGrammar& g, const std::string& s) {
+    for (unsigned char c : s)
+        if (!g.feed(c)) return false;
+    return true;
+}
+
+static void test_grammar() {
+    for (const char* s : {"{}", "[]", "\"hi\"", "123", "-1.5e3", "true", "false", "null", "{\"a\":1}",
+                          "[1,2,3]", "{\"a\":[1,{\"b\":\"c\"}],\"d\":null}", "  {  \"x\" : 1 }  ",
+                          "[ -0.5 , 2 ]", "[12,34]", "{\"n\":42}", "42", "42   ", "\"\\u00e9\\n\""}) {
+        JsonGrammar g;
+        const bool ok = feed_all(g, s) && g.complete();
+        if (!ok) std::fprintf(stderr, "  accept: %s\n", s);
+        CHECK(ok);
+    }
+    for (const char* s : {"{", "{\"a\"", "{\"a\":", "[1,", "\"ab", "tr", "-", "[1"}) {
+        JsonGrammar g;
+        CHECK(feed_all(g, s));
+        CHECK(!g.complete());
+    }
+    for (const char* s : {"{,}", "[,]", "[1,]", "{\"a\" 1}", "{1:2}", "trux", "{}x", "01a", "[1 2]", "}",
+                          "42x", "\"\\x\"", "\"\\u12g\"", "[}", "{]"}) {
+        JsonGrammar g;
+        const bool rej = !feed_all(g, s);
+        if (!rej) std::fprintf(stderr, "  reject: %s\n", s);
+        CHECK(rej);
+    }
+    JsonGrammar g;
+    CHECK(feed_all(g, "{}"));
+    CHECK(g.complete());
+    CHECK(g.feed(' '));
+    CHECK(g.complete());
+    CHECK(!g.feed('x'));
+}
+
+static std::vector<std::string> synthetic_pieces() {
+    std::vector<std::string> p;
+    for (int b = 0; b < 256; ++b) p.push_back(std::string(1, static_cast<char>(b)));
+    for (const char* s : {"{\"", "\":", "\", \"", "\"}", "true", "false", "null", "tru", "ul", "123", "-0.5e3",
+                          "1.", "e+", "\\u00", "e9", "\\n", "  ", "\n  ", "},", "]}", "[[", "]]", "{}", "[]",
+                          ",\"", "\": \"", "\":[", "\":{", "abc", "ab\"", "\"a\":1", "1,2", "0]", "}}", "\"\"",
+                          "x", "", ""}) {
+        p.push_back(s);
+    }
+    std::mt19937_64 r(7);
+    const char alpha[] = "{}[]\":,. -+eE0123456789tfnrulsa\\bx \n";
+    for (int i = 0; i < 600; ++i) {
+        std::string s;
+        const int n = 1 + static_cast<int>(r() % 12);
+        for (int k = 0; k < n; ++k) s.push_back(alpha[r() % (sizeof(alpha) - 1)]);
+        p.push_back(s);
+    }
+    return p;
+}
+
+static void test_mask_builder() {
+    auto pieces = synthetic_pieces();
+    auto mb = std::make_shared<const JsonMaskBuilder>(pieces, 64);
+    const std::uint32_t V = static_cast<std::uint32_t>(pieces.size()) + 37;   // tail tokens allowed
+    const std::uint32_t words = (V + 31) / 32;
+    std::vector<std::uint32_t> m(words), brute(words);
+    int states = 0, mism = 0;
+    for (const char* doc : {"{\"a\": [1, -2.5e3, true, null, {\"b\": \"x\\u00e9y\\n\"}], \"c\": false}",
+                            "[[[[{\"k\":[]}]]], \"s\", 0]", "  \"str\"  ", "-12.5E+3", "{\"a\":{\"b\":{\"c\":{}}}}"}) {
+        JsonTokenConstraint c(mb);
+        const std::string d = doc;
+        for (std::size_t i = 0; i <= d.size(); ++i) {
+            CHECK(c.allow_mask(V, m.data()));
+            std::fill(brute.begin(), brute.end(), 0u);
+            for (std::uint32_t t = 0; t < V; ++t)
+                if (c.allows(static_cast<TokenId>(t))) brute[t >> 5] |= 1u << (t & 31);
+            ++states;
+            if (m != brute) ++mism;
+            // a second build of the same state comes from the cache and must agree
+            std::vector<std::uint32_t> again(words);
+            c.allow_mask(V, again.data());
+            if (again != m) ++mism;
+            if (i < d.size()) {
+                // advance by the single-byte token of the next byte (piece t == byte t)
+                c.commit(static_cast<TokenId>(static_cast<unsigned char>(d[i])));
+            }
+        }
+    }
+    std::fprintf(stderr, "  mask builder: %d states, %d mismatches, cache hits/misses %llu/%llu\n", states,
+                 mism, (unsigned long long)mb->cache_stats().first, (unsigned long long)mb->cache_stats().second);
+    CHECK(states > 100);
+    CHECK(mism == 0);
+}
+
+static void test_ngram() {
+    CHECK((ngram_draft(std::vector<TokenId>{1, 2, 3, 4, 1, 2, 3}, 2, 3) == std::vector<TokenId>{4, 1, 2}));
+    CHECK((ngram_draft(std::vector<TokenId>{9, 9, 5, 9, 9, 7, 9, 9}, 2, 2) == std::vector<TokenId>{7, 9}));
+    const std::vector<TokenId> none{5, 6, 7}, tiny{1, 2};
+    CHECK(ngram_draft(none, 2, 3).empty());
+    CHECK(ngram_draft(tiny, 2, 3).empty());
+    CHECK(ngram_draft(none, 0, 3).empty());
+    CHECK(ngram_draft(none, 1, 0).empty());
+    // overlapping match: the draft may run into the trailing n-gram itself
+    CHECK((ngram_draft(std::vector<TokenId>{3, 3, 3}, 1, 5) == std::vector<TokenId>{3}));
+}
+
+static void test_registry(bool gpu) {
+    using namespace locus::backend;
+    const auto all = sampler_backends();
+    CHECK(all.size() == 1 && all[0].name == "hip");
+    CHECK(find_sampler_backend("hip") != nullptr);
+    CHECK(find_sampler_backend("scalar") == nullptr);
+    CHECK(throws<std::invalid_argument>([] { resolve_sampler_backend("scalar"); }));
+    CHECK(throws<std::invalid_argument>([] { resolve_sampler_backend("bogus"); }));
+    if (gpu) {
+        CHECK(all[0].available);
+        CHECK(resolve_sampler_backend("").name == "hip");
+        CHECK(resolve_sampler_backend("hip").name == "hip");
+        CHECK(best_sampler_backend().ops.sample_batch != nullptr);
+    } else {
+        CHECK(!all[0].available);
+        CHECK(throws<std::runtime_error>([] { best_sampler_backend(); }));
+        CHECK(throws<std::invalid_argument>([] { resolve_sampler_backend("hip"); }));
+    }
+}
+
+namespace {
+struct AllowSet : TokenConstraint {
+    std::set<TokenId> ok;
+    bool allows(TokenId t) const override { return ok.count(t) > 0; }
+    void commit(TokenId) override {}
+};
+}  // namespace
+
+static void test_sampling_gpu() {
+    std::mt19937_64 rng(123);
+    const std::vector<TokenId> none;
+    {
+        std::vector<float> l{1.0f, 3.0f, 2.0f, 0.5f};
+        CHECK(sample(l, SamplingParams{}, none, rng) == 1);
+    }
+    {
+        std::vector<float> l{5.0f, 4.9f};
+        SamplingParams p;
+        p.repeat_penalty = 10.0f;
+        const std::vector<TokenId> h{0};
+        CHECK(sample(l, p, h, rng) == 1);
+        CHECK(l[0] == 0.5f);   // penalised in place
+    }
+    {
+        std::vector<float> l{5.0f, 4.0f};
+        SamplingParams p;
+        p.frequency_penalty = 1.0f;
+        const std::vector<TokenId> h{0, 0, 0};
+        CHECK(sample(l, p, h, rng) == 1);
+        CHECK(l[0] == 2.0f);
+    }
+    {
+        SamplingParams p;
+        p.temperature = 1.5f;
+        p.top_k = 1;
+        for (int i = 0; i < 20; ++i) {
+            std::vector<float> l{0.1f, 0.2f, 5.0f, 0.3f};
+            CHECK(sample(l, p, none, rng) == 2);
+        }
+    }
+    {
+        SamplingParams p;
+        p.temperature = 1.0f;
+        std::mt19937_64 a(42), b(42);
+        for (int i = 0; i < 16; ++i) {
+            std::vector<float> la{1, 1, 1, 1}, lb{1, 1, 1, 1};
+            CHECK(sample(la, p, none, a) == sample(lb, p, none, b));
+        }
+        // exactly one engine output per stochastic call, none per greedy call
+        std::mt19937_64 c(42), d(42);
+        std::vector<float> l{1, 2, 3};
+        sample(l, p, none, c);
+        d();
+        CHECK(c() == d());
+        std::vector<float> g{1, 2, 3};
+        sample(g, SamplingParams{}, none, c);
+        CHECK(c() == d());
+    }
+    {
+        AllowSet c;
+        c.ok = {2, 3};
+        std::vector<float> l{5.0f, 4.0f, 3.0f, 2.0f, 1.0f};
+        CHECK(sample(l, SamplingParams{}, none, rng, &c) == 2);
+        SamplingParams p;
+        p.temperature = 1.0f;
+        for (int i = 0; i < 30; ++i) {
+            std::vector<float> m{5.0f, 4.0f, 3.0f, 2.0f, 1.0f};
+            CHECK(c.ok.count(sample(m, p, none, rng, &c)) == 1);
+        }
+    }
+    {
+        SamplingParams p;
+        p.temperature = 1.0f;
+        for (int i = 0; i < 50; ++i) {
+            std::vector<float> l{0.0f, 40.0f, 0.0f};
+            CHECK(sample(l, p, none, rng) == 1);
+        }
+    }
+    {
+        const std::vector<float> l{1.0f, 2.0f, 3.0f};
+        float clp = 0.0f;
+        std::vector<TokenLogprob> top;
+        logprobs_from(l, 2, 3, clp, top);
+        double psum = 0.0;
+        for (const auto& t : top) psum += std::exp(static_cast<double>(t.logprob));
+        CHECK(std::fabs(psum - 1.0) < 1e-5);
+        CHECK(top.size() == 3 && top[0].token == 2 && top[1].token == 1 && top[2].token == 0);
+        CHECK(std::fabs(top[0].logprob - clp) < 1e-6);
+        for (const auto& t : top) CHECK(t.logprob <= 0.0f);
+        std::vector<TokenLogprob> one;
+        float lp2 = 0.0f;
+        logprobs_from(l, 0, 1, lp2, one);
+        CHECK(one.size() == 1 && one[0].token == 2);
+        CHECK(lp2 < clp);
+        float lp3 = 1.0f;
+        logprobs_from(l, 7, 0, lp3, one);   // chosen outside [0, V): 0
+        CHECK(lp3 == 0.0f && one.empty());
+    }
+    {
+        const std::vector<float> l{0.5f, 2.0f, -1.0f, 2.0f};
+        CHECK(argmax(l) == 1);   // first index of the max
+    }
+    {
+        // JSON mask through allow_mask(): a sampled row only draws allowed tokens
+        std::vector<std::string> pieces{"{", "}", "\"", "a", ":", "1", ",", " ", "x", "]"};
+        auto mb = std::make_shared<const JsonMaskBuilder>(pieces);
+        JsonTokenConstraint c(mb);
+        SamplingParams p;
+        p.temperature = 1.0f;
+        std::string out;
+        for (int step = 0; step < 6; ++step) {
+            std::vector<float> l(12, 0.0f);
+            const TokenId t = sample(l, p, none, rng, &c);
+            CHECK(c.allows(t));
+            c.commit(t);
+            if (t < 10) out += pieces[t];
+        }
+        JsonGrammar g;
+        CHECK(feed_all(g, out));
+    }
+}
+
+int main(int argc, char** argv) {
+    const std::string mode = argc > 1 ? argv[1] : "cpu";
+    try {
+        if (mode == "cpu") {
+            test_grammar();
+            test_mask_builder();
+            test_ngram();
+            test_registry(false);
+        } else if (mode == "gpu") {
+            test_registry(true);
+            test_sampling_gpu();
+        } else {
+            std::fprintf(stderr, "usage: test_host cpu|gpu\n");
+            return 2;
+        }
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "exception: %s\n", e.what());
+        return 1;
+    }
+    std::printf("%s: %d checks passed, %d failed\n", mode.c_str(), g_pass, g_fail);
+    return g_fail == 0 ? 0 : 1;
+}

@@ -12,12 +12,12 @@ from locus_amd import sampler
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared_functions():
+def declared_functions(prefix="lcs_", header="*.h"):
     names = set()
-    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+    for h in glob.glob(os.path.join(ROOT, "include", header)):
         text = open(h).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-        for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(lcs_\w+)\s*\(", text, flags=re.M):
+        for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(" + prefix + r"\w+)\s*\(", text, flags=re.M):
             names.add(m.group(1))
     return sorted(names)
 
@@ -31,6 +31,16 @@ def test_headers_declare_the_abi():
 def test_library_exports_every_declared_symbol():
     lib = sampler.lib()
     for n in declared_functions():
+        assert hasattr(lib, n), n
+
+
+def test_host_library_exports_every_declared_symbol():
+    from locus_amd import host_lib
+    names = declared_functions("lch_", "locus_host.h")
+    assert {"lch_json_new", "lch_json_feed", "lch_mask_build", "lch_ngram_draft",
+            "lch_resolve_sampler_backend"} <= set(names)
+    lib = host_lib.lib()
+    for n in names:
         assert hasattr(lib, n), n
 
 

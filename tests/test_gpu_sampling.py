@@ -223,3 +223,28 @@ def test_hist_capacity_is_reported(sampler):
         assert small.status() & 1
     finally:
         small.close()
+
+
+def test_logprobs_of_given_ids(sampler):
+    """lp_ids: chosen_lp reports logprobs_from(raw, lp_ids[row], n) on both
+    paths (sliced: c2 / c1g, exact: c3), ids outside [0, V) giving 0."""
+    import torch
+    for name, rows in (("c2", 8), ("c3", 6), ("c1g", None)):
+        w = W.make(name, rows=rows, set_index=13)
+        ids = np.random.default_rng(5).integers(-2, w.vocab + 2, size=w.rows).astype(np.int32)
+        ids[0] = -1
+        if w.rows > 1:
+            ids[1] = w.vocab
+        say("lp_ids", name, ids.tolist())
+        d = sampler.upload(w)
+        out = sampler.alloc_out(w.rows, 3, True)
+        lp_ids = torch.from_numpy(ids).cuda()
+        sampler.sample_dev(d, out, n_top=3, want_lp=True, lp_ids=lp_ids)
+        sampler.torch.cuda.synchronize()
+        g = sampler.fetch(out, 3)
+        assert sampler.status() == 0
+        for r in range(w.rows):
+            raw = np.asarray(w.logits[r], dtype=np.float32)
+            lp, tid, tlp, _ = O.logprobs(raw, int(ids[r]), 3)
+            assert abs(float(g["chosen_lp"][r]) - lp) <= LOGPROB_TOL, (name, r, g["chosen_lp"][r], lp)
+            assert np.allclose(g["top_lp"][r], tlp, atol=LOGPROB_TOL, rtol=0)
