@@ -56,6 +56,24 @@ __device__ __forceinline__ float penalize(float l, uint32_t count, const lcs_par
                            p.presence_penalty);
     return fsub(l, sub);
 }
+// penalize() with the divide l / repeat_penalty done as
+// (float)((double)l * RN(1 / repeat_penalty)). For a quotient in the normal
+// float range this is the correctly rounded l / rp: the f64 product is within
+// 2^-52 (relative) of the exact quotient, while no float rounding midpoint
+// lies within 2^-49 of a quotient of two floats (and none equals one). Tiny
+// quotients, where the float grid is coarser, use the exact divide.
+__device__ __forceinline__ float penalize_fast(float l, uint32_t count, const lcs_params& p, double inv_rp) {
+    if (p.repeat_penalty != 1.0f) {
+        if (l > 0.0f) {
+            const double y = (double)l * inv_rp;
+            l = y >= 0x1p-125 ? (float)y : fdiv(l, p.repeat_penalty);
+        } else {
+            l = fmul(l, p.repeat_penalty);
+        }
+    }
+    const float sub = fadd(fmul(p.frequency_penalty, static_cast<float>(count)), p.presence_penalty);
+    return fsub(l, sub);
+}
 __device__ __forceinline__ bool penalties_active(const lcs_params& p) {
     return !(p.repeat_penalty == 1.0f && p.frequency_penalty == 0.0f &&
              p.presence_penalty == 0.0f);

@@ -966,7 +966,8 @@ constexpr float kLog2E = 1.4426950408889634f;
 
 // cross-wave partials of a slice's local phase
 struct SliceLocal {
-    float mraw[kSliceWaves];
+    float lmax[kSliceThreads];   // raw lane maxima
+    float m_s, t_s;              // raw slice max, top-n threshold
     float mpen[kSliceWaves];
     uint32_t ipen[kSliceWaves];
     float rpen[kSliceWaves];
@@ -1416,16 +1417,26 @@ void slice_kernel(SampleArgs a) {
     const bool hany = pen && hn > hstart;
     const bool htwo = hany && hn - hstart > (uint32_t)(NT * HC);
     uint32_t hA[HC], hB[HC];
+    const uint32_t nwin_h = hn - hstart;
     auto load_ids = [&](uint32_t (&h)[HC], uint32_t c0) {
 #pragma unroll
         for (int k = 0; k < HC; ++k) {
             const uint32_t i = hstart + c0 + (uint32_t)k * NT + tid;
-            h[k] = (uint32_t)a.hist_ids[hoff + (i < hn ? i : hn - 1)];
-            h[k] = i < hn ? h[k] : 0xffffffffu;
+            h[k] = (uint32_t)a.hist_ids[hoff + (i < hn ? i : hn - 1)];   // clamped: no branch around the load
+        }
+        // slots past the window are invalid where a wave's slot runs past it
+#pragma unroll
+        for (int k = 0; k < HC; ++k) {
+            if (c0 + (uint32_t)k * NT + (uint32_t)wv * kWave + kWave > nwin_h) {
+                const uint32_t i = c0 + (uint32_t)k * NT + tid;
+                h[k] = i < nwin_h ? h[k] : 0xffffffffu;
+            }
         }
     };
     if (hany) load_ids(hA, 0);
     if (htwo) load_ids(hB, NT * HC);
+    // the slice's logits, one 16-byte load per group (groups past the slice
+    // load the slice's first group and are masked below)
     uint4 raw[NG];
 #pragma unroll
     for (int j = 0; j < NG; ++j) {
@@ -1443,13 +1454,15 @@ void slice_kernel(SampleArgs a) {
     }
     if (tid == 0) { sm.l.ncand = 0; sm.l.nwin = 0; }
 
-    // ---- penalties: LDS table of (penalised ^ raw) bits per slice position,
-    // 0 where no history id falls (sampling.cpp:16-41 applied once per id) ----
+    // ---- penalties, part 1: an LDS table of (penalised ^ raw) bits per slice
+    // position, 0 where no history id falls (sampling.cpp:16-41 applied once per
+    // id): clear it, fetch the raw logits of the in-slice ids, count them; the
+    // lane whose increment finds 0 owns the id ----
+    float rA[HC], rB[HC];
+    uint32_t oA = 0, oB = 0;
     if (hany) {
 #pragma unroll
         for (int i = 0; i < (int)(kSliceMax / 4 / NT); ++i) sm.u.ovr4[i * NT + tid] = make_uint4(0, 0, 0, 0);
-        // raw logits of the in-slice history ids, fetched while the table clears
-        float rA[HC], rB[HC];
         auto gather = [&](const uint32_t (&h)[HC], float (&r)[HC]) {
 #pragma unroll
             for (int k = 0; k < HC; ++k) {
@@ -1460,8 +1473,6 @@ void slice_kernel(SampleArgs a) {
         gather(hA, rA);
         if (htwo) gather(hB, rB);
         __syncthreads();
-        // counts; the lane whose increment finds 0 owns the id
-        uint32_t oA = 0, oB = 0;
         auto count = [&](const uint32_t (&h)[HC], uint32_t& own) {
 #pragma unroll
             for (int k = 0; k < HC; ++k) {
@@ -1471,22 +1482,7 @@ void slice_kernel(SampleArgs a) {
         };
         count(hA, oA);
         if (htwo) count(hB, oB);
-        __syncthreads();
-        auto put = [&](const uint32_t (&h)[HC], const float (&r)[HC], uint32_t own) {
-#pragma unroll
-            for (int k = 0; k < HC; ++k) {
-                if ((own >> k) & 1u) {
-                    const uint32_t d = h[k] - lo;
-                    const float p = penalize(r[k], sm.u.ovr[d], P);
-                    sm.u.ovr[d] = __float_as_uint(p) ^ __float_as_uint(r[k]);
-                }
-            }
-        };
-        put(hA, rA, oA);
-        if (htwo) put(hB, rB, oB);
     }
-    __syncthreads();
-    PROF_MARK(1);
 
     // ---- values; positions past the slice read as -inf ----
     float v[kSliceElems];
@@ -1505,19 +1501,65 @@ void slice_kernel(SampleArgs a) {
     }
     auto eid = [&](int q) { return lo + ((q / G) * NT + tid) * G + (uint32_t)(q % G); };
 
-    // ---- raw statistics: max, top-n candidates, sum of exp ----
+    // ---- raw lane maxima, shared for the slice's statistics ----
     float lm = NEG;
 #pragma unroll
     for (int q = 0; q < kSliceElems; ++q) lm = fmaxf(lm, v[q]);
-    const float Mw = wave_max(lm);
-    if (ntop) {
-        // the ntop-th largest lane max bounds the wave's top-n from below
-        float cur = lm, t = NEG;
-        for (uint32_t r = 0; r < ntop; ++r) {
-            t = wave_max(cur);
-            const uint64_t hit = ballot(cur == t);
-            if (lane == __builtin_ctzll(hit)) cur = NEG;
+    sm.l.lmax[tid] = lm;
+    __syncthreads();
+    float Ms;   // raw slice max
+    {
+        float m4 = sm.l.lmax[lane];
+#pragma unroll
+        for (int c = 1; c < kSliceWaves; ++c) m4 = fmaxf(m4, sm.l.lmax[lane + c * kWave]);
+        Ms = wave_max(m4);
+    }
+    // ---- penalties, part 2: each owner writes its id's word; one wave finds
+    // the ntop-th largest lane maximum, a lower bound of the slice's top-n ----
+    if (hany || ntop) {
+        if (hany) {
+            const double inv_rp = 1.0 / (double)P.repeat_penalty;
+            auto put = [&](const uint32_t (&h)[HC], const float (&r)[HC], uint32_t own) {
+#pragma unroll
+                for (int k = 0; k < HC; ++k) {
+                    if ((own >> k) & 1u) {
+                        const uint32_t d = h[k] - lo;
+                        const float p = penalize_fast(r[k], sm.u.ovr[d], P, inv_rp);
+                        sm.u.ovr[d] = __float_as_uint(p) ^ __float_as_uint(r[k]);
+                    }
+                }
+            };
+            put(hA, rA, oA);
+            if (htwo) put(hB, rB, oB);
         }
+        if (ntop && wv == kSliceWaves - 1) {
+            float c4[kSliceWaves];
+#pragma unroll
+            for (int c = 0; c < kSliceWaves; ++c) c4[c] = sm.l.lmax[lane + c * kWave];
+            float t = NEG;
+            for (uint32_t r = 0; r < ntop; ++r) {
+                float m = c4[0];
+#pragma unroll
+                for (int c = 1; c < kSliceWaves; ++c) m = fmaxf(m, c4[c]);
+                t = wave_max(m);
+                const uint64_t hit = ballot(m == t);
+                if (lane == __builtin_ctzll(hit)) {
+                    bool done = false;
+#pragma unroll
+                    for (int c = 0; c < kSliceWaves; ++c) {
+                        if (!done && c4[c] == t) { c4[c] = NEG; done = true; }
+                    }
+                }
+            }
+            if (lane == 0) sm.l.t_s = t;
+        }
+        __syncthreads();
+    }
+    PROF_MARK(1);
+
+    // ---- top-n candidates: elements >= the threshold, in the few lanes that hold one ----
+    if (ntop) {
+        const float t = sm.l.t_s;
         if (lm >= t) {
 #pragma unroll
             for (int q = 0; q < kSliceElems; ++q) {
@@ -1531,9 +1573,10 @@ void slice_kernel(SampleArgs a) {
             }
         }
     }
+    // ---- raw sum of exp against the slice max ----
     double sw = 0.0;
-    if (want_lp && Mw != NEG) {
-        const float b = -Mw * kLog2E;
+    if (want_lp && Ms != NEG) {
+        const float b = -Ms * kLog2E;
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < NG; ++j) {
@@ -1548,7 +1591,7 @@ void slice_kernel(SampleArgs a) {
         }
         sw = wave_sum((double)s);
     }
-    if (lane == 0) { sm.l.mraw[wv] = Mw; sm.l.sraw[wv] = sw; }
+    if (lane == 0) sm.l.sraw[wv] = sw;
     PROF_MARK(2);
 
     // ---- penalised values ----
@@ -1667,10 +1710,8 @@ void slice_kernel(SampleArgs a) {
     if (wv == 0) {
         const bool lw = lane < kSliceWaves;
         const int wl = lw ? lane : 0;
-        const float mrw = lw ? sm.l.mraw[wl] : NEG;
-        const float mrs = wave_max(mrw);
-        const double ses = wave_sum(lw && want_lp && mrw != NEG
-                                        ? sm.l.sraw[wl] * (double)fast_exp2((mrw - mrs) * kLog2E) : 0.0);
+        const float mrs = Ms;
+        const double ses = wave_sum(lw && want_lp ? sm.l.sraw[wl] : 0.0);
         float ma = lw ? sm.l.mpen[wl] : NEG;
         uint32_t ia = lw ? sm.l.ipen[wl] : kNoIdx;
         float ra = lw ? sm.l.rpen[wl] : 0.0f;
