@@ -49,17 +49,22 @@ constexpr uint32_t kFbBins = 512;
 constexpr uint32_t kFbCap = 512;
 constexpr uint32_t kFbHistCap = kFastHistMax;
 
-enum RowMode : uint32_t { kModeGreedy = 1, kModeWindow = 2, kModeGeneral = 4 };
+enum RowMode : uint32_t { kModeGreedy = 1, kModeWindow = 2, kModeGeneral = 4, kModeTopK = 8 };
+constexpr uint32_t kTopKMax = 64;         // top_k served by the sliced path
+constexpr uint32_t kTopKMerge = 1024;     // slices x top_k entries the finalize merges
 
 // Which implementation path a row takes; pure function of its parameters.
 __host__ __device__ inline uint32_t row_mode(const lcs_params& p, bool masked, uint32_t vocab) {
     if (p.temperature <= 0.0f) return kModeGreedy;
     const bool pen = !(p.repeat_penalty == 1.0f && p.frequency_penalty == 0.0f &&
                        p.presence_penalty == 0.0f);
+    const bool pen_ok = !pen || p.repeat_last_n <= kFastHistMax;
     const bool topk = p.top_k > 0 && p.top_k < vocab;
-    if (p.min_p > 0.0f && !masked && !topk && (!pen || p.repeat_last_n <= kFastHistMax)) {
-        return kModeWindow;
+    const uint32_t slices = (vocab + kSliceMax - 1) / kSliceMax;
+    if (topk && !masked && pen_ok && p.top_k <= kTopKMax && p.top_k * slices <= kTopKMerge) {
+        return kModeTopK;
     }
+    if (p.min_p > 0.0f && !masked && !topk && pen_ok) return kModeWindow;
     return kModeGeneral;
 }
 

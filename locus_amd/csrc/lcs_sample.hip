@@ -988,12 +988,14 @@ struct SliceLocal {
 };
 // the row's finalize (two waves of the last-arriving workgroup)
 struct SliceFin {
-    uint64_t top[kWave * kTopMax];
+    uint64_t top[kMaxSlices * kTopMax];
     uint64_t ent[kRowWin];
     float entraw[kRowWin];
     uint64_t sorted[kRowWin];
     float sortedraw[kRowWin];
     double sw[kRowWin];
+    uint64_t tkey[kTopKMerge];   // top-k rows: each slice's list, rank order
+    float traw[kTopKMerge];
 };
 struct SliceSmem {
     union {
@@ -1089,13 +1091,13 @@ __device__ __forceinline__ bool fin_logprobs(const SampleArgs& a, uint32_t row, 
     if (ballot(mine && (flags & rec::kFlagCandOverflow))) return true;
 #pragma unroll
     for (int j = 0; j < (int)kTopMax; ++j) {
-        if ((uint32_t)j < ntop) sm.u.f.top[lane * kTopMax + j] = (mine && (uint32_t)j < nts) ? tk[j] : ~0ull;
+        if (mine && (uint32_t)j < ntop) sm.u.f.top[lane * kTopMax + j] = (uint32_t)j < nts ? tk[j] : ~0ull;
     }
     wave_sync();
     uint32_t p = 0;
     uint64_t myk = ~0ull;
     for (uint32_t r = 0; r < ntop; ++r) {
-        const uint64_t head = p < ntop ? sm.u.f.top[lane * kTopMax + p] : ~0ull;
+        const uint64_t head = mine && p < ntop ? sm.u.f.top[lane * kTopMax + p] : ~0ull;
         const uint64_t best = wave_min_u64(head);
         if (head == best && best != ~0ull) ++p;
         if ((uint32_t)lane == r) myk = best;
@@ -1157,6 +1159,8 @@ __device__ __forceinline__ bool fin_gather(const SampleArgs& a, uint32_t row, ui
     const uint64_t* my = recs + (uint64_t)(mine ? lane : 0) * rec::kWords64;
     const float NEG = -__builtin_huge_valf();
     const bool stoch = mode == kModeWindow;
+    const bool topk = mode == kModeTopK;
+    (void)topk;
 
     uint64_t h[rec::kHdr];
 #pragma unroll
@@ -1179,7 +1183,7 @@ __device__ __forceinline__ bool fin_gather(const SampleArgs& a, uint32_t row, ui
     const uint32_t i_msk = mine ? (uint32_t)(h[3] >> 32) : kNoIdx;
     const uint32_t n_allowed = mine ? (uint32_t)h[4] : 0u;
 
-    if (!stoch) {
+    if (mode == kModeGreedy) {
         const uint32_t tot_allowed = wave_sum_u(n_allowed);
         const bool use_mask = masked && tot_allowed > 0;
         float bv = use_mask ? m_msk : m_pen;
@@ -1199,6 +1203,57 @@ __device__ __forceinline__ bool fin_gather(const SampleArgs& a, uint32_t row, ui
                 dg.path = LCS_PATH_GREEDY;
                 a.diag[row] = dg;
             }
+        }
+        return false;
+    }
+
+    if (mode == kModeTopK) {
+        // the row's top-k (sampling.cpp:87-97): a k-way merge of the slices'
+        // rank-ordered top-k lists, then the exact normaliser over those k
+        if (ballot(mine && (flags & rec::kFlagWinLost))) return true;
+        const uint32_t K = P.top_k;
+        const uint32_t ns = min(n_win, K);
+        for (uint32_t j0 = 0; j0 < K; j0 += 8) {
+            uint64_t kk[8];
+            uint32_t rr[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t j = j0 + u;
+                const bool ok = mine && j < ns;
+                kk[u] = ok ? ld_dev_u64(my + rec::kWin + j) : ~0ull;
+                rr[u] = ok ? (uint32_t)ld_dev_u64(my + rec::kWinRaw + j) : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t j = j0 + u;
+                if (mine && j < ns) {
+                    sm.u.f.tkey[lane * K + j] = kk[u];
+                    sm.u.f.traw[lane * K + j] = __uint_as_float(rr[u]);
+                }
+            }
+        }
+        wave_sync();
+        const uint32_t Ke = min(K, wave_sum_u(ns));
+        uint32_t p = 0;
+        for (uint32_t r = 0; r < Ke; ++r) {
+            const uint64_t head = (mine && p < ns) ? sm.u.f.tkey[lane * K + p] : ~0ull;
+            const uint64_t best = wave_min_u64(head);
+            if (head == best) {
+                sm.u.f.sorted[r] = best;
+                sm.u.f.sortedraw[r] = sm.u.f.traw[lane * K + p];
+                ++p;
+            }
+        }
+        wave_sync();
+        const float maxl = rank_val(sm.u.f.sorted[0]);
+        const float inv_t = fdiv(1.0f, P.temperature);
+        const double w = (uint32_t)lane < Ke ? exp((double)tempered(rank_val(sm.u.f.sorted[lane]), maxl, inv_t)) : 0.0;
+        const double Sf = wave_sum(w);
+        if (lane == 0) {
+            sm.l.fin_S = Sf;
+            sm.l.fin_rel = 0x1p-45;   // tree vs sequential summation of at most 64 terms
+            sm.l.fin_L0 = Ke;
+            sm.l.fin_maxl = maxl;
         }
         return false;
     }
@@ -1275,7 +1330,7 @@ __device__ __forceinline__ bool fin_gather(const SampleArgs& a, uint32_t row, ui
 // entries at a time; weights exp((double)((p - maxl) * inv_t)) as the
 // reference's. Returns true when a top-p / min-p decision lies within the
 // normaliser's error bound.
-__device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, SliceSmem& sm) {
+__device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, SliceSmem& sm, uint32_t path) {
     const int lane = lane_id();
     PROF_WMARK(12);
     const lcs_params P = a.params[row];
@@ -1364,7 +1419,7 @@ __device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, Sl
             lcs_row_diag dg{};
             dg.n_cand = a.vocab; dg.keep = keep; dg.maxl = maxl;
             dg.boundary = rank_val(sm.u.f.sorted[keep - 1]);
-            dg.path = LCS_PATH_WINDOW; dg.sum = Sf; dg.kept_sum = kept_sum;
+            dg.path = path; dg.sum = Sf; dg.kept_sum = kept_sum;
             a.diag[row] = dg;
         }
     }
@@ -1405,6 +1460,8 @@ void slice_kernel(SampleArgs a) {
     uint64_t* myrec = reinterpret_cast<uint64_t*>(a.recs) + ((uint64_t)row * S + slice) * rec::kWords64;
     const float NEG = -__builtin_huge_valf();
     const bool stoch = mode == kModeWindow;
+    const bool topk = mode == kModeTopK;
+    const bool wins = stoch || topk;   // rows that publish a ranked entry list
 
     // ---- loads: history window ids first, then the slice's logits ----
     const bool pen = penalties_active(P) && a.hist_off != nullptr;
@@ -1701,6 +1758,47 @@ void slice_kernel(SampleArgs a) {
         const double bsum = wave_sum((double)bs);
         const double btsum = wave_sum((double)bt);
         if (lane == 0) { sm.l.bulk[wv] = bsum; sm.l.bterm[wv] = btsum; }
+    } else if (topk) {
+        // the slice's top-k by penalised value (sampling.cpp:87-97): elements
+        // >= the k-th largest lane maximum, found by one wave over all 256
+        sm.l.lmax[tid] = lpm;
+        __syncthreads();
+        if (wv == kSliceWaves - 1) {
+            float c4[kSliceWaves];
+#pragma unroll
+            for (int c = 0; c < kSliceWaves; ++c) c4[c] = sm.l.lmax[lane + c * kWave];
+            float t = NEG;
+            for (uint32_t r = 0; r < P.top_k; ++r) {
+                float m = c4[0];
+#pragma unroll
+                for (int c = 1; c < kSliceWaves; ++c) m = fmaxf(m, c4[c]);
+                t = wave_max(m);
+                const uint64_t hit = ballot(m == t);
+                if (lane == __builtin_ctzll(hit)) {
+                    bool done = false;
+#pragma unroll
+                    for (int c = 0; c < kSliceWaves; ++c) {
+                        if (!done && c4[c] == t) { c4[c] = NEG; done = true; }
+                    }
+                }
+            }
+            if (lane == 0) sm.l.t_s = t;
+        }
+        __syncthreads();
+        const float t = sm.l.t_s;
+        if (lpm >= t) {
+#pragma unroll
+            for (int q = 0; q < kSliceElems; ++q) {
+                if (v[q] >= t) {
+                    const uint32_t e = eid(q);
+                    if (e < hi) {
+                        const uint32_t s = atomicAdd(&sm.l.nwin, 1u);
+                        if (s < kWinLds) sm.l.wk[s] = rank_key(v[q], e);
+                    }
+                }
+            }
+        }
+        if (lane == 0) { sm.l.bulk[wv] = 0.0; sm.l.bterm[wv] = 0.0; }
     }
     PROF_MARK(4);
     __syncthreads();
@@ -1737,7 +1835,7 @@ void slice_kernel(SampleArgs a) {
                 na = wave_sum_u(lw ? sm.l.nall[wl] : 0u);
             }
         }
-        const uint32_t nwr = stoch ? sm.l.nwin : 0u;
+        const uint32_t nwr = wins ? sm.l.nwin : 0u;
         const uint32_t nw = min(min(nwr, kWinLds), kWinCap);
         const uint32_t nts = min(ntop, len);
         const uint32_t fl = (nwr > kWinCap ? rec::kFlagWinTrunc : 0u) |
@@ -1770,7 +1868,7 @@ void slice_kernel(SampleArgs a) {
                 if (e < ncc && rk[c] < nts) st_dev_u64(myrec + rec::kTop + rk[c], k[c]);
             }
         }
-    } else if (wv == 2 && stoch) {
+    } else if (wv == 2 && wins) {
         // window entries: the top kWinCap by rank, in ascending rank order,
         // each with its raw logit (the value itself unless penalised)
         const uint32_t nwl = min(sm.l.nwin, kWinLds);
@@ -1815,8 +1913,8 @@ void slice_kernel(SampleArgs a) {
     }
     if (fb && lane == 0) sm.l.fin_fb = 1u;
     __syncthreads();
-    if (wv == 0 && stoch && !sm.l.fin_fb) {
-        fb = fin_decide(a, row, sm);
+    if (wv == 0 && wins && !sm.l.fin_fb) {
+        fb = fin_decide(a, row, sm, topk ? LCS_PATH_TOPK : LCS_PATH_WINDOW);
         if (fb && lane == 0) sm.l.fin_fb = 1u;
     }
     __syncthreads();

@@ -248,3 +248,26 @@ def test_logprobs_of_given_ids(sampler):
             lp, tid, tlp, _ = O.logprobs(raw, int(ids[r]), 3)
             assert abs(float(g["chosen_lp"][r]) - lp) <= LOGPROB_TOL, (name, r, g["chosen_lp"][r], lp)
             assert np.allclose(g["top_lp"][r], tlp, atol=LOGPROB_TOL, rtol=0)
+
+
+def test_topk_rows_on_the_sliced_path(sampler):
+    """top_k <= 64 rows run on the sliced exact top-k path (path 5), with and
+    without penalties, top-p and min-p; top_k 65 stays on the exact path."""
+    base = W.make("c2", rows=12, set_index=17)
+    p = base.params.copy()
+    ks = [1, 2, 5, 17, 40, 64, 40, 40, 64, 8, 65, 33]
+    for r, k in enumerate(ks):
+        p["top_k"][r] = k
+        p["min_p"][r] = 0.0 if r % 3 else 0.05
+        p["top_p"][r] = 1.0 if r % 4 == 1 else 0.9
+        p["temperature"][r] = [0.7, 1.0, 1.5][r % 3]
+    p["repeat_penalty"][6] = 1.0
+    p["frequency_penalty"][6] = 0.0
+    p["presence_penalty"][6] = 0.0
+    w = W.Workload("topk", base.rows, base.vocab, "f32", base.logits, p, base.seeds, base.u,
+                   base.hist_off, base.hist_ids, None, 5, True)
+    g = run(sampler, w)
+    compare(w, g, O.sample_batch(w, threads=8), "topk", expect_paths={4, 5})
+    paths = g["diag"]["path"]
+    assert (paths[[i for i, k in enumerate(ks) if k <= 64]] == 5).all(), paths.tolist()
+    assert paths[ks.index(65)] == 4
