@@ -226,6 +226,9 @@ int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
     a.status = c->status;
     a.slices = slices_for(b->vocab);
     a.slice_len = slice_len_for(b->vocab);
+    // every row known to run sliced: the slice kernel may start its logit
+    // loads before it has the row's parameters
+    a.all_sliced = (b->params_host && !any_general) ? 1u : 0u;
 
     DeviceGuard g(c->device);
     hipStream_t st = static_cast<hipStream_t>(stream);

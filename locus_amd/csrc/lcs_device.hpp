@@ -125,6 +125,17 @@ __device__ __forceinline__ uint32_t wave_sum_u(uint32_t v) {
     LCS_WAVE_REDUCE_32(uint32_t, v, 0u, u_add);
     return v;
 }
+__device__ __forceinline__ float f_add(float a, float b) { return a + b; }
+__device__ __forceinline__ float wave_sum_f(float v) {
+    LCS_WAVE_REDUCE_32(float, v, 0.0f, f_add);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t u_min(uint32_t a, uint32_t b) { return a < b ? a : b; }
+__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
+    LCS_WAVE_REDUCE_32(uint32_t, v, 0xffffffffu, u_min);
+    return v;
+}
 
 // 64-bit payloads move as two 32-bit DPP halves with the same control.
 template <int CTRL, int ROWS = 0xF>
@@ -198,6 +209,20 @@ __device__ __forceinline__ uint32_t wave_scan_incl_u(uint32_t v) {
     return v;
 }
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+// The n-th largest of the wave's 4 x 64 keys k[c] (1 <= n <= 256): the
+// largest T with at least n keys >= T, built bit by bit from the top with
+// ballot counts. Wave-uniform result.
+__device__ __forceinline__ uint32_t wave_kth_largest4(const uint32_t (&k)[4], uint32_t n) {
+    uint32_t T = 0;
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t Tb = T | (1u << b);
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) cnt += (uint32_t)__builtin_popcountll(__ballot(k[c] >= Tb));
+        if (cnt >= n) T = Tb;
+    }
+    return T;
+}
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
 // Orders LDS traffic between lanes of one wave (no cross-wave barrier).
 __device__ __forceinline__ void wave_sync() {
@@ -372,6 +397,29 @@ __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected
     }
     __syncthreads();
     return *flag_lds != 0;
+}
+
+// ------------------------------------------------------- scalar loads ----
+// Read-only per-row words through the scalar cache (SMEM): waiting for them
+// does not wait for the vector loads in flight. For data the kernel never
+// writes.
+template <class T>
+__device__ __forceinline__ T scalar_load(const T* p) {
+    static_assert(sizeof(T) % 4 == 0, "dword-sized words");
+    typedef __attribute__((address_space(4))) const uint32_t CWord;
+    const CWord* q = (const CWord*)p;
+    uint32_t w[sizeof(T) / 4];
+#pragma unroll
+    for (uint32_t i = 0; i < sizeof(T) / 4; ++i) w[i] = q[i];
+    T r;
+    __builtin_memcpy(&r, w, sizeof(T));
+    return r;
+}
+// One byte, from the aligned dword that holds it (never crosses a page).
+__device__ __forceinline__ uint32_t scalar_load_u8(const uint8_t* p) {
+    const uintptr_t u = reinterpret_cast<uintptr_t>(p);
+    const uint32_t w = scalar_load(reinterpret_cast<const uint32_t*>(u & ~(uintptr_t)3));
+    return (w >> ((u & 3u) * 8u)) & 0xffu;
 }
 
 // ------------------------------------------------------- vector loads ----

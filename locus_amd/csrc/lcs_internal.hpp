@@ -94,6 +94,8 @@ struct SampleArgs {
     uint32_t* status;        // device error word (sticky bits)
     uint32_t slices;         // workgroups per row on the sliced path
     uint32_t slice_len;      // elements per slice (multiple of 8)
+    uint32_t all_sliced;     // 1: the host saw every row take a sliced mode
+    uint32_t pad_;
 };
 
 struct VerifyArgs {

@@ -914,6 +914,15 @@ write_back:
 // Copies the launch arguments into LDS for the out-of-line exact path, one
 // dword per lane straight from the kernel argument segment (a reference to
 // the by-value argument would give every lane a private copy in scratch).
+// Thread-0 copy of the kernel arguments into LDS; uniform addresses, so the
+// reads are scalar loads of the kernarg segment (no private copy of the
+// by-value argument).
+__device__ __forceinline__ void stash_args(SampleArgs* dst) {
+    const uint32_t* src = (const uint32_t*)__builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t* d = reinterpret_cast<uint32_t*>(dst);
+#pragma unroll
+    for (uint32_t i = 0; i < sizeof(SampleArgs) / 4; ++i) d[i] = src[i];
+}
 __device__ __forceinline__ void stage_args(SampleArgs* dst) {
     static_assert(sizeof(SampleArgs) % 4 == 0 && sizeof(SampleArgs) / 4 <= 64, "args size");
     const uint32_t* src = (const uint32_t*)__builtin_amdgcn_kernarg_segment_ptr();
@@ -960,7 +969,6 @@ __device__ uint64_t g_prof[16384 * 32];
 constexpr int kSliceWaves = kSliceThreads / kWave;
 constexpr uint32_t kCandCap = 128;   // top-n candidates one slice can hold
 constexpr uint32_t kWinLds = 256;    // window entries one slice can rank
-constexpr uint32_t kSpecWin = 8;     // window entries fetched with each slice header
 constexpr uint32_t kRowWin = 4 * kWave;  // row-window entries the finalize can rank
 constexpr float kLog2E = 1.4426950408889634f;
 
@@ -981,14 +989,16 @@ struct SliceLocal {
     uint32_t ncand, nwin, last;
     // finalize hand-off between its waves
     double log_z, fin_S, fin_rel;
+    double win_delta;                    // T (ln(1/min_p) + 1e-3), sampled rows
     float chosen_raw, fin_maxl;
     uint32_t fin_fb, fin_L0;
     uint64_t ck[kCandCap];               // top-n candidates (rank keys)
     uint64_t wk[kWinLds];                // window entries (rank keys)
+    SampleArgs args;                     // the kernel arguments, for the finalize
 };
-// the row's finalize (two waves of the last-arriving workgroup)
+// the row's finalize (the last-arriving workgroup)
 struct SliceFin {
-    uint64_t top[kMaxSlices * kTopMax];
+    uint64_t top[kMaxSlices * kTopMax];     // the slices' top-n lists
     uint64_t ent[kRowWin];
     float entraw[kRowWin];
     uint64_t sorted[kRowWin];
@@ -1006,6 +1016,9 @@ struct SliceSmem {
     } u;
     SliceLocal l;
 };
+// The slice kernels' LDS, at file scope so that the finalize (a separate
+// function) addresses it directly.
+__shared__ SliceSmem g_slice;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 // The next float below a finite x.
@@ -1058,22 +1071,48 @@ __device__ __forceinline__ void lds_rank4(const uint64_t* keys, uint32_t n, uint
     }
 }
 
-// ---- the row's finalize, spread over the waves of the last-arriving workgroup ----
-// wave 0: headers, the row window gathered and ranked (greedy rows finish here)
-// wave 1: raw log-normaliser and the top-n merge (logprob rows)
-// wave 2: the sampling normaliser S and its error bound
-// then, after one barrier, wave 0 walks top-p / min-p / the draw.
+// ---- the row's finalize, by the last-arriving workgroup ----
+// Each wave fetches what it needs from the slice records in one round trip
+// (lane s reads slice s), then
+//   wave 0: greedy rows, the argmax; sampled rows, the row window (entries at
+//           or above the row threshold) compacted, ranked and weighed; top-k
+//           rows, the k-way merge of the lists waves 2-3 fetched;
+//   wave 1: the raw log-normaliser and the top-n merge (logprob rows);
+//   wave 2: the sampling normaliser and its error bound (sampled rows);
+// and after one barrier wave 0 walks top-p / min-p / the draw. The finalize
+// is a separate function so that its live values do not crowd the slices'
+// main phase; its LDS is the file-scope g_slice.
+constexpr uint32_t kSpecWin = 16;   // window entries fetched with each slice header
 
-// Raw log-normaliser over the slices and the k-way merge of their top-n lists
-// (logprobs_from, sampling.cpp:150-190). Returns true when a slice's candidate
-// list overflowed.
-__device__ __forceinline__ bool fin_logprobs(const SampleArgs& a, uint32_t row, SliceSmem& sm) {
+__device__ __forceinline__ float next_up(float x) {
+    const uint32_t b = __float_as_uint(x);
+    if (x == 0.0f) return __uint_as_float(1u);
+    return __uint_as_float(x > 0.0f ? b + 1u : b - 1u);
+}
+
+// The kernel arguments thread 0 staged in LDS, read back as wave-uniform values.
+__device__ __forceinline__ SampleArgs uniform_args(const SampleArgs& s) {
+    constexpr uint32_t N = sizeof(SampleArgs) / 4;
+    static_assert(sizeof(SampleArgs) % 4 == 0, "args size");
+    uint32_t w[N];
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(&s);
+#pragma unroll
+    for (uint32_t i = 0; i < N; ++i) w[i] = (uint32_t)__builtin_amdgcn_readfirstlane((int)src[i]);
+    SampleArgs r;
+    __builtin_memcpy(&r, w, sizeof(r));
+    return r;
+}
+
+
+// Raw log-normaliser over the slices and the k-way merge of their top-n
+// lists (logprobs_from, sampling.cpp:150-190). Returns true when a slice's
+// candidate list overflowed.
+__device__ __forceinline__ bool fin_logprobs(const SampleArgs& a, const uint64_t* recs, uint32_t row, uint32_t ntop,
+                                             SliceSmem& sm) {
     const int lane = lane_id();
     const uint32_t S = a.slices;
-    const uint32_t ntop = min(a.n_top, kTopMax);
-    const uint64_t* recs = reinterpret_cast<const uint64_t*>(a.recs) + (uint64_t)row * S * rec::kWords64;
     const bool mine = (uint32_t)lane < S;
-    const uint64_t* my = recs + (uint64_t)(mine ? lane : 0) * rec::kWords64;
+    const uint64_t* my = recs + (mine ? lane : 0) * rec::kWords64;
     const float NEG = -__builtin_huge_valf();
     const uint64_t h0 = ld_dev_u64(my + 0), h1 = ld_dev_u64(my + 1), h4 = ld_dev_u64(my + 4);
     uint64_t tk[kTopMax];
@@ -1094,12 +1133,19 @@ __device__ __forceinline__ bool fin_logprobs(const SampleArgs& a, uint32_t row, 
         if (mine && (uint32_t)j < ntop) sm.u.f.top[lane * kTopMax + j] = (uint32_t)j < nts ? tk[j] : ~0ull;
     }
     wave_sync();
+    // merge on the value half of the rank keys; among equal values the
+    // lowest lane holds the lowest index (slices are in index order)
     uint32_t p = 0;
     uint64_t myk = ~0ull;
     for (uint32_t r = 0; r < ntop; ++r) {
-        const uint64_t head = mine && p < ntop ? sm.u.f.top[lane * kTopMax + p] : ~0ull;
-        const uint64_t best = wave_min_u64(head);
-        if (head == best && best != ~0ull) ++p;
+        const uint64_t head = mine && p < nts ? sm.u.f.top[lane * kTopMax + p] : ~0ull;
+        const uint32_t hk = (uint32_t)(head >> 32);
+        const uint32_t mk = wave_min_u(hk);
+        const uint64_t hit = ballot(head != ~0ull && hk == mk);
+        if (!hit) break;
+        const int wl = __builtin_ctzll(hit);
+        const uint64_t best = readlane_u64(head, wl);
+        if (lane == wl) ++p;
         if ((uint32_t)lane == r) myk = best;
     }
     if ((uint32_t)lane < ntop) {
@@ -1112,24 +1158,22 @@ __device__ __forceinline__ bool fin_logprobs(const SampleArgs& a, uint32_t row, 
 
 // The sampling normaliser: slice bulks rescaled to the row max, with the
 // bound that certifies top-p decisions (sampled rows).
-__device__ __forceinline__ void fin_norm(const SampleArgs& a, uint32_t row, SliceSmem& sm) {
+__device__ __forceinline__ void fin_norm(const SampleArgs& a, const uint64_t* recs, SliceSmem& sm, float inv_t) {
     const int lane = lane_id();
-    const uint32_t S = a.slices;
-    const lcs_params P = a.params[row];
-    const uint64_t* recs = reinterpret_cast<const uint64_t*>(a.recs) + (uint64_t)row * S * rec::kWords64;
-    const bool mine = (uint32_t)lane < S;
-    const uint64_t* my = recs + (uint64_t)(mine ? lane : 0) * rec::kWords64;
+    const bool mine = (uint32_t)lane < a.slices;
+    const uint64_t* my = recs + (mine ? lane : 0) * rec::kWords64;
     const float NEG = -__builtin_huge_valf();
     const uint64_t h2 = ld_dev_u64(my + 2), h5 = ld_dev_u64(my + 5), h6 = ld_dev_u64(my + 6);
     const float m_pen = mine ? __uint_as_float((uint32_t)h2) : NEG;
     const double bulk = mine ? bits_d(h5) : 0.0;
     const double berr = mine ? bits_d(h6) : 0.0;
-    const float inv_t = fdiv(1.0f, P.temperature);
     const float maxl = wave_max(m_pen);
     const double d_s = mine ? ((double)m_pen - (double)maxl) * (double)inv_t : 0.0;
     const double es = mine && m_pen != NEG ? exp(d_s) : 0.0;
     const double Sf = wave_sum(es * bulk);
-    const double eps = wave_sum(es * (berr + fabs(d_s) * 0x1p-50 * bulk));
+    // the reference rounds (p - maxl) * inv_t in float: relative 2^-23 of the
+    // slice-to-row part |d_s| as well as of each term's own offset
+    const double eps = wave_sum(es * (berr + fabs(d_s) * bulk * 0x1p-22));
     if (lane == 0) {
         sm.l.fin_S = Sf;
         sm.l.fin_rel = 2.0 * eps / Sf + 0x1p-50;
@@ -1137,135 +1181,74 @@ __device__ __forceinline__ void fin_norm(const SampleArgs& a, uint32_t row, Slic
     PROF_WMARK(22);
 }
 
-__device__ __forceinline__ float next_up(float x) {
-    const uint32_t b = __float_as_uint(x);
-    if (x == 0.0f) return __uint_as_float(1u);
-    return __uint_as_float(x > 0.0f ? b + 1u : b - 1u);
-}
-
-// Headers and the row window. Greedy rows: the argmax over the slices
-// (sampling.cpp:52-67), written out here. Sampled rows: every entry with
-// p >= maxl - delta gathered from the slices' rank-ordered lists and ranked in
-// LDS (sorted / sortedraw, count in fin_L0). Returns true when the row needs
-// the exact single-workgroup path (a slice dropped window entries, or the
-// row window holds more than kRowWin entries).
-__device__ __forceinline__ bool fin_gather(const SampleArgs& a, uint32_t row, uint32_t mode, SliceSmem& sm) {
+// Greedy rows: the argmax over the slices (sampling.cpp:52-67), written out.
+__device__ __forceinline__ void fin_greedy(const SampleArgs& a, const uint64_t* recs, uint32_t row, bool masked,
+                                           SliceSmem& sm) {
     const int lane = lane_id();
     const uint32_t S = a.slices, V = a.vocab;
-    const lcs_params P = a.params[row];
-    const bool masked = a.mask != nullptr && (a.has_mask == nullptr || a.has_mask[row] != 0);
-    const uint64_t* recs = reinterpret_cast<const uint64_t*>(a.recs) + (uint64_t)row * S * rec::kWords64;
     const bool mine = (uint32_t)lane < S;
-    const uint64_t* my = recs + (uint64_t)(mine ? lane : 0) * rec::kWords64;
+    const uint64_t* my = recs + (mine ? lane : 0) * rec::kWords64;
     const float NEG = -__builtin_huge_valf();
-    const bool stoch = mode == kModeWindow;
-    const bool topk = mode == kModeTopK;
-    (void)topk;
+    const uint64_t h2 = ld_dev_u64(my + 2), h3 = ld_dev_u64(my + 3), h4 = ld_dev_u64(my + 4), h7 = ld_dev_u64(my + 7);
+    PROF_WMARK(7);
+    const uint32_t n_allowed = mine ? (uint32_t)h4 : 0u;
+    const uint32_t tot_allowed = wave_sum_u(n_allowed);
+    const bool use_mask = masked && tot_allowed > 0;
+    const uint64_t hb = use_mask ? h3 : h2;
+    float bv = mine ? __uint_as_float((uint32_t)hb) : NEG;
+    uint32_t bi = mine ? (uint32_t)(hb >> 32) : kNoIdx;
+    float braw = use_mask ? __uint_as_float((uint32_t)(h7 >> 32)) : __uint_as_float((uint32_t)h7);
+    if (bi >= V) { bv = NEG; bi = kNoIdx; }
+    const uint32_t bi0 = bi;
+    wave_argmax(bv, bi);
+    const uint64_t own = ballot(bi0 == bi && bi < V);
+    braw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(braw), own ? __builtin_ctzll(own) : 0));
+    if (lane == 0) {
+        a.ids[row] = (int32_t)bi;
+        sm.l.chosen_raw = braw;
+        if (a.diag) {
+            lcs_row_diag dg{};
+            dg.n_cand = use_mask ? tot_allowed : V; dg.maxl = bv; dg.boundary = bv;
+            dg.path = LCS_PATH_GREEDY;
+            a.diag[row] = dg;
+        }
+    }
+}
 
-    uint64_t h[rec::kHdr];
-#pragma unroll
-    for (int k = 0; k < (int)rec::kHdr; ++k) h[k] = ld_dev_u64(my + k);
+// Sampled rows: every entry with p >= maxl - delta, gathered from the slices'
+// rank-ordered lists, ranked into sorted / sortedraw with its weight
+// exp((double)((p - maxl) * inv_t)) in sw. Returns true when the row needs
+// the exact single-workgroup path (a slice dropped window entries, or the row
+// window holds more than kRowWin).
+__device__ __forceinline__ bool fin_window(const SampleArgs& a, const uint64_t* recs, const lcs_params& P,
+                                           SliceSmem& sm, float inv_t) {
+    const int lane = lane_id();
+    const uint32_t S = a.slices;
+    const bool mine = (uint32_t)lane < S;
+    const uint64_t* my = recs + (mine ? lane : 0) * rec::kWords64;
+    const float NEG = -__builtin_huge_valf();
+    const uint64_t h0 = ld_dev_u64(my + 0), h2 = ld_dev_u64(my + 2);
     uint64_t wk[kSpecWin];
     uint32_t wr[kSpecWin];
-    if (stoch) {
 #pragma unroll
-        for (int j = 0; j < (int)kSpecWin; ++j) {
-            wk[j] = ld_dev_u64(my + rec::kWin + j);
-            wr[j] = (uint32_t)ld_dev_u64(my + rec::kWinRaw + j);
-        }
+    for (int j = 0; j < (int)kSpecWin; ++j) {
+        wk[j] = ld_dev_u64(my + rec::kWin + j);
+        wr[j] = (uint32_t)ld_dev_u64(my + rec::kWinRaw + j);
     }
     PROF_WMARK(7);
-    const uint32_t n_win = mine ? (uint32_t)(h[0] >> 32) & 0xffffu : 0u;
-    const uint32_t flags = mine ? (uint32_t)(h[0] >> 48) : 0u;
-    const float m_pen = mine ? __uint_as_float((uint32_t)h[2]) : NEG;
-    const uint32_t i_pen = mine ? (uint32_t)(h[2] >> 32) : kNoIdx;
-    const float m_msk = mine ? __uint_as_float((uint32_t)h[3]) : NEG;
-    const uint32_t i_msk = mine ? (uint32_t)(h[3] >> 32) : kNoIdx;
-    const uint32_t n_allowed = mine ? (uint32_t)h[4] : 0u;
-
-    if (mode == kModeGreedy) {
-        const uint32_t tot_allowed = wave_sum_u(n_allowed);
-        const bool use_mask = masked && tot_allowed > 0;
-        float bv = use_mask ? m_msk : m_pen;
-        uint32_t bi = use_mask ? i_msk : i_pen;
-        float braw = use_mask ? __uint_as_float((uint32_t)(h[7] >> 32)) : __uint_as_float((uint32_t)h[7]);
-        if (bi >= V) { bv = NEG; bi = kNoIdx; }
-        const uint32_t bi0 = bi;
-        wave_argmax(bv, bi);
-        const uint64_t own = ballot(bi0 == bi && bi < V);
-        braw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(braw), own ? __builtin_ctzll(own) : 0));
-        if (lane == 0) {
-            a.ids[row] = (int32_t)bi;
-            sm.l.chosen_raw = braw;
-            if (a.diag) {
-                lcs_row_diag dg{};
-                dg.n_cand = use_mask ? tot_allowed : V; dg.maxl = bv; dg.boundary = bv;
-                dg.path = LCS_PATH_GREEDY;
-                a.diag[row] = dg;
-            }
-        }
-        return false;
-    }
-
-    if (mode == kModeTopK) {
-        // the row's top-k (sampling.cpp:87-97): a k-way merge of the slices'
-        // rank-ordered top-k lists, then the exact normaliser over those k
-        if (ballot(mine && (flags & rec::kFlagWinLost))) return true;
-        const uint32_t K = P.top_k;
-        const uint32_t ns = min(n_win, K);
-        for (uint32_t j0 = 0; j0 < K; j0 += 8) {
-            uint64_t kk[8];
-            uint32_t rr[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const uint32_t j = j0 + u;
-                const bool ok = mine && j < ns;
-                kk[u] = ok ? ld_dev_u64(my + rec::kWin + j) : ~0ull;
-                rr[u] = ok ? (uint32_t)ld_dev_u64(my + rec::kWinRaw + j) : 0u;
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const uint32_t j = j0 + u;
-                if (mine && j < ns) {
-                    sm.u.f.tkey[lane * K + j] = kk[u];
-                    sm.u.f.traw[lane * K + j] = __uint_as_float(rr[u]);
-                }
-            }
-        }
-        wave_sync();
-        const uint32_t Ke = min(K, wave_sum_u(ns));
-        uint32_t p = 0;
-        for (uint32_t r = 0; r < Ke; ++r) {
-            const uint64_t head = (mine && p < ns) ? sm.u.f.tkey[lane * K + p] : ~0ull;
-            const uint64_t best = wave_min_u64(head);
-            if (head == best) {
-                sm.u.f.sorted[r] = best;
-                sm.u.f.sortedraw[r] = sm.u.f.traw[lane * K + p];
-                ++p;
-            }
-        }
-        wave_sync();
-        const float maxl = rank_val(sm.u.f.sorted[0]);
-        const float inv_t = fdiv(1.0f, P.temperature);
-        const double w = (uint32_t)lane < Ke ? exp((double)tempered(rank_val(sm.u.f.sorted[lane]), maxl, inv_t)) : 0.0;
-        const double Sf = wave_sum(w);
-        if (lane == 0) {
-            sm.l.fin_S = Sf;
-            sm.l.fin_rel = 0x1p-45;   // tree vs sequential summation of at most 64 terms
-            sm.l.fin_L0 = Ke;
-            sm.l.fin_maxl = maxl;
-        }
-        return false;
-    }
-
+    const uint32_t n_win = mine ? (uint32_t)(h0 >> 32) & 0xffffu : 0u;
+    const uint32_t flags = mine ? (uint32_t)(h0 >> 48) : 0u;
+    const float m_pen = mine ? __uint_as_float((uint32_t)h2) : NEG;
     // row window threshold maxl - delta, as the smallest float at or above it
-    const double delta = (double)P.temperature * (-log((double)P.min_p) + 1e-3);
+    // (delta as this workgroup's slice phase computed it)
+    const double delta = sm.l.win_delta;
     const float maxl = wave_max(m_pen);
     const double thr = (double)maxl - delta;
     float thr_up = (float)thr;
     if ((double)thr_up < thr) thr_up = next_up(thr_up);
     // a slice that could hold row-window entries must not have lost any
     if (ballot(mine && (flags & rec::kFlagWinLost) && m_pen >= thr_up)) return true;
+    // entries are in ascending rank order, so the qualifying ones lead
     uint32_t q = 0;
 #pragma unroll
     for (int j = 0; j < (int)kSpecWin; ++j) q += ((uint32_t)j < n_win && rank_val(wk[j]) >= thr_up) ? 1u : 0u;
@@ -1279,8 +1262,7 @@ __device__ __forceinline__ bool fin_gather(const SampleArgs& a, uint32_t row, ui
             sm.u.f.entraw[base + j] = __uint_as_float(wr[j]);
         }
     }
-    // slices whose leading entries all qualify and that hold more (rare);
-    // entries are in ascending rank order, so the qualifying ones lead
+    // slices whose fetched entries all qualify and that hold more (rare)
     uint32_t qtot = q;
     bool more = mine && q == kSpecWin && n_win > kSpecWin;
     for (uint32_t j0 = kSpecWin; ballot(more); j0 += kSpecWin) {
@@ -1319,17 +1301,87 @@ __device__ __forceinline__ bool fin_gather(const SampleArgs& a, uint32_t row, ui
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
-        if (e < L0) { sm.u.f.sorted[rk[c]] = k[c]; sm.u.f.sortedraw[rk[c]] = sm.u.f.entraw[e]; }
+        if (e < L0) {
+            sm.u.f.sorted[rk[c]] = k[c];
+            sm.u.f.sortedraw[rk[c]] = sm.u.f.entraw[e];
+            sm.u.f.sw[rk[c]] = exp((double)tempered(rank_val(k[c]), maxl, inv_t));
+        }
     }
     if (lane == 0) { sm.l.fin_L0 = L0; sm.l.fin_maxl = maxl; }
     PROF_WMARK(11);
     return false;
 }
 
+// Top-k rows: waves 2-3 copy the slices' rank-ordered top-k lists into LDS
+// (slot i: entry i % K of slice i / K), all loads issued before any store.
+__device__ __forceinline__ void fin_fetch_topk(const uint64_t* recs, uint32_t S, uint32_t K, SliceSmem& sm) {
+    constexpr uint32_t NF = 2 * kWave;                  // fetching threads
+    constexpr uint32_t SL = kTopKMerge / NF;            // slots per thread
+    const uint32_t t = threadIdx.x - 2 * kWave;
+    uint64_t kk[SL];
+    uint32_t rr[SL];
+#pragma unroll
+    for (uint32_t c = 0; c < SL; ++c) {
+        const uint32_t i = t + c * NF, s = i / K, j = i - s * K;
+        kk[c] = ~0ull;
+        rr[c] = 0u;
+        if (s < S) {
+            const uint64_t* r = recs + (uint64_t)s * rec::kWords64;
+            kk[c] = ld_dev_u64(r + rec::kWin + j);
+            rr[c] = (uint32_t)ld_dev_u64(r + rec::kWinRaw + j);
+        }
+    }
+#pragma unroll
+    for (uint32_t c = 0; c < SL; ++c) {
+        const uint32_t i = t + c * NF;
+        if (i < S * K) {
+            sm.u.f.tkey[i] = kk[c];
+            sm.u.f.traw[i] = __uint_as_float(rr[c]);
+        }
+    }
+}
+
+// Top-k rows (sampling.cpp:87-97): the k-way merge of the slices' top-k lists
+// (h0: this lane's slice header word 0), then the exact normaliser over those
+// k. Returns true when a slice could not rank its list.
+__device__ __forceinline__ bool fin_merge_topk(uint32_t S, uint32_t K, SliceSmem& sm, float inv_t, uint64_t h0) {
+    const int lane = lane_id();
+    const bool mine = (uint32_t)lane < S;
+    const uint32_t s = mine ? (uint32_t)lane : 0u;
+    const uint32_t flags = mine ? (uint32_t)(h0 >> 48) : 0u;
+    if (ballot(mine && (flags & rec::kFlagWinLost))) return true;
+    const uint32_t ns = mine ? min((uint32_t)(h0 >> 32) & 0xffffu, K) : 0u;
+    const uint32_t Ke = min(K, wave_sum_u(ns));
+    uint32_t p = 0;
+    for (uint32_t r = 0; r < Ke; ++r) {
+        const uint64_t head = p < ns ? sm.u.f.tkey[s * K + p] : ~0ull;
+        const uint32_t hk = (uint32_t)(head >> 32);
+        const uint32_t mk = wave_min_u(hk);
+        const uint64_t hit = ballot(head != ~0ull && hk == mk);
+        const int wl = hit ? __builtin_ctzll(hit) : 0;
+        if (lane == wl) {
+            sm.u.f.sorted[r] = head;
+            sm.u.f.sortedraw[r] = sm.u.f.traw[s * K + p];
+            ++p;
+        }
+    }
+    wave_sync();
+    const float maxl = rank_val(sm.u.f.sorted[0]);
+    const double w = (uint32_t)lane < Ke ? exp((double)tempered(rank_val(sm.u.f.sorted[lane]), maxl, inv_t)) : 0.0;
+    if ((uint32_t)lane < Ke) sm.u.f.sw[lane] = w;
+    const double Sf = wave_sum(w);
+    if (lane == 0) {
+        sm.l.fin_S = Sf;
+        sm.l.fin_rel = 0x1p-45;   // tree vs sequential summation of at most 64 terms
+        sm.l.fin_L0 = Ke;
+        sm.l.fin_maxl = maxl;
+    }
+    return false;
+}
+
 // Top-p, then min-p (sampling.cpp order), then the draw, 64 ranked row-window
-// entries at a time; weights exp((double)((p - maxl) * inv_t)) as the
-// reference's. Returns true when a top-p / min-p decision lies within the
-// normaliser's error bound.
+// entries at a time over the weights in sw. Returns true when a top-p / min-p
+// decision lies within the normaliser's error bound.
 __device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, SliceSmem& sm, uint32_t path) {
     const int lane = lane_id();
     PROF_WMARK(12);
@@ -1337,7 +1389,6 @@ __device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, Sl
     const uint32_t L0 = sm.l.fin_L0;
     const float maxl = sm.l.fin_maxl;
     const double Sf = sm.l.fin_S, rel = sm.l.fin_rel;
-    const float inv_t = fdiv(1.0f, P.temperature);
     bool uncertain = false;
     uint32_t keep_p = 0xffffffffu, keep = 0;
     const double tp = (double)P.top_p;
@@ -1351,8 +1402,7 @@ __device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, Sl
     for (uint32_t c0 = 0; c0 < L0 && keep == 0; c0 += kWave) {
         const uint32_t i = c0 + (uint32_t)lane;
         const bool in = i < L0;
-        const double w = in ? exp((double)tempered(rank_val(sm.u.f.sorted[i]), maxl, inv_t)) : 0.0;
-        if (in) sm.u.f.sw[i] = w;
+        const double w = in ? sm.u.f.sw[i] : 0.0;
         const double W = Wc + wave_scan_incl(w);
         const double cum = W * inv_S;
         if (P.top_p < 1.0f && keep_p == 0xffffffffu) {
@@ -1392,7 +1442,6 @@ __device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, Sl
     PROF_WMARK(13);
     if (pos == 0xffffffffu) {
         // kept set past the first 64 entries (r -= w_i walk, sampling.cpp:135-147)
-        wave_sync();
         kept_sum = 0.0;
         for (uint32_t c0 = 0; c0 < keep; c0 += kWave) {
             const uint32_t i = c0 + (uint32_t)lane;
@@ -1426,6 +1475,64 @@ __device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, Sl
     return false;
 }
 
+// The row's finalize, then the chosen token's logprob; every thread of the
+// last-arriving workgroup calls it after thread 0 staged the kernel arguments
+// in g_slice.l.args (read back from LDS, so that the kernel's argument
+// registers need not live through the main phase). Returns true when the row
+// needs the exact single-workgroup path.
+template <int G>
+__device__ __forceinline__ bool fin_row(uint32_t row, uint32_t mode, const lcs_params& P, bool masked,
+                                        const uint64_t* recs) {
+    SliceSmem& sm = g_slice;
+    const SampleArgs a = uniform_args(sm.l.args);
+    const uint32_t tid = threadIdx.x;
+    const int lane = lane_id(), wv = (int)(tid / kWave);
+    const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
+    const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
+    const bool stoch = mode == kModeWindow, topk = mode == kModeTopK;
+    const float inv_t = fdiv(1.0f, P.temperature);
+    bool fb = false;
+    if (topk) {
+        uint64_t h0 = 0;
+        if (wv == 0) h0 = ld_dev_u64(recs + ((uint32_t)lane < a.slices ? lane : 0) * rec::kWords64);
+        else if (wv == 1) { if (want_lp) fb = fin_logprobs(a, recs, row, ntop, sm); }
+        else fin_fetch_topk(recs, a.slices, P.top_k, sm);
+        if (fb && lane == 0) sm.l.fin_fb = 1u;
+        __syncthreads();
+        if (wv == 0) fb = fin_merge_topk(a.slices, P.top_k, sm, inv_t, h0);
+    } else if (wv == 0) {
+        if (stoch) fb = fin_window(a, recs, P, sm, inv_t);
+        else fin_greedy(a, recs, row, masked, sm);
+    } else if (wv == 1) {
+        if (want_lp) fb = fin_logprobs(a, recs, row, ntop, sm);
+    } else if (wv == 2) {
+        if (stoch) fin_norm(a, recs, sm, inv_t);
+    }
+    if (fb && lane == 0) sm.l.fin_fb = 1u;
+    __syncthreads();
+    if (sm.l.fin_fb) return true;
+    if (wv == 0 && (stoch || topk)) {
+        fb = fin_decide(a, row, sm, topk ? LCS_PATH_TOPK : LCS_PATH_WINDOW);
+        if (fb && lane == 0) sm.l.fin_fb = 1u;
+    }
+    __syncthreads();
+    if (sm.l.fin_fb) return true;
+    if (tid == 0 && want_lp) {
+        // logprob of the chosen token, or of the caller's lp_ids token
+        constexpr uint32_t DT = G == 8 ? LCS_BF16 : LCS_F32;
+        const void* rowp = static_cast<const char*>(a.logits) + (uint64_t)row * a.row_stride * (G == 8 ? 2u : 4u);
+        float raw = sm.l.chosen_raw;
+        bool inr = true;
+        if (a.lp_ids) {
+            const int32_t lid = a.lp_ids[row];
+            inr = lid >= 0 && (uint32_t)lid < a.vocab;
+            raw = inr ? load_elem(rowp, DT, (uint32_t)lid) : 0.0f;
+        }
+        a.chosen_lp[row] = inr ? (float)((double)raw - sm.l.log_z) : 0.0f;
+    }
+    return false;
+}
+
 // One workgroup per (row, slice of <= 8192 logits); 32 logits per thread in
 // registers. Penalised logits reach the slice through an LDS table of
 // override bits written once per distinct history id. Every slice publishes a
@@ -1436,24 +1543,45 @@ void slice_kernel(SampleArgs a) {
     constexpr int NT = kSliceThreads;
     constexpr int NG = kSliceElems / G;   // 16-byte groups per thread
     constexpr int HC = 8;                 // history ids per thread per chunk
-    __shared__ SliceSmem sm;
+    SliceSmem& sm = g_slice;
     const uint32_t tid = threadIdx.x;
     const int lane = lane_id(), wv = (int)(tid / kWave);
     const uint32_t S = a.slices;
     const uint32_t row = blockIdx.x / S, slice = blockIdx.x % S;
     if (row >= a.rows) return;
-    const lcs_params P = a.params[row];
-    const bool masked = a.mask != nullptr && (a.has_mask == nullptr || a.has_mask[row] != 0);
     if ((a.flags & LCS_WRITE_PENALIZED) != 0) return;
-    const uint32_t mode = row_mode(P, masked, a.vocab);
-    if (mode == kModeGeneral) return;
     PROF_MARK(0);
     const uint32_t V = a.vocab;
-    const uint32_t esz = a.dtype == LCS_BF16 ? 2u : 4u;
+    constexpr uint32_t DT = G == 8 ? LCS_BF16 : LCS_F32;   // the launch picks G from the dtype
+    constexpr uint32_t esz = G == 8 ? 2u : 4u;
     const void* rowp = static_cast<const char*>(a.logits) + (uint64_t)row * a.row_stride * esz;
     const uint32_t lo = slice * a.slice_len;
     const uint32_t hi = min(V, lo + a.slice_len);
     const uint32_t len = hi - lo;
+    // the slice's logits, one 16-byte load per group (groups past the slice
+    // load the slice's first group and are masked below); issued before
+    // anything else when the host saw every row of the batch take a sliced
+    // mode, else once this row's mode is known
+    uint4 raw[NG];
+    auto load_logits = [&]() {
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            const uint32_t e0 = lo + (j * NT + tid) * G;
+            raw[j] = load16(rowp, (e0 < hi ? e0 : lo) / G);
+        }
+    };
+    const bool early = a.all_sliced != 0u;
+    if (early) load_logits();
+    // the row's parameters and the small per-row words come through the
+    // scalar cache, so that waiting for them never waits for logits
+    const lcs_params P = scalar_load(a.params + row);
+    const bool masked = a.mask != nullptr && (a.has_mask == nullptr || scalar_load_u8(a.has_mask + row) != 0);
+    const uint32_t mode = row_mode(P, masked, V);
+    if (mode == kModeGeneral) {
+        wait_all_memory();   // (only when the host's parameter copy disagreed)
+        return;
+    }
+    if (!early) load_logits();
     const uint32_t* mrow = masked ? a.mask + (uint64_t)row * a.mask_words : nullptr;
     const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
     const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
@@ -1463,43 +1591,28 @@ void slice_kernel(SampleArgs a) {
     const bool topk = mode == kModeTopK;
     const bool wins = stoch || topk;   // rows that publish a ranked entry list
 
-    // ---- loads: history window ids first, then the slice's logits ----
+    // ---- then the history window ids [hstart, hn) (clamped addresses, no
+    // branch around a load; slots past the window are skipped where used) ----
     const bool pen = penalties_active(P) && a.hist_off != nullptr;
     uint32_t hn = 0, hstart = 0, hoff = 0;
     if (pen) {
-        hoff = a.hist_off[row];
-        hn = a.hist_off[row + 1] - hoff;
+        hoff = scalar_load(a.hist_off + row);
+        hn = scalar_load(a.hist_off + row + 1) - hoff;
         hstart = hn > P.repeat_last_n ? hn - P.repeat_last_n : 0u;
     }
     const bool hany = pen && hn > hstart;
-    const bool htwo = hany && hn - hstart > (uint32_t)(NT * HC);
-    uint32_t hA[HC], hB[HC];
     const uint32_t nwin_h = hn - hstart;
+    const bool htwo = hany && nwin_h > (uint32_t)(NT * HC);
+    uint32_t hA[HC], hB[HC];
     auto load_ids = [&](uint32_t (&h)[HC], uint32_t c0) {
 #pragma unroll
         for (int k = 0; k < HC; ++k) {
-            const uint32_t i = hstart + c0 + (uint32_t)k * NT + tid;
-            h[k] = (uint32_t)a.hist_ids[hoff + (i < hn ? i : hn - 1)];   // clamped: no branch around the load
-        }
-        // slots past the window are invalid where a wave's slot runs past it
-#pragma unroll
-        for (int k = 0; k < HC; ++k) {
-            if (c0 + (uint32_t)k * NT + (uint32_t)wv * kWave + kWave > nwin_h) {
-                const uint32_t i = c0 + (uint32_t)k * NT + tid;
-                h[k] = i < nwin_h ? h[k] : 0xffffffffu;
-            }
+            const uint32_t i = c0 + (uint32_t)k * NT + tid;
+            h[k] = (uint32_t)a.hist_ids[hoff + hstart + (i < nwin_h ? i : nwin_h - 1)];
         }
     };
     if (hany) load_ids(hA, 0);
     if (htwo) load_ids(hB, NT * HC);
-    // the slice's logits, one 16-byte load per group (groups past the slice
-    // load the slice's first group and are masked below)
-    uint4 raw[NG];
-#pragma unroll
-    for (int j = 0; j < NG; ++j) {
-        const uint32_t e0 = lo + (j * NT + tid) * G;
-        raw[j] = load16(rowp, (e0 < hi ? e0 : lo) / G);
-    }
     uint32_t mw[NG];
     if (mrow) {
 #pragma unroll
@@ -1510,35 +1623,14 @@ void slice_kernel(SampleArgs a) {
         }
     }
     if (tid == 0) { sm.l.ncand = 0; sm.l.nwin = 0; }
-
-    // ---- penalties, part 1: an LDS table of (penalised ^ raw) bits per slice
-    // position, 0 where no history id falls (sampling.cpp:16-41 applied once per
-    // id): clear it, fetch the raw logits of the in-slice ids, count them; the
-    // lane whose increment finds 0 owns the id ----
-    float rA[HC], rB[HC];
-    uint32_t oA = 0, oB = 0;
+    // ---- penalties, part 1: an LDS table over the slice's positions, cleared
+    // here, then counting the in-slice history ids; the thread whose
+    // increment finds 0 owns the id (sampling.cpp:16-41 applies each distinct
+    // id once, with its count) ----
     if (hany) {
 #pragma unroll
         for (int i = 0; i < (int)(kSliceMax / 4 / NT); ++i) sm.u.ovr4[i * NT + tid] = make_uint4(0, 0, 0, 0);
-        auto gather = [&](const uint32_t (&h)[HC], float (&r)[HC]) {
-#pragma unroll
-            for (int k = 0; k < HC; ++k) {
-                const uint32_t d = h[k] - lo;
-                r[k] = load_elem(rowp, a.dtype, (h[k] < V && d < len) ? h[k] : lo);
-            }
-        };
-        gather(hA, rA);
-        if (htwo) gather(hB, rB);
         __syncthreads();
-        auto count = [&](const uint32_t (&h)[HC], uint32_t& own) {
-#pragma unroll
-            for (int k = 0; k < HC; ++k) {
-                const uint32_t d = h[k] - lo;
-                if (h[k] < V && d < len && atomicAdd(&sm.u.ovr[d], 1u) == 0u) own |= 1u << k;
-            }
-        };
-        count(hA, oA);
-        if (htwo) count(hB, oB);
     }
 
     // ---- values; positions past the slice read as -inf ----
@@ -1563,74 +1655,53 @@ void slice_kernel(SampleArgs a) {
 #pragma unroll
     for (int q = 0; q < kSliceElems; ++q) lm = fmaxf(lm, v[q]);
     sm.l.lmax[tid] = lm;
-    __syncthreads();
-    float Ms;   // raw slice max
-    {
-        float m4 = sm.l.lmax[lane];
+    // counts, then the owners' raw logits (in flight while the raw statistics run)
+    uint32_t oA = 0, oB = 0;
+    float rA[HC], rB[HC];
+    if (hany) {
+        auto count = [&](const uint32_t (&h)[HC], uint32_t c0, uint32_t& own) {
 #pragma unroll
-        for (int c = 1; c < kSliceWaves; ++c) m4 = fmaxf(m4, sm.l.lmax[lane + c * kWave]);
-        Ms = wave_max(m4);
-    }
-    // ---- penalties, part 2: each owner writes its id's word; one wave finds
-    // the ntop-th largest lane maximum, a lower bound of the slice's top-n ----
-    if (hany || ntop) {
-        if (hany) {
-            const double inv_rp = 1.0 / (double)P.repeat_penalty;
-            auto put = [&](const uint32_t (&h)[HC], const float (&r)[HC], uint32_t own) {
-#pragma unroll
-                for (int k = 0; k < HC; ++k) {
-                    if ((own >> k) & 1u) {
-                        const uint32_t d = h[k] - lo;
-                        const float p = penalize_fast(r[k], sm.u.ovr[d], P, inv_rp);
-                        sm.u.ovr[d] = __float_as_uint(p) ^ __float_as_uint(r[k]);
-                    }
-                }
-            };
-            put(hA, rA, oA);
-            if (htwo) put(hB, rB, oB);
-        }
-        if (ntop && wv == kSliceWaves - 1) {
-            float c4[kSliceWaves];
-#pragma unroll
-            for (int c = 0; c < kSliceWaves; ++c) c4[c] = sm.l.lmax[lane + c * kWave];
-            float t = NEG;
-            for (uint32_t r = 0; r < ntop; ++r) {
-                float m = c4[0];
-#pragma unroll
-                for (int c = 1; c < kSliceWaves; ++c) m = fmaxf(m, c4[c]);
-                t = wave_max(m);
-                const uint64_t hit = ballot(m == t);
-                if (lane == __builtin_ctzll(hit)) {
-                    bool done = false;
-#pragma unroll
-                    for (int c = 0; c < kSliceWaves; ++c) {
-                        if (!done && c4[c] == t) { c4[c] = NEG; done = true; }
-                    }
-                }
+            for (int k = 0; k < HC; ++k) {
+                const uint32_t i = c0 + (uint32_t)k * NT + tid;
+                const uint32_t d = h[k] - lo;
+                if (i < nwin_h && h[k] < V && d < len && atomicAdd(&sm.u.ovr[d], 1u) == 0u) own |= 1u << k;
             }
-            if (lane == 0) sm.l.t_s = t;
+        };
+        auto gather = [&](const uint32_t (&h)[HC], uint32_t own, float (&r)[HC]) {
+#pragma unroll
+            for (int k = 0; k < HC; ++k) r[k] = load_elem(rowp, DT, ((own >> k) & 1u) ? h[k] : lo);
+        };
+        count(hA, 0, oA);
+        gather(hA, oA, rA);
+        if (htwo) {
+            count(hB, NT * HC, oB);
+            gather(hB, oB, rB);
         }
-        __syncthreads();
+    }
+    __syncthreads();
+    // the raw slice max from the 256 lane maxima; one wave also finds the
+    // ntop-th largest of them, a lower bound of the slice's top-n, while the
+    // others start the raw sums
+    float Ms;
+    {
+        float m4[kSliceWaves];
+#pragma unroll
+        for (int c = 0; c < kSliceWaves; ++c) m4[c] = sm.l.lmax[lane + c * kWave];
+        Ms = wave_max(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])));
+        if (ntop && wv == kSliceWaves - 1) {
+            __builtin_amdgcn_s_setprio(2);   // a serial chain among busy waves
+            uint32_t k4[kSliceWaves];
+#pragma unroll
+            for (int c = 0; c < kSliceWaves; ++c) k4[c] = fkey(m4[c]);
+            const float t = key_to_f(wave_kth_largest4(k4, ntop));
+            if (lane == 0) sm.l.t_s = t;
+            __builtin_amdgcn_s_setprio(0);
+        }
     }
     PROF_MARK(1);
 
-    // ---- top-n candidates: elements >= the threshold, in the few lanes that hold one ----
-    if (ntop) {
-        const float t = sm.l.t_s;
-        if (lm >= t) {
-#pragma unroll
-            for (int q = 0; q < kSliceElems; ++q) {
-                if (v[q] >= t) {
-                    const uint32_t e = eid(q);
-                    if (e < hi) {
-                        const uint32_t s = atomicAdd(&sm.l.ncand, 1u);
-                        if (s < kCandCap) sm.l.ck[s] = rank_key(v[q], e);
-                    }
-                }
-            }
-        }
-    }
-    // ---- raw sum of exp against the slice max ----
+    // ---- raw sum of exp against the slice max: terms 2^fma(v, L, b) with b =
+    // RN(-Ms L) share the exponent error e_b = Ms L + b, taken out in f64 ----
     double sw = 0.0;
     if (want_lp && Ms != NEG) {
         const float b = -Ms * kLog2E;
@@ -1646,12 +1717,52 @@ void slice_kernel(SampleArgs a) {
                 for (int k = 0; k < w; ++k) c[k] += c[k + w];
             s += c[0];
         }
-        sw = wave_sum((double)s);
+        const double eb = ((double)Ms * (double)kLog2E + (double)b) * 0.6931471805599453;
+        sw = (double)wave_sum_f(s) * (1.0 - eb + 0.5 * eb * eb);   // 2^-e_b, |e_b| tiny
     }
     if (lane == 0) sm.l.sraw[wv] = sw;
     PROF_MARK(2);
 
-    // ---- penalised values ----
+    // ---- penalties, part 2: each owner writes its id's word, penalised ^ raw
+    // bits (penalize_fast: exact for normal-range quotients) ----
+    if (hany) {
+        const double inv_rp = 1.0 / (double)P.repeat_penalty;
+        auto put = [&](const uint32_t (&h)[HC], const float (&r)[HC], uint32_t own) {
+#pragma unroll
+            for (int k = 0; k < HC; ++k) {
+                if ((own >> k) & 1u) {
+                    const uint32_t d = h[k] - lo;
+                    const float p = penalize_fast(r[k], sm.u.ovr[d], P, inv_rp);
+                    sm.u.ovr[d] = __float_as_uint(p) ^ __float_as_uint(r[k]);
+                }
+            }
+        };
+        put(hA, rA, oA);
+        if (htwo) put(hB, rB, oB);
+    }
+    if (hany || ntop) __syncthreads();
+
+    // ---- top-n candidates (raw values): elements >= the threshold, in the
+    // few lanes that hold one ----
+    if (ntop) {
+        const float t = sm.l.t_s;
+        if (ballot(lm >= t)) {
+            if (lm >= t) {
+#pragma unroll
+                for (int q = 0; q < kSliceElems; ++q) {
+                    if (v[q] >= t) {
+                        const uint32_t e = eid(q);
+                        if (e < hi) {
+                            const uint32_t s = atomicAdd(&sm.l.ncand, 1u);
+                            if (s < kCandCap) sm.l.ck[s] = rank_key(v[q], e);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    // ---- penalised values: raw ^ word (0 where no history id falls); later
+    // steps recover raw logits the same way ----
     if (hany) {
 #pragma unroll
         for (int j = 0; j < NG; ++j) {
@@ -1712,10 +1823,12 @@ void slice_kernel(SampleArgs a) {
         for (int q = 0; q < kSliceElems; ++q) lpm = fmaxf(lpm, v[q]);
         const float pm = wave_max(lpm);
         if (lane == 0) { sm.l.mpen[wv] = pm; sm.l.ipen[wv] = kNoIdx; sm.l.nall[wv] = 0; }
+        wave_sync();
     }
     PROF_MARK(3);
 
-    // ---- min-p window entries and the normaliser's bulk, against the slice max ----
+    // ---- min-p window entries and the normaliser's bulk, against the slice's
+    // penalised max ----
     if (stoch) {
         __syncthreads();
         float ms = sm.l.mpen[0];
@@ -1723,15 +1836,18 @@ void slice_kernel(SampleArgs a) {
         for (int w = 1; w < kSliceWaves; ++w) ms = fmaxf(ms, sm.l.mpen[w]);
         const float inv_t = fdiv(1.0f, P.temperature);
         const float kk = fmul(inv_t, kLog2E);
-        // bulk term c = 2^t, t = (p - ms) * inv_t * log2(e) <= 0; sum of c|t| bounds
-        // the effect of the rounding of t here and in the reference's tempered offsets
+        // bulk term c = 2^t, t = RN(p kk + bb) = (p - ms) kk + e + rounding, with
+        // bb = RN(-ms kk) and e = ms kk + bb common to all terms (taken out in
+        // f64 below); sum of c|t| bounds the rounding of t here and in the
+        // reference's tempered offsets (t clamped so that -inf logits add 0)
+        const float bb = -ms * kk;
         float bs = 0.0f, bt = 0.0f;
 #pragma unroll
         for (int j = 0; j < NG; ++j) {
             float c[G];
 #pragma unroll
             for (int k = 0; k < G; ++k) {
-                const float t = fmaxf(fmul(fsub(v[j * G + k], ms), kk), -250.0f);
+                const float t = fmaxf(fmaf(v[j * G + k], kk, bb), -1e30f);
                 c[k] = fast_exp2(t);
                 bt = fmaf(c[k], -t, bt);
             }
@@ -1743,57 +1859,45 @@ void slice_kernel(SampleArgs a) {
         }
         // window test in float, rounded down from the exact threshold (a superset)
         const double delta = (double)P.temperature * (-log((double)P.min_p) + 1e-3);
+        if (tid == 0) sm.l.win_delta = delta;   // for this workgroup's finalize, if last
         const double thr = (double)ms - delta;
         float thr_f = (float)thr;
         if ((double)thr_f > thr) thr_f = next_down(thr_f);
-        if (lpm >= thr_f) {
+        if (ballot(lpm >= thr_f)) {
+            if (lpm >= thr_f) {
 #pragma unroll
-            for (int q = 0; q < kSliceElems; ++q) {
-                if (v[q] >= thr_f) {
-                    const uint32_t s = atomicAdd(&sm.l.nwin, 1u);
-                    if (s < kWinLds) sm.l.wk[s] = rank_key(v[q], eid(q));
-                }
-            }
-        }
-        const double bsum = wave_sum((double)bs);
-        const double btsum = wave_sum((double)bt);
-        if (lane == 0) { sm.l.bulk[wv] = bsum; sm.l.bterm[wv] = btsum; }
-    } else if (topk) {
-        // the slice's top-k by penalised value (sampling.cpp:87-97): elements
-        // >= the k-th largest lane maximum, found by one wave over all 256
-        sm.l.lmax[tid] = lpm;
-        __syncthreads();
-        if (wv == kSliceWaves - 1) {
-            float c4[kSliceWaves];
-#pragma unroll
-            for (int c = 0; c < kSliceWaves; ++c) c4[c] = sm.l.lmax[lane + c * kWave];
-            float t = NEG;
-            for (uint32_t r = 0; r < P.top_k; ++r) {
-                float m = c4[0];
-#pragma unroll
-                for (int c = 1; c < kSliceWaves; ++c) m = fmaxf(m, c4[c]);
-                t = wave_max(m);
-                const uint64_t hit = ballot(m == t);
-                if (lane == __builtin_ctzll(hit)) {
-                    bool done = false;
-#pragma unroll
-                    for (int c = 0; c < kSliceWaves; ++c) {
-                        if (!done && c4[c] == t) { c4[c] = NEG; done = true; }
+                for (int q = 0; q < kSliceElems; ++q) {
+                    if (v[q] >= thr_f) {
+                        const uint32_t s = atomicAdd(&sm.l.nwin, 1u);
+                        if (s < kWinLds) sm.l.wk[s] = rank_key(v[q], eid(q));
                     }
                 }
             }
-            if (lane == 0) sm.l.t_s = t;
         }
+        const double eb = ((double)ms * (double)kk + (double)bb) * 0.6931471805599453;
+        const double fe = 1.0 - eb + 0.5 * eb * eb;   // 2^-e, |e| tiny
+        const double bsum = (double)wave_sum_f(bs) * fe;
+        const double btsum = (double)wave_sum_f(bt) * fe;
+        if (lane == 0) { sm.l.bulk[wv] = bsum; sm.l.bterm[wv] = btsum; }
+    } else if (topk) {
+        // the slice's top-k by penalised value (sampling.cpp:87-97): elements
+        // >= the k-th largest penalised lane maximum of the slice
+        sm.l.lmax[tid] = lpm;
         __syncthreads();
-        const float t = sm.l.t_s;
-        if (lpm >= t) {
+        uint32_t k4[kSliceWaves];
 #pragma unroll
-            for (int q = 0; q < kSliceElems; ++q) {
-                if (v[q] >= t) {
-                    const uint32_t e = eid(q);
-                    if (e < hi) {
-                        const uint32_t s = atomicAdd(&sm.l.nwin, 1u);
-                        if (s < kWinLds) sm.l.wk[s] = rank_key(v[q], e);
+        for (int c = 0; c < kSliceWaves; ++c) k4[c] = fkey(sm.l.lmax[lane + c * kWave]);
+        const float t = key_to_f(wave_kth_largest4(k4, P.top_k));
+        if (ballot(lpm >= t)) {
+            if (lpm >= t) {
+#pragma unroll
+                for (int q = 0; q < kSliceElems; ++q) {
+                    if (v[q] >= t) {
+                        const uint32_t e = eid(q);
+                        if (e < hi) {
+                            const uint32_t s = atomicAdd(&sm.l.nwin, 1u);
+                            if (s < kWinLds) sm.l.wk[s] = rank_key(v[q], e);
+                        }
                     }
                 }
             }
@@ -1822,7 +1926,9 @@ void slice_kernel(SampleArgs a) {
             ma = wave_max(ma);
             ia = kNoIdx;
             bk = wave_sum(lw ? sm.l.bulk[wl] : 0.0);
-            be = wave_sum(lw ? sm.l.bterm[wl] : 0.0) * 0x1p-22 + bk * 0x1p-20 + (double)len * 0x1p-120;
+            // f32 terms: exp2 and the per-lane and cross-lane f32 sums within
+            // 2^-19 of the bulk; the offsets' roundings within 2^-22 c|t|
+            be = wave_sum(lw ? sm.l.bterm[wl] : 0.0) * 0x1p-22 + bk * 0x1p-19 + (double)len * 0x1p-120;
         } else {
             const uint32_t ia0 = ia, im0 = im;
             wave_argmax(ma, ia);
@@ -1895,7 +2001,10 @@ void slice_kernel(SampleArgs a) {
         const uint32_t prev = __hip_atomic_fetch_add(a.counters + row, 1u, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
         const bool last = prev == S - 1;
-        if (last) st_dev(a.counters + row, 0u);
+        if (last) {
+            st_dev(a.counters + row, 0u);
+            stash_args(&sm.l.args);   // for the finalize (fin_row)
+        }
         sm.l.last = last ? 1u : 0u;
         sm.l.fin_fb = 0u;
     }
@@ -1903,35 +2012,9 @@ void slice_kernel(SampleArgs a) {
     PROF_MARK(5);
     if (!sm.l.last) return;
     // =============== last-arriving workgroup finishes the row ===============
-    bool fb = false;
-    if (wv == 0) {
-        fb = fin_gather(a, row, mode, sm);
-    } else if (wv == 1) {
-        if (want_lp) fb = fin_logprobs(a, row, sm);
-    } else if (wv == 2) {
-        if (stoch) fin_norm(a, row, sm);
-    }
-    if (fb && lane == 0) sm.l.fin_fb = 1u;
-    __syncthreads();
-    if (wv == 0 && wins && !sm.l.fin_fb) {
-        fb = fin_decide(a, row, sm, topk ? LCS_PATH_TOPK : LCS_PATH_WINDOW);
-        if (fb && lane == 0) sm.l.fin_fb = 1u;
-    }
-    __syncthreads();
+    const bool fb = fin_row<G>(row, mode, P, masked, reinterpret_cast<const uint64_t*>(a.recs) + (uint64_t)row * S * rec::kWords64);
     PROF_MARK(6);
-    if (sm.l.fin_fb) {
-        stage_args(&sm.u.ex.args);
-        exact_row<kSliceThreads, kFbBins, kFbCap, kFbHistCap, G>(sm.u.ex.args, row, sm.u.ex);
-    } else if (tid == 0 && want_lp) {
-        float raw = sm.l.chosen_raw;
-        bool inr = true;
-        if (a.lp_ids) {
-            const int32_t lid = a.lp_ids[row];
-            inr = lid >= 0 && (uint32_t)lid < V;
-            raw = inr ? load_elem(rowp, a.dtype, (uint32_t)lid) : 0.0f;
-        }
-        a.chosen_lp[row] = inr ? (float)((double)raw - sm.l.log_z) : 0.0f;
-    }
+    if (fb) exact_row<kSliceThreads, kFbBins, kFbCap, kFbHistCap, G>(sm.l.args, row, sm.u.ex);
 }
 
 #ifdef LCS_PROFILE
