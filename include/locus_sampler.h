@@ -102,7 +102,8 @@ enum lcs_path {
     LCS_PATH_WINDOW = 2u,     /* sliced min-p window, certified normaliser */
     LCS_PATH_WINDOW_EXACT = 3u, /* window with an exactly recomputed normaliser */
     LCS_PATH_GENERAL = 4u,    /* single-workgroup exact selection */
-    LCS_PATH_TOPK = 5u        /* sliced exact top-k (k <= 64) */
+    LCS_PATH_TOPK = 5u,       /* sliced exact top-k (k <= 64) */
+    LCS_PATH_NUCLEUS = 6u     /* sliced histogram passes, exact decisions (no top-k) */
 };
 
 typedef struct lcs_out {

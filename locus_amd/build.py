@@ -29,7 +29,7 @@ HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
              "-fno-honor-nans", "-mno-amdgpu-ieee",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I" + INCLUDE]
-HIP_SOURCES = ["lcs_api.hip", "lcs_sample.hip", "lcs_verify.hip"]
+HIP_SOURCES = ["lcs_api.hip", "lcs_sample.hip", "lcs_nucleus.hip", "lcs_verify.hip"]
 SAMPLER_SO = os.path.join(HERE, "liblocus_sampler.so")
 HOST_SO = os.path.join(HERE, "liblocus_host.so")
 HOST_SOURCES = ["grammar.cpp", "speculative.cpp", "sampler_registry.cpp", "host_capi.cpp", "sampling.cpp"]

@@ -14,6 +14,7 @@
 namespace lcs {
 hipError_t launch_slice(const SampleArgs& a, hipStream_t st);
 hipError_t launch_general(const SampleArgs& a, hipStream_t st);
+hipError_t launch_nucleus(const SampleArgs& a, hipStream_t st);
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t st);
 }  // namespace lcs
 
@@ -28,6 +29,11 @@ struct lcs_ctx {
     float* d_raw = nullptr;
     float* d_pen = nullptr;
     uint32_t* status = nullptr;
+    // nucleus path workspace (kNucRows rows at a time)
+    lcs::NucRow* nrow = nullptr;
+    uint32_t* nh_cnt = nullptr;
+    double* nh_mass = nullptr;
+    uint64_t* nlist = nullptr;
     std::string err;
 };
 
@@ -110,6 +116,8 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t 
     c->max_slices = slices_for(max_vocab);
     const size_t rec_bytes = (size_t)max_rows * c->max_slices * lcs::rec::kWords * 4;
     const size_t d_elems = (size_t)max_rows * c->max_hist;
+    const size_t nuc_rows = max_rows < lcs::kNucRows ? max_rows : lcs::kNucRows;
+    const size_t nh_elems = nuc_rows * lcs::kMaxSlices * lcs::kNucBins;
     hipError_t e = hipSuccess;
     if ((e = hipMalloc(&c->recs, rec_bytes)) != hipSuccess ||
         (e = hipMalloc(&c->counters, (size_t)max_rows * 4)) != hipSuccess ||
@@ -118,6 +126,10 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t 
         (e = hipMalloc(&c->d_raw, d_elems * 4)) != hipSuccess ||
         (e = hipMalloc(&c->d_pen, d_elems * 4)) != hipSuccess ||
         (e = hipMalloc(&c->status, 4)) != hipSuccess ||
+        (e = hipMalloc(&c->nrow, nuc_rows * sizeof(lcs::NucRow))) != hipSuccess ||
+        (e = hipMalloc(&c->nh_cnt, nh_elems * 4)) != hipSuccess ||
+        (e = hipMalloc(&c->nh_mass, nh_elems * 8)) != hipSuccess ||
+        (e = hipMalloc(&c->nlist, nuc_rows * lcs::kNucList * 8)) != hipSuccess ||
         (e = hipMemset(c->counters, 0, (size_t)max_rows * 4)) != hipSuccess ||
         (e = hipMemset(c->vcounters, 0, (size_t)max_rows * 4)) != hipSuccess ||
         (e = hipMemset(c->status, 0, 4)) != hipSuccess ||
@@ -138,6 +150,10 @@ void lcs_destroy(lcs_ctx* c) {
     (void)hipFree(c->vcounters);
     (void)hipFree(c->d_ids);
     (void)hipFree(c->d_raw);
+    (void)hipFree(c->nrow);
+    (void)hipFree(c->nh_cnt);
+    (void)hipFree(c->nh_mass);
+    (void)hipFree(c->nlist);
     (void)hipFree(c->d_pen);
     (void)hipFree(c->status);
     delete c;
@@ -179,9 +195,9 @@ int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
     // Which kernels to launch: a row runs in exactly one of them (the
     // kernels re-derive each row's mode on the device). Without a host copy
     // of the params both are launched.
-    bool any_slice = true, any_general = true;
+    bool any_slice = true, any_general = true, any_nucleus = true;
     if (b->params_host) {
-        any_slice = any_general = false;
+        any_slice = any_general = any_nucleus = false;
         for (uint32_t r = 0; r < b->rows; ++r) {
             const lcs_params& p = b->params_host[r];
             for (int mk = 0; mk < 2; ++mk) {
@@ -189,12 +205,13 @@ int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
                 if (masked && !b->mask) continue;
                 if (!masked && b->mask && !b->has_mask) continue;  // every row masked
                 const uint32_t m = lcs::row_mode(p, masked, b->vocab);
-                any_slice = any_slice || m != lcs::kModeGeneral;
+                any_slice = any_slice || (m != lcs::kModeGeneral && m != lcs::kModeNucleus);
                 any_general = any_general || m == lcs::kModeGeneral;
+                any_nucleus = any_nucleus || m == lcs::kModeNucleus;
             }
         }
     }
-    if (b->flags & LCS_WRITE_PENALIZED) { any_slice = false; any_general = true; }
+    if (b->flags & LCS_WRITE_PENALIZED) { any_slice = false; any_nucleus = false; any_general = true; }
 
     lcs::SampleArgs a{};
     a.logits = b->logits;
@@ -228,13 +245,18 @@ int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
     a.slice_len = slice_len_for(b->vocab);
     // every row known to run sliced: the slice kernel may start its logit
     // loads before it has the row's parameters
-    a.all_sliced = (b->params_host && !any_general) ? 1u : 0u;
+    a.all_sliced = (b->params_host && !any_general && !any_nucleus) ? 1u : 0u;
+    a.nrow = c->nrow;
+    a.nh_cnt = c->nh_cnt;
+    a.nh_mass = c->nh_mass;
+    a.nlist = c->nlist;
 
     DeviceGuard g(c->device);
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t e = hipSuccess;
     if (any_general && (e = lcs::launch_general(a, st)) != hipSuccess) return hip_fail(c, e, "general kernel launch");
     if (any_slice && (e = lcs::launch_slice(a, st)) != hipSuccess) return hip_fail(c, e, "slice kernel launch");
+    if (any_nucleus && (e = lcs::launch_nucleus(a, st)) != hipSuccess) return hip_fail(c, e, "nucleus kernels launch");
     return LCS_OK;
 }
 

@@ -479,4 +479,49 @@ __device__ __forceinline__ void stream_groups(const void* rowp, uint32_t V, F&& 
     }
 }
 
+// ------------------------------------------------------ misc helpers ----
+__device__ __forceinline__ double bits_d(uint64_t b) { return __longlong_as_double((long long)b); }
+__device__ __forceinline__ uint64_t d_bits(double d) { return (uint64_t)__double_as_longlong(d); }
+__device__ __forceinline__ uint64_t pack2(uint32_t lo, uint32_t hi) { return ((uint64_t)hi << 32) | lo; }
+
+// Ascending ranks of n <= 4*64 unique keys in LDS, by one wave: lane l takes
+// entries l, l+64, l+128, l+192 (k[c], ~0 past n) and counts the smaller keys
+// with broadcast reads, 8 per batch.
+__device__ __forceinline__ void lds_rank4(const uint64_t* keys, uint32_t n, uint64_t (&k)[4], uint32_t (&rk)[4]) {
+    const uint32_t lane = (uint32_t)lane_id();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t e = lane + (uint32_t)c * kWave;
+        k[c] = e < n ? keys[e] : ~0ull;
+        rk[c] = 0;
+    }
+    if (n <= (uint32_t)kWave) {
+        uint32_t f = 0;
+        for (; f + 8 <= n; f += 8) {
+            uint64_t o[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) o[u] = keys[f + u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) rk[0] += o[u] < k[0] ? 1u : 0u;
+        }
+        for (; f < n; ++f) rk[0] += keys[f] < k[0] ? 1u : 0u;
+        return;
+    }
+    uint32_t f = 0;
+    for (; f + 8 <= n; f += 8) {
+        uint64_t o[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) o[u] = keys[f + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) rk[c] += o[u] < k[c] ? 1u : 0u;
+    }
+    for (; f < n; ++f) {
+        const uint64_t o = keys[f];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rk[c] += o < k[c] ? 1u : 0u;
+    }
+}
+
 }  // namespace lcs

@@ -49,7 +49,7 @@ constexpr uint32_t kFbBins = 512;
 constexpr uint32_t kFbCap = 512;
 constexpr uint32_t kFbHistCap = kFastHistMax;
 
-enum RowMode : uint32_t { kModeGreedy = 1, kModeWindow = 2, kModeGeneral = 4, kModeTopK = 8 };
+enum RowMode : uint32_t { kModeGreedy = 1, kModeWindow = 2, kModeGeneral = 4, kModeTopK = 8, kModeNucleus = 16 };
 constexpr uint32_t kTopKMax = 64;         // top_k served by the sliced path
 constexpr uint32_t kTopKMerge = 1024;     // slices x top_k entries the finalize merges
 
@@ -65,8 +65,36 @@ __host__ __device__ inline uint32_t row_mode(const lcs_params& p, bool masked, u
         return kModeTopK;
     }
     if (p.min_p > 0.0f && !masked && !topk && pen_ok) return kModeWindow;
+    if (!topk && pen_ok) return kModeNucleus;
     return kModeGeneral;
 }
+
+// ---- nucleus path (three slice-parallel passes; see lcs_nucleus.hip) ----
+constexpr uint32_t kNucBins = 512;      // histogram bins over the tempered offset
+constexpr uint32_t kNucRows = 256;      // rows per nucleus launch (workspace rows)
+constexpr uint32_t kNucList = 4096;     // candidates the select pass compacts per row
+constexpr uint32_t kNucRanges = 4;      // bin ranges a row's decisions can need
+constexpr uint32_t kNucSub = 128;       // sub-bins per range in the select pass
+constexpr float kNucXFloor = -128.0f;   // offsets below collapse into the last bin
+constexpr uint32_t kNucFallback = 1u;   // row state flag: resolve with exact_row
+struct NucRange {
+    uint32_t b0, b1;   // bins [b0, b1]
+    uint32_t c0, cnt;  // candidates before the range, in it
+    double m0, m;      // mass before the range, in it
+};
+struct NucRow {
+    float maxl;        // penalised candidate max (pass A)
+    float sx;          // bins per unit of -x: kNucBins / -x_lo
+    uint32_t n_cand;   // candidates after the constraint
+    uint32_t use_mask; // the row's mask allows at least one id
+    uint32_t maxi;     // index of maxl (first)
+    uint32_t nr;       // ranges planned (pass B)
+    uint32_t flags;
+    uint32_t list_n;   // candidates compacted (pass C counter)
+    double log_z;      // raw log-normaliser (pass A)
+    double S;          // sum of the weights (pass B)
+    NucRange r[kNucRanges];
+};
 
 struct SampleArgs {
     const void* logits;
@@ -95,7 +123,12 @@ struct SampleArgs {
     uint32_t slices;         // workgroups per row on the sliced path
     uint32_t slice_len;      // elements per slice (multiple of 8)
     uint32_t all_sliced;     // 1: the host saw every row take a sliced mode
-    uint32_t pad_;
+    uint32_t nuc_row0;       // first row of this nucleus launch
+    // nucleus path workspace, for rows nuc_row0 .. nuc_row0 + kNucRows - 1
+    NucRow* nrow;            // kNucRows
+    uint32_t* nh_cnt;        // kNucRows x kMaxSlices x kNucBins
+    double* nh_mass;         // kNucRows x kMaxSlices x kNucBins
+    uint64_t* nlist;         // kNucRows x kNucList rank keys
 };
 
 struct VerifyArgs {

@@ -1,0 +1,1127 @@
+// Nucleus path for MI355X (gfx950): stochastic rows without top-k whose
+// candidate set stays large (top-p only, constrained rows, min-p over a flat
+// row), in three slice-parallel passes over device-resident logits.
+//
+// Each pass cuts a row into `slices` workgroups of 256 threads (one HBM read
+// of <= 8192 logits each, 32 per thread in registers), as the sliced kernel
+// does. Every workgroup publishes a record; the row's last-arriving
+// workgroup combines them. No workgroup ever waits for another.
+//
+//   A  nuc_stats:  penalties and the constraint (sampling.cpp:16-41, 70-86);
+//                  the raw max, log-normaliser and top-n (logprobs_from,
+//                  sampling.cpp:150-190); the penalised candidate max (the
+//                  reference's maxl) and min. The last arrival writes the
+//                  row state and the top-n logprobs.
+//   B  nuc_hist:   the reference's weights exp((double)((p - maxl) * inv_t))
+//                  (sampling.cpp:101-109) binned by the tempered offset into
+//                  kNucBins bins (counts, f64 masses). The last arrival
+//                  merges the row's histograms and plans the few bin ranges
+//                  that can hold the top-p crossing, the min-p cut and the
+//                  draw (sampling.cpp:113-147).
+//   C  nuc_select: the candidates of those ranges are compacted into a row
+//                  list; the last arrival rebuilds each range's sub-bin
+//                  masses, sorts only the decisive sub-bins' candidates (rank
+//                  key: logit, then id) and walks them in the reference's
+//                  order: top-p, min-p, kept mass, the draw.
+//
+// Bin-level decisions carry a 1e-10 relative guard (a target that close to
+// a bin or sub-bin edge takes both neighbours). A plan that would compact
+// more than kNucList candidates, or a decisive sub-bin group larger than
+// one wave can rank, resolves the row with the exact single-workgroup path.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "lcs_device.hpp"
+#include "lcs_exact.hpp"
+#include "lcs_internal.hpp"
+
+namespace lcs {
+
+namespace {
+constexpr int NT = kSliceThreads;
+constexpr int kNW = NT / kWave;
+constexpr uint32_t kNone = 0xffffffffu;
+constexpr uint32_t kNucCand = 128;     // top-n candidates one slice holds
+constexpr uint32_t kGroupMax = 4 * kWave;  // candidates one decisive group may hold
+constexpr float kL2E = 1.4426950408889634f;
+constexpr double kGuard = 1e-10;
+}  // namespace
+
+// ------------------------------------------------------------------ LDS ----
+struct NucLocal {
+    float lmax[NT];
+    float t_s;
+    uint32_t ncand, nloc, last, gbase;
+    uint32_t bmap[kNucBins / 32];   // planned bins (select pass)
+    float mraw[kNW];
+    double sraw[kNW];
+    float mpen[kNW], npen[kNW], mmsk[kNW], nmsk[kNW];
+    uint32_t ipen[kNW], imsk[kNW], nall[kNW];
+    uint64_t ck[kNucCand];
+    // select-pass finalize
+    uint32_t ng;               // group size
+    uint32_t out_flag;
+    double out_m;              // kept mass at the top-p crossing
+    SampleArgs args;           // for the exact fallback
+};
+struct NucFinC {
+    uint32_t scnt[kNucRanges][kNucSub];   // sub-bin counts, then inclusive
+    double smass[kNucRanges][kNucSub];    // sub-bin masses, then inclusive
+    uint64_t gkey[kGroupMax];             // decisive group (rank keys)
+    uint64_t gsorted[kGroupMax];
+    double gw[kGroupMax];                 // weights in rank order
+};
+struct NucSmem {
+    union {
+        uint32_t ovr[kSliceMax];          // penalty words per slice position
+        uint4 ovr4[kSliceMax / 4];
+        struct {
+            uint32_t cnt[kNucBins];
+            double mass[kNucBins];
+        } h;                              // histogram (pass B)
+        uint64_t lkeys[kNucList];         // compacted candidates (pass C)
+        uint64_t top[kMaxSlices * kTopMax];   // top-n merge (pass A finalize)
+        NucFinC fc;                       // select finalize
+        ExactSmem<kSliceThreads, kFbBins, kFbCap, kFbHistCap> ex;
+    } u;
+    NucLocal l;
+};
+__shared__ NucSmem g_nuc;
+
+// ---------------------------------------------------- one slice of a row ----
+// The slice's logits (penalised in place once apply() ran), its mask words
+// and the penalty bookkeeping, for one thread.
+template <int G>
+struct SliceIn {
+    static constexpr int NG = kSliceElems / G;
+    static constexpr int HC = 8;
+    const void* rowp;
+    uint32_t lo, hi, len, V;
+    const uint32_t* mrow;
+    bool hany, htwo;
+    uint32_t hoff, hstart, nwin_h;
+    uint4 raw[NG];
+    uint32_t mbits;    // bit q: element q allowed (load_mask)
+    uint32_t hA[HC], hB[HC];
+    uint32_t oA, oB;
+    float rA[HC], rB[HC];
+    float v[kSliceElems];
+
+    // logits first, then the history window ids and the mask words
+    __device__ __forceinline__ void start(const SampleArgs& a, uint32_t row, uint32_t slice,
+                                          const lcs_params& P, bool masked) {
+        const uint32_t tid = threadIdx.x;
+        V = a.vocab;
+        rowp = static_cast<const char*>(a.logits) + (uint64_t)row * a.row_stride * (G == 8 ? 2u : 4u);
+        lo = slice * a.slice_len;
+        hi = min(V, lo + a.slice_len);
+        len = hi - lo;
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            const uint32_t e0 = lo + (j * NT + tid) * G;
+            raw[j] = load16(rowp, (e0 < hi ? e0 : lo) / G);
+        }
+        mrow = masked ? a.mask + (uint64_t)row * a.mask_words : nullptr;
+        const bool pen = penalties_active(P) && a.hist_off != nullptr;
+        uint32_t hn = 0;
+        hoff = 0;
+        hstart = 0;
+        if (pen) {
+            hoff = scalar_load(a.hist_off + row);
+            hn = scalar_load(a.hist_off + row + 1) - hoff;
+            hstart = hn > P.repeat_last_n ? hn - P.repeat_last_n : 0u;
+        }
+        hany = pen && hn > hstart;
+        nwin_h = hn - hstart;
+        htwo = hany && nwin_h > (uint32_t)(NT * HC);
+        oA = oB = 0;
+        if (hany) {
+#pragma unroll
+            for (int k = 0; k < HC; ++k) {
+                const uint32_t i = (uint32_t)k * NT + tid;
+                hA[k] = (uint32_t)a.hist_ids[hoff + hstart + (i < nwin_h ? i : nwin_h - 1)];
+            }
+        }
+        if (htwo) {
+#pragma unroll
+            for (int k = 0; k < HC; ++k) {
+                const uint32_t i = (uint32_t)(k + HC) * NT + tid;
+                hB[k] = (uint32_t)a.hist_ids[hoff + hstart + (i < nwin_h ? i : nwin_h - 1)];
+            }
+        }
+        mbits = 0xffffffffu;
+    }
+    // the thread's 32 mask bits (bit q for element q), where the row is masked
+    __device__ __forceinline__ void load_mask() {
+        if (!mrow) return;
+        uint32_t w[NG];
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            const uint32_t e0 = lo + (j * NT + threadIdx.x) * G;
+            const uint32_t ee = e0 < hi ? e0 : lo;
+            w[j] = mrow[ee >> 5] >> (ee & 31u);
+        }
+        uint32_t m = 0;
+#pragma unroll
+        for (int j = 0; j < NG; ++j) m |= (w[j] & ((1u << G) - 1u)) << (j * G);
+        mbits = m;
+    }
+    __device__ __forceinline__ void clear(NucSmem& sm) const {
+#pragma unroll
+        for (int i = 0; i < (int)(kSliceMax / 4 / NT); ++i) sm.u.ovr4[i * NT + threadIdx.x] = make_uint4(0, 0, 0, 0);
+    }
+    // values; positions past the slice read as -inf
+    __device__ __forceinline__ void decode() {
+        const uint32_t tid = threadIdx.x, wv = tid / kWave;
+        const float NEG = -__builtin_huge_valf();
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            float t[G];
+            ::lcs::decode<G>(raw[j], t);
+#pragma unroll
+            for (int k = 0; k < G; ++k) v[j * G + k] = t[k];
+            if (lo + (j * NT + wv * kWave + kWave) * G > hi) {
+                const uint32_t e0 = lo + (j * NT + tid) * G;
+#pragma unroll
+                for (int k = 0; k < G; ++k) v[j * G + k] = e0 + k < hi ? v[j * G + k] : NEG;
+            }
+        }
+    }
+    __device__ __forceinline__ uint32_t eid(int q) const {
+        return lo + ((q / G) * NT + threadIdx.x) * G + (uint32_t)(q % G);
+    }
+    // a candidate: inside the slice and, when the row's mask is used, allowed
+    __device__ __forceinline__ bool cand(int q, bool use_mask) const {
+        const bool in = eid(q) < hi;
+        return use_mask ? in && ((mbits >> q) & 1u) : in;
+    }
+    // counts of the in-slice history ids; the thread whose increment finds 0
+    // owns the id and fetches its raw logit
+    __device__ __forceinline__ void count_gather(NucSmem& sm) {
+        const uint32_t tid = threadIdx.x;
+        auto one = [&](const uint32_t (&h)[HC], uint32_t c0, uint32_t& own, float (&r)[HC]) {
+#pragma unroll
+            for (int k = 0; k < HC; ++k) {
+                const uint32_t i = c0 + (uint32_t)k * NT + tid;
+                const uint32_t d = h[k] - lo;
+                if (i < nwin_h && h[k] < V && d < len && atomicAdd(&sm.u.ovr[d], 1u) == 0u) own |= 1u << k;
+            }
+#pragma unroll
+            for (int k = 0; k < HC; ++k) r[k] = load_elem(rowp, G == 8 ? LCS_BF16 : LCS_F32, ((own >> k) & 1u) ? h[k] : lo);
+        };
+        one(hA, 0, oA, rA);
+        if (htwo) one(hB, NT * HC, oB, rB);
+    }
+    // owners write penalised ^ raw bits (sampling.cpp:33-40 per distinct id)
+    __device__ __forceinline__ void put(NucSmem& sm, const lcs_params& P) const {
+        const double inv_rp = 1.0 / (double)P.repeat_penalty;
+        auto one = [&](const uint32_t (&h)[HC], const float (&r)[HC], uint32_t own) {
+#pragma unroll
+            for (int k = 0; k < HC; ++k) {
+                if ((own >> k) & 1u) {
+                    const uint32_t d = h[k] - lo;
+                    const float p = penalize_fast(r[k], sm.u.ovr[d], P, inv_rp);
+                    sm.u.ovr[d] = __float_as_uint(p) ^ __float_as_uint(r[k]);
+                }
+            }
+        };
+        one(hA, rA, oA);
+        if (htwo) one(hB, rB, oB);
+    }
+    // penalised values: raw ^ word (0 where no history id falls)
+    __device__ __forceinline__ void apply(const NucSmem& sm) {
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+#pragma unroll
+            for (int h4 = 0; h4 < G / 4; ++h4) {
+                const uint4 o = sm.u.ovr4[((j * NT + threadIdx.x) * G) / 4 + h4];
+                const uint32_t ob[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int qq = j * G + h4 * 4 + k;
+                    v[qq] = __uint_as_float(__float_as_uint(v[qq]) ^ ob[k]);
+                }
+            }
+        }
+    }
+    // the whole penalty step for passes that need no raw statistics
+    __device__ __forceinline__ void penalise(NucSmem& sm, const lcs_params& P) {
+        if (!hany) {
+            decode();
+            return;
+        }
+        clear(sm);
+        __syncthreads();
+        decode();
+        count_gather(sm);
+        __syncthreads();
+        put(sm, P);
+        __syncthreads();
+        apply(sm);
+        __syncthreads();
+    }
+};
+
+// Bins over the tempered offset x in [x_lo, 0]: f = -x * sx, bin 0 holds
+// the largest offsets.
+__device__ __forceinline__ float nuc_f(float x, float sx) { return fmul(-x, sx); }
+__device__ __forceinline__ uint32_t nuc_bin(float f) {
+    f = fminf(f, (float)(kNucBins - 1));
+    return f > 0.0f ? (uint32_t)f : 0u;
+}
+// Sub-bin of f inside the range [b0, b1] (kNucSub per range, in bin order).
+__device__ __forceinline__ uint32_t nuc_sub(float f, uint32_t b0, uint32_t b1) {
+    const float s = fmul(f - (float)b0, (float)kNucSub / (float)(b1 - b0 + 1));
+    const float c = fminf(s, (float)(kNucSub - 1));
+    return c > 0.0f ? (uint32_t)c : 0u;
+}
+
+// Arrival at the row's counter after this workgroup's stores are complete;
+// true in every thread of the last arrival.
+__device__ __forceinline__ bool nuc_arrive(uint32_t* counter, uint32_t S, NucSmem& sm) {
+    wait_all_memory();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = prev == S - 1;
+        if (last) st_dev(counter, 0u);
+        sm.l.last = last ? 1u : 0u;
+    }
+    __syncthreads();
+    return sm.l.last != 0u;
+}
+
+// Row and mode for a nucleus launch; false when this workgroup has no work.
+__device__ __forceinline__ bool nuc_row(const SampleArgs& a, uint32_t& row, uint32_t& slice, lcs_params& P,
+                                        bool& masked) {
+    const uint32_t S = a.slices;
+    row = a.nuc_row0 + blockIdx.x / S;
+    slice = blockIdx.x % S;
+    if (row >= a.rows || blockIdx.x / S >= kNucRows) return false;
+    P = scalar_load(a.params + row);
+    masked = a.mask != nullptr && (a.has_mask == nullptr || scalar_load_u8(a.has_mask + row) != 0);
+    return row_mode(P, masked, a.vocab) == kModeNucleus;
+}
+
+// ========================================================== A: nuc_stats ==
+// Record words (u64) of pass A, per slice:
+namespace nrec {
+constexpr uint32_t kHdr = 8;
+// 0: f32 raw max | u16 top-n entries << 32 | u16 flags << 48
+// 1: f64 sum exp(raw - raw max)
+// 2: f32 penalised max | u32 its index       3: same over allowed ids
+// 4: u32 allowed ids                          5: f32 penalised min | f32 allowed min
+constexpr uint32_t kTop = kHdr;               // kTopMax rank keys, ascending
+}  // namespace nrec
+
+template <int G>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nuc_stats(SampleArgs a) {
+    NucSmem& sm = g_nuc;
+    uint32_t row, slice;
+    lcs_params P;
+    bool masked;
+    if (!nuc_row(a, row, slice, P, masked)) return;
+    const uint32_t tid = threadIdx.x, S = a.slices;
+    const int lane = lane_id(), wv = (int)(tid / kWave);
+    const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
+    const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
+    const float NEG = -__builtin_huge_valf();
+    SliceIn<G> in;
+    in.start(a, row, slice, P, masked);
+    if (tid == 0) sm.l.ncand = 0;
+    if (in.hany) {
+        in.clear(sm);
+        __syncthreads();
+    }
+    in.decode();
+    float lm = NEG;
+#pragma unroll
+    for (int q = 0; q < kSliceElems; ++q) lm = fmaxf(lm, in.v[q]);
+    sm.l.lmax[tid] = lm;
+    if (in.hany) in.count_gather(sm);
+    __syncthreads();
+    // raw slice max; one wave finds the ntop-th largest lane maximum
+    float Ms;
+    {
+        float m4[kNW];
+#pragma unroll
+        for (int c = 0; c < kNW; ++c) m4[c] = sm.l.lmax[lane + c * kWave];
+        Ms = wave_max(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])));
+        if (ntop && wv == kNW - 1) {
+            uint32_t k4[kNW];
+#pragma unroll
+            for (int c = 0; c < kNW; ++c) k4[c] = fkey(m4[c]);
+            const float t = key_to_f(wave_kth_largest4(k4, ntop));
+            if (lane == 0) sm.l.t_s = t;
+        }
+    }
+    // raw sum of exp against the slice max (common exponent-offset error out)
+    double sw = 0.0;
+    if (want_lp && Ms != NEG) {
+        const float b = -Ms * kL2E;
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kSliceElems; ++q) s += __builtin_amdgcn_exp2f(fmaf(in.v[q], kL2E, b));
+        const double eb = ((double)Ms * (double)kL2E + (double)b) * 0.6931471805599453;
+        sw = (double)wave_sum_f(s) * (1.0 - eb + 0.5 * eb * eb);
+    }
+    if (lane == 0) { sm.l.mraw[wv] = Ms; sm.l.sraw[wv] = sw; }
+    if (in.hany) in.put(sm, P);
+    if (in.hany || ntop) __syncthreads();
+    // top-n candidates (raw values)
+    if (ntop) {
+        const float t = sm.l.t_s;
+        if (ballot(lm >= t)) {
+            if (lm >= t) {
+#pragma unroll
+                for (int q = 0; q < kSliceElems; ++q) {
+                    if (in.v[q] >= t) {
+                        const uint32_t e = in.eid(q);
+                        if (e < in.hi) {
+                            const uint32_t s = atomicAdd(&sm.l.ncand, 1u);
+                            if (s < kNucCand) sm.l.ck[s] = rank_key(in.v[q], e);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    if (in.hany) in.apply(sm);
+    in.load_mask();
+    // penalised candidate statistics over all ids and over the allowed ids
+    {
+        float bv = NEG, mv = NEG, nb = __builtin_huge_valf(), nm = __builtin_huge_valf();
+        uint32_t bi = kNone, mi = kNone, na = 0;
+#pragma unroll
+        for (int q = 0; q < kSliceElems; ++q) {
+            const uint32_t e = in.eid(q);
+            const bool ok = e < in.hi;
+            const float x = in.v[q];
+            if (ok && (bi == kNone || x > bv)) { bv = x; bi = e; }
+            if (ok) nb = fminf(nb, x);
+            if (in.mrow) {
+                const bool al = ok && ((in.mbits >> q) & 1u);
+                na += al ? 1u : 0u;
+                if (al && (mi == kNone || x > mv)) { mv = x; mi = e; }
+                if (al) nm = fminf(nm, x);
+            }
+        }
+        if (bi == kNone) bi = 0xfffffffeu;
+        wave_argmax(bv, bi);
+        nb = wave_min(nb);
+        if (in.mrow) {
+            if (mi == kNone) mi = 0xfffffffeu;
+            wave_argmax(mv, mi);
+            nm = wave_min(nm);
+            na = wave_sum_u(na);
+        }
+        if (lane == 0) {
+            sm.l.mpen[wv] = bv; sm.l.ipen[wv] = bi; sm.l.npen[wv] = nb;
+            sm.l.mmsk[wv] = mv; sm.l.imsk[wv] = mi; sm.l.nmsk[wv] = nm; sm.l.nall[wv] = na;
+        }
+    }
+    __syncthreads();
+    // ---- publish ----
+    uint64_t* myrec = reinterpret_cast<uint64_t*>(a.recs) + ((uint64_t)row * S + slice) * rec::kWords64;
+    if (wv == 0) {
+        const bool lw = lane < kNW;
+        const int wl = lw ? lane : 0;
+        const float mr = wave_max(lw ? sm.l.mraw[wl] : NEG);
+        // waves' raw sums rescaled to the slice max
+        const float mrw = lw ? sm.l.mraw[wl] : NEG;
+        const double ses = wave_sum(lw && want_lp && mrw != NEG ? sm.l.sraw[wl] * exp((double)mrw - (double)mr) : 0.0);
+        float ma = lw ? sm.l.mpen[wl] : NEG;
+        uint32_t ia = lw ? sm.l.ipen[wl] : kNone;
+        float mm = lw ? sm.l.mmsk[wl] : NEG;
+        uint32_t im = lw ? sm.l.imsk[wl] : kNone;
+        const float na_ = __builtin_huge_valf();
+        const float mnb = wave_min(lw ? sm.l.npen[wl] : na_);
+        const float mnm = wave_min(lw ? sm.l.nmsk[wl] : na_);
+        wave_argmax(ma, ia);
+        wave_argmax(mm, im);
+        const uint32_t na = wave_sum_u(lw ? sm.l.nall[wl] : 0u);
+        const uint32_t nts = min(ntop, in.len);
+        const uint32_t fl = (nts && sm.l.ncand > kNucCand) ? rec::kFlagCandOverflow : 0u;
+        uint64_t hw = 0;
+        switch (lane) {
+            case 0: hw = (uint64_t)__float_as_uint(mr) | ((uint64_t)nts << 32) | ((uint64_t)fl << 48); break;
+            case 1: hw = d_bits(ses); break;
+            case 2: hw = pack2(__float_as_uint(ma), ia); break;
+            case 3: hw = pack2(__float_as_uint(mm), im); break;
+            case 4: hw = (uint64_t)na; break;
+            case 5: hw = pack2(__float_as_uint(mnb), __float_as_uint(mnm)); break;
+            default: break;
+        }
+        if (lane < 6) st_dev_u64(myrec + lane, hw);
+    } else if (wv == 1) {
+        const uint32_t nts = min(ntop, in.len);
+        const uint32_t ncc = min(sm.l.ncand, kNucCand);
+        if (nts) {
+            uint64_t k[4];
+            uint32_t rk[4];
+            lds_rank4(sm.l.ck, ncc, k, rk);
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
+                if (e < ncc && rk[c] < nts) st_dev_u64(myrec + nrec::kTop + rk[c], k[c]);
+            }
+        }
+    }
+    if (!nuc_arrive(a.counters + row, S, sm)) return;
+
+    // ---- the row's state (wave 0) and logprobs (wave 1) ----
+    const uint64_t* recs = reinterpret_cast<const uint64_t*>(a.recs) + (uint64_t)row * S * rec::kWords64;
+    const bool mine = (uint32_t)lane < S;
+    const uint64_t* my = recs + (mine ? lane : 0) * rec::kWords64;
+    NucRow* nr = a.nrow + (row - a.nuc_row0);
+    if (wv == 0) {
+        const uint64_t h0 = ld_dev_u64(my + 0), h2 = ld_dev_u64(my + 2), h3 = ld_dev_u64(my + 3),
+                       h4 = ld_dev_u64(my + 4), h5 = ld_dev_u64(my + 5);
+        // a slice whose top-n candidates overflowed sends the row to the exact path
+        const bool ovf = ntop && ballot(mine && ((uint32_t)(h0 >> 48) & rec::kFlagCandOverflow));
+        const uint32_t na = wave_sum_u(mine ? (uint32_t)h4 : 0u);
+        const bool use_mask = masked && na > 0;
+        const uint64_t hb = use_mask ? h3 : h2;
+        float mx = mine ? __uint_as_float((uint32_t)hb) : NEG;
+        uint32_t mi = mine ? (uint32_t)(hb >> 32) : 0xfffffffeu;
+        wave_argmax(mx, mi);
+        const float mn = wave_min(mine ? __uint_as_float(use_mask ? (uint32_t)(h5 >> 32) : (uint32_t)h5)
+                                       : __builtin_huge_valf());
+        if (lane == 0) {
+            const float inv_t = fdiv(1.0f, P.temperature);
+            float x_lo = (mx == NEG) ? 0.0f : tempered(mn, mx, inv_t);
+            if (!(x_lo >= kNucXFloor)) x_lo = kNucXFloor;   // also NaN
+            nr->maxl = mx;
+            nr->maxi = mi;
+            nr->sx = x_lo < 0.0f ? fdiv((float)kNucBins, -x_lo) : 0.0f;
+            nr->n_cand = use_mask ? na : a.vocab;
+            nr->use_mask = use_mask ? 1u : 0u;
+            nr->flags = ovf ? kNucFallback : 0u;
+            nr->nr = 0u;
+            nr->list_n = 0u;
+        }
+    } else if (wv == 1 && want_lp) {
+        const uint64_t h0 = ld_dev_u64(my + 0), h1 = ld_dev_u64(my + 1);
+        uint64_t tk[kTopMax];
+#pragma unroll
+        for (int j = 0; j < (int)kTopMax; ++j) tk[j] = (uint32_t)j < ntop ? ld_dev_u64(my + nrec::kTop + j) : ~0ull;
+        const float m_raw = mine ? __uint_as_float((uint32_t)h0) : NEG;
+        const uint32_t nts = mine ? (uint32_t)(h0 >> 32) & 0xffffu : 0u;
+        const uint32_t flags = mine ? (uint32_t)(h0 >> 48) : 0u;
+        const double s_raw = mine ? bits_d(h1) : 0.0;
+        const float M = wave_max(m_raw);
+        const double z = wave_sum(mine && m_raw != NEG ? s_raw * exp((double)m_raw - (double)M) : 0.0);
+        const double log_z = log(z) + (double)M;
+        if (lane == 0) nr->log_z = log_z;
+        if (ntop && !ballot(mine && (flags & rec::kFlagCandOverflow))) {
+#pragma unroll
+            for (int j = 0; j < (int)kTopMax; ++j) {
+                if (mine && (uint32_t)j < ntop) sm.u.top[lane * kTopMax + j] = (uint32_t)j < nts ? tk[j] : ~0ull;
+            }
+            wave_sync();
+            uint32_t p = 0;
+            uint64_t myk = ~0ull;
+            for (uint32_t r = 0; r < ntop; ++r) {
+                const uint64_t head = mine && p < nts ? sm.u.top[lane * kTopMax + p] : ~0ull;
+                const uint32_t hk = (uint32_t)(head >> 32);
+                const uint32_t mk = wave_min_u(hk);
+                const uint64_t hit = ballot(head != ~0ull && hk == mk);
+                if (!hit) break;
+                const int wl = __builtin_ctzll(hit);
+                const uint64_t best = readlane_u64(head, wl);
+                if (lane == wl) ++p;
+                if ((uint32_t)lane == r) myk = best;
+            }
+            if ((uint32_t)lane < ntop) {
+                a.top_ids[(uint64_t)row * a.n_top + lane] = (int32_t)rank_idx(myk);
+                a.top_lp[(uint64_t)row * a.n_top + lane] = (float)((double)rank_val(myk) - log_z);
+            }
+        }
+    }
+}
+
+// =========================================================== B: nuc_hist ==
+template <int G>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nuc_hist(SampleArgs a) {
+    NucSmem& sm = g_nuc;
+    uint32_t row, slice;
+    lcs_params P;
+    bool masked;
+    if (!nuc_row(a, row, slice, P, masked)) return;
+    const uint32_t tid = threadIdx.x, S = a.slices;
+    const uint32_t wrow = row - a.nuc_row0;
+    NucRow* nr = a.nrow + wrow;
+    if (scalar_load(&nr->flags) & kNucFallback) return;   // resolved by the exact path
+    const float maxl = scalar_load(&nr->maxl);
+    const float sx = scalar_load(&nr->sx);
+    const bool use_mask = scalar_load(&nr->use_mask) != 0u;
+    SliceIn<G> in;
+    in.start(a, row, slice, P, masked);
+    in.penalise(sm, P);   // (ends on a barrier when it used the LDS)
+    if (use_mask) in.load_mask();
+    for (uint32_t b = tid; b < kNucBins; b += NT) { sm.u.h.cnt[b] = 0u; sm.u.h.mass[b] = 0.0; }
+    __syncthreads();
+    const float inv_t = fdiv(1.0f, P.temperature);
+#pragma unroll
+    for (int q = 0; q < kSliceElems; ++q) {
+        if (in.cand(q, use_mask)) {
+            const float x = tempered(in.v[q], maxl, inv_t);
+            const uint32_t b = nuc_bin(nuc_f(x, sx));
+            atomicAdd(&sm.u.h.cnt[b], 1u);
+            atomicAdd(&sm.u.h.mass[b], exp((double)x));
+        }
+    }
+    __syncthreads();
+    uint32_t* gc = a.nh_cnt + ((uint64_t)wrow * kMaxSlices + slice) * kNucBins;
+    double* gm = a.nh_mass + ((uint64_t)wrow * kMaxSlices + slice) * kNucBins;
+    for (uint32_t b = tid; b < kNucBins; b += NT) {
+        st_dev(gc + b, sm.u.h.cnt[b]);
+        st_dev_d(gm + b, sm.u.h.mass[b]);
+    }
+    if (!nuc_arrive(a.counters + row, S, sm)) return;
+
+    // ---- the row's histogram: merged, then inclusive prefix sums ----
+    constexpr uint32_t BPT = kNucBins / NT;   // bins per thread
+    static_assert(kNucBins % NT == 0, "bins per thread");
+    uint32_t c[BPT];
+    double m[BPT];
+#pragma unroll
+    for (uint32_t k = 0; k < BPT; ++k) { c[k] = 0u; m[k] = 0.0; }
+    const uint32_t* rc = a.nh_cnt + (uint64_t)wrow * kMaxSlices * kNucBins;
+    const double* rm = a.nh_mass + (uint64_t)wrow * kMaxSlices * kNucBins;
+    {
+        // slices in chunks of 10: a chunk's words are all issued before any is
+        // summed; sums run in slice order (deterministic)
+        constexpr uint32_t CH = 10;
+        for (uint32_t s0 = 0; s0 < S; s0 += CH) {
+            uint32_t cc[CH][BPT];
+            double mm[CH][BPT];
+#pragma unroll
+            for (uint32_t i = 0; i < CH; ++i) {
+                const uint32_t ss = s0 + i < S ? s0 + i : s0;
+#pragma unroll
+                for (uint32_t k = 0; k < BPT; ++k) {
+                    const uint32_t b = tid * BPT + k;
+                    cc[i][k] = ld_dev(rc + (uint64_t)ss * kNucBins + b);
+                    mm[i][k] = ld_dev_d(rm + (uint64_t)ss * kNucBins + b);
+                }
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < CH; ++i) {
+#pragma unroll
+                for (uint32_t k = 0; k < BPT; ++k) {
+                    if (s0 + i < S) { c[k] += cc[i][k]; m[k] += mm[i][k]; }
+                }
+            }
+        }
+    }
+    {
+        uint32_t cs = 0;
+        double ms = 0.0;
+#pragma unroll
+        for (uint32_t k = 0; k < BPT; ++k) { cs += c[k]; ms += m[k]; c[k] = cs; m[k] = ms; }
+        // exclusive prefix of the per-thread totals across the block
+        const int lane = lane_id(), w = (int)(tid / kWave);
+        const uint32_t ci = wave_scan_incl_u(cs);
+        const double mi = wave_scan_incl(ms);
+        if (lane == kWave - 1) { sm.l.nall[w] = ci; sm.l.sraw[w] = mi; }
+        __syncthreads();
+        uint32_t cb = ci - cs;
+        double mb = mi - ms;
+        for (int k = 0; k < w; ++k) { cb += sm.l.nall[k]; mb += sm.l.sraw[k]; }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t k = 0; k < BPT; ++k) {
+            sm.u.h.cnt[tid * BPT + k] = cb + c[k];
+            sm.u.h.mass[tid * BPT + k] = mb + m[k];
+        }
+        __syncthreads();
+    }
+    if (tid != 0) return;
+    // ---- plan (thread 0): the bin ranges each decision can need ----
+    const uint32_t* hc = sm.u.h.cnt;
+    const double* hm = sm.u.h.mass;
+    constexpr int NB = (int)kNucBins;
+    const double Stot = hm[NB - 1];
+    const uint32_t ncand = hc[NB - 1];
+    auto cb = [&](int b) -> uint32_t { return b > 0 ? hc[b - 1] : 0u; };
+    auto mb = [&](int b) -> double { return b > 0 ? hm[b - 1] : 0.0; };
+    auto first_mass = [&](double t) -> int {   // first bin whose inclusive mass >= t
+        int lo = 0, hi = NB - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (hm[mid] >= t) hi = mid; else lo = mid + 1;
+        }
+        return lo;
+    };
+    auto first_count = [&](uint32_t n) -> int {   // bin holding candidate position n - 1
+        int lo = 0, hi = NB - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (hc[mid] >= n) hi = mid; else lo = mid + 1;
+        }
+        return lo;
+    };
+    int ivl[kNucRanges + 3][2];
+    int niv = 0;
+    auto add = [&](int b0, int b1) { ivl[niv][0] = b0; ivl[niv][1] = b1; ++niv; };
+    uint32_t kp_lo = ncand, kp_hi = ncand, km_lo = ncand, km_hi = ncand;
+    if (P.top_p < 1.0f) {
+        const double T = (double)P.top_p * Stot;
+        const int b0 = first_mass(T * (1.0 - kGuard)), b1 = first_mass(T * (1.0 + kGuard));
+        add(b0, b1);
+        kp_lo = cb(b0) + 1u;
+        kp_hi = hc[b1];
+    }
+    if (P.min_p > 0.0f) {
+        // survivors have w >= min_p (w_0 = 1): offsets about ln(min_p) decide
+        const float xm = (float)log((double)P.min_p);
+        const float d = 1e-4f * fmaxf(1.0f, fabsf(xm));
+        const int b0 = (int)nuc_bin(nuc_f(xm + d, sx)), b1 = (int)nuc_bin(nuc_f(xm - d, sx));
+        add(b0, b1);
+        km_lo = max(1u, cb(b0));
+        km_hi = max(1u, hc[b1]);
+    }
+    const uint32_t keep_lo = max(1u, min(kp_lo, km_lo)), keep_hi = max(1u, min(kp_hi, km_hi));
+    const double K_lo = mb(first_count(keep_lo)), K_hi = hm[first_count(keep_hi)];
+    const double u = a.u[row];
+    const int kb = first_count(keep_hi);
+    const int d0 = min(first_mass(u * K_lo * (1.0 - kGuard)), kb);
+    const int d1 = min(first_mass(u * K_hi * (1.0 + kGuard)), kb);
+    add(d0, d1);
+    // merge overlapping or adjacent intervals (insertion sort by start)
+    for (int i = 1; i < niv; ++i) {
+        for (int j = i; j > 0 && ivl[j][0] < ivl[j - 1][0]; --j) {
+            const int t0 = ivl[j][0], t1 = ivl[j][1];
+            ivl[j][0] = ivl[j - 1][0]; ivl[j][1] = ivl[j - 1][1];
+            ivl[j - 1][0] = t0; ivl[j - 1][1] = t1;
+        }
+    }
+    int nm_ = 0;
+    for (int i = 0; i < niv; ++i) {
+        if (nm_ > 0 && ivl[i][0] <= ivl[nm_ - 1][1] + 1) {
+            ivl[nm_ - 1][1] = max(ivl[nm_ - 1][1], ivl[i][1]);
+        } else {
+            ivl[nm_][0] = ivl[i][0]; ivl[nm_][1] = ivl[i][1];
+            ++nm_;
+        }
+    }
+    uint32_t total = 0;
+    for (int i = 0; i < nm_; ++i) total += hc[ivl[i][1]] - cb(ivl[i][0]);
+    nr->S = Stot;
+    nr->nr = (uint32_t)nm_;
+    for (int i = 0; i < nm_ && i < (int)kNucRanges; ++i) {
+        NucRange g;
+        g.b0 = (uint32_t)ivl[i][0];
+        g.b1 = (uint32_t)ivl[i][1];
+        g.c0 = cb(ivl[i][0]);
+        g.cnt = hc[ivl[i][1]] - g.c0;
+        g.m0 = mb(ivl[i][0]);
+        g.m = hm[ivl[i][1]] - g.m0;
+        nr->r[i] = g;
+    }
+    nr->list_n = 0u;
+    if (total > kNucList || nm_ > (int)kNucRanges || ncand != scalar_load(&nr->n_cand)) nr->flags |= kNucFallback;
+}
+
+// ========================================================= C: nuc_select ==
+// Resolves one decision: the first candidate position, in rank order, whose
+// inclusive prefix mass reaches `target` (ranges and sub-bins give the mass
+// before each sub-bin; the sub-bins within kGuard of the target are
+// gathered and ranked). On return (every thread): sm.l.ng candidates in
+// gsorted with weights gw, and the group's count/mass before it.
+struct NucGroup {
+    uint32_t k;      // range
+    uint32_t s0, s1; // sub-bins
+    uint32_t c_before;
+    double m_before;
+    bool ok;
+};
+
+// The select pass's last arrival: exact decisions over the compacted ranges.
+// Every thread of the workgroup calls it, with the kernel arguments staged
+// in g_nuc.l.args; out of line so that its live values do not crowd the
+// compaction pass.
+template <int G>
+__device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exact) {
+    NucSmem& sm = g_nuc;
+    if (exact) {
+        exact_row<kSliceThreads, kFbBins, kFbCap, kFbHistCap, G>(sm.l.args, row, sm.u.ex);
+        return;
+    }
+    const SampleArgs a = uniform_args(sm.l.args);
+    const uint32_t tid = threadIdx.x;
+    const int lane = lane_id(), wv = (int)(tid / kWave);
+    const lcs_params P = scalar_load(a.params + row);
+    const uint32_t wrow = row - a.nuc_row0;
+    NucRow* nr = a.nrow + wrow;
+    const float maxl = nr->maxl;
+    const float sx = nr->sx;
+    const uint32_t nrg = nr->nr;
+    const float inv_t = fdiv(1.0f, P.temperature);
+    const uint64_t* list = a.nlist + (uint64_t)wrow * kNucList;
+    // =========== last arrival: exact decisions over the compacted ranges ===
+    const uint32_t n_all = ld_dev(&nr->list_n);
+    const uint32_t n = min(n_all, kNucList);
+    NucRange rg[kNucRanges];
+#pragma unroll
+    for (uint32_t k = 0; k < kNucRanges; ++k) {
+        if (k < nrg) rg[k] = nr->r[k];
+        else { rg[k].b0 = 1; rg[k].b1 = 0; rg[k].c0 = 0; rg[k].cnt = 0; rg[k].m0 = 0.0; rg[k].m = 0.0; }
+    }
+    const double Stot = nr->S;
+    const uint32_t ncand = nr->n_cand;
+    // sub-bin tables
+    for (uint32_t i = tid; i < kNucRanges * kNucSub; i += NT) {
+        sm.u.fc.scnt[i / kNucSub][i % kNucSub] = 0u;
+        sm.u.fc.smass[i / kNucSub][i % kNucSub] = 0.0;
+    }
+    if (tid == 0) sm.l.out_flag = n_all > kNucList ? 1u : 0u;
+    __syncthreads();
+    // range and sub-bin of a compacted candidate; its weight as the reference's
+    auto locate = [&](uint64_t key, uint32_t& k, uint32_t& s) -> float {
+        const float x = tempered(rank_val(key), maxl, inv_t);
+        const float f = nuc_f(x, sx);
+        const uint32_t b = nuc_bin(f);
+        k = kNucRanges;
+        s = 0u;
+#pragma unroll
+        for (uint32_t j = 0; j < kNucRanges; ++j) {
+            if (k == kNucRanges && b >= rg[j].b0 && b <= rg[j].b1) {
+                k = j;
+                s = nuc_sub(f, rg[j].b0, rg[j].b1);
+            }
+        }
+        return x;
+    };
+    for (uint32_t i = tid; i < n; i += NT) {
+        uint32_t k, s;
+        const float x = locate(ld_dev_u64(list + i), k, s);
+        if (k < kNucRanges) {
+            atomicAdd(&sm.u.fc.scnt[k][s], 1u);
+            atomicAdd(&sm.u.fc.smass[k][s], exp((double)x));
+        }
+    }
+    __syncthreads();
+    // inclusive sub-bin prefix sums, one wave per range (kNucSub = 2 per lane)
+    static_assert(kNucRanges == kNW && kNucSub == 2 * kWave, "one wave per range");
+    {
+        const uint32_t k = (uint32_t)wv;
+        const uint32_t c0 = sm.u.fc.scnt[k][2 * lane], c1 = sm.u.fc.scnt[k][2 * lane + 1];
+        const double m0 = sm.u.fc.smass[k][2 * lane], m1 = sm.u.fc.smass[k][2 * lane + 1];
+        const uint32_t ci = wave_scan_incl_u(c0 + c1);
+        const double mi = wave_scan_incl(m0 + m1);
+        sm.u.fc.scnt[k][2 * lane] = ci - c1;
+        sm.u.fc.scnt[k][2 * lane + 1] = ci;
+        sm.u.fc.smass[k][2 * lane] = mi - m1;
+        sm.u.fc.smass[k][2 * lane + 1] = mi;
+    }
+    __syncthreads();
+    // count / mass before sub-bin s of range k (row-level)
+    auto c_before = [&](uint32_t k, uint32_t s) -> uint32_t { return rg[k].c0 + (s > 0 ? sm.u.fc.scnt[k][s - 1] : 0u); };
+    auto m_before = [&](uint32_t k, uint32_t s) -> double { return rg[k].m0 + (s > 0 ? sm.u.fc.smass[k][s - 1] : 0.0); };
+    auto m_incl = [&](uint32_t k, uint32_t s) -> double { return rg[k].m0 + sm.u.fc.smass[k][s]; };
+    // first (range, sub-bin) whose inclusive mass reaches t (by rank order)
+    auto find_mass = [&](double t, uint32_t& k, uint32_t& s) -> bool {
+        for (uint32_t j = 0; j < nrg && j < kNucRanges; ++j) {
+            if (rg[j].m0 + rg[j].m >= t && rg[j].m0 <= t * (1.0 + kGuard)) {
+                int lo = 0, hi = (int)kNucSub - 1;
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (m_incl(j, (uint32_t)mid) >= t) hi = mid; else lo = mid + 1;
+                }
+                k = j;
+                s = (uint32_t)lo;
+                return true;
+            }
+        }
+        return false;
+    };
+    // Gathers the candidates of range k's sub-bins [s0, s1] into gkey and ranks
+    // them (wave 0) into gsorted with weights gw. Every thread calls it.
+    auto gather = [&](uint32_t k, uint32_t s0, uint32_t s1) -> uint32_t {
+        if (tid == 0) sm.l.ng = 0u;
+        __syncthreads();
+        for (uint32_t i = tid; i < n; i += NT) {
+            const uint64_t key = ld_dev_u64(list + i);
+            uint32_t kk, s;
+            locate(key, kk, s);
+            if (kk == k && s >= s0 && s <= s1) {
+                const uint32_t slot = atomicAdd(&sm.l.ng, 1u);
+                if (slot < kGroupMax) sm.u.fc.gkey[slot] = key;
+            }
+        }
+        __syncthreads();
+        const uint32_t ng = sm.l.ng;
+        if (ng <= kGroupMax && wv == 0) {
+            uint64_t kk[4];
+            uint32_t rk[4];
+            lds_rank4(sm.u.fc.gkey, ng, kk, rk);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
+                if (e < ng) {
+                    sm.u.fc.gsorted[rk[c]] = kk[c];
+                    sm.u.fc.gw[rk[c]] = exp((double)tempered(rank_val(kk[c]), maxl, inv_t));
+                }
+            }
+        }
+        __syncthreads();
+        return ng;
+    };
+
+    // ---- decisions; `fail` sends the row to the exact path ----
+    bool fail = sm.l.out_flag != 0u;
+    uint32_t keep = ncand;
+    double kept_sum = Stot;
+    uint64_t last_key = ~0ull;     // the candidate at position keep - 1, when known
+    // top-p (sampling.cpp:113-123): first position with cum = prefix / S >= top_p
+    uint32_t keep_p = ncand;
+    double mass_p = Stot;
+    uint64_t key_p = ~0ull;
+    if (!fail && P.top_p < 1.0f) {
+        const double tp = (double)P.top_p;
+        uint32_t k0, s0, k1, s1;
+        const bool f0 = find_mass(tp * Stot * (1.0 - kGuard), k0, s0);
+        const bool f1 = find_mass(tp * Stot * (1.0 + kGuard), k1, s1);
+        if (!f0 || !f1 || k0 != k1) {
+            fail = true;
+        } else {
+            const uint32_t ng = gather(k0, s0, s1);
+            if (ng > kGroupMax) {
+                fail = true;
+            } else {
+                // walk (one thread: the group is small)
+                if (tid == 0) {
+                    double m = m_before(k0, s0);
+                    uint32_t pos = kNone;
+                    for (uint32_t i = 0; i < ng; ++i) {
+                        m += sm.u.fc.gw[i];
+                        if (m / Stot >= tp) { pos = i; break; }
+                    }
+                    sm.l.ng = pos;
+                    sm.l.out_m = m;
+                }
+                __syncthreads();
+                const uint32_t pos = sm.l.ng;
+                if (pos == kNone) {
+                    fail = true;
+                } else {
+                    keep_p = c_before(k0, s0) + pos + 1u;
+                    mass_p = sm.l.out_m;
+                    key_p = sm.u.fc.gsorted[pos];
+                }
+                __syncthreads();
+            }
+        }
+    }
+    // min-p (sampling.cpp:125-133): survivors are the leading candidates with
+    // w / S >= min_p * (w_0 / S); w is non-increasing in rank order, so the
+    // survivors of the deciding range are counted without ordering them
+    uint32_t keep_m = ncand;
+    double mass_m = Stot;
+    uint64_t key_m = ~0ull;
+    if (!fail && P.min_p > 0.0f) {
+        const double thresh = (double)P.min_p * (1.0 / Stot);
+        const float xm = (float)log((double)P.min_p);
+        const uint32_t bm = nuc_bin(nuc_f(xm, sx));
+        uint32_t km = kNucRanges;
+        for (uint32_t j = 0; j < nrg && j < kNucRanges; ++j) if (km == kNucRanges && bm >= rg[j].b0 && bm <= rg[j].b1) km = j;
+        if (km == kNucRanges) {
+            fail = true;
+        } else {
+            // count, mass and last (largest rank key) survivor of range km
+            uint32_t cnt = 0;
+            double ms = 0.0;
+            uint64_t kl = 0ull;
+            for (uint32_t i = tid; i < n; i += NT) {
+                const uint64_t key = ld_dev_u64(list + i);
+                uint32_t kk, s;
+                const float x = locate(key, kk, s);
+                const double w = kk == km ? exp((double)x) : 0.0;
+                if (kk == km && w / Stot >= thresh) {
+                    ++cnt;
+                    ms += w;
+                    kl = key > kl ? key : kl;
+                }
+            }
+            const uint32_t tc = block_sum_u<NT>(cnt, sm.l.nall);
+            const double tm = block_sum<NT>(ms, sm.l.sraw);
+            const uint64_t tk = ~block_min_u64<NT>(~kl, sm.l.ck);
+            keep_m = max(1u, rg[km].c0 + tc);
+            mass_m = rg[km].m0 + tm;
+            key_m = tc > 0 ? tk : ~0ull;
+            if (rg[km].c0 + tc == 0) fail = true;   // (w_0 always survives)
+        }
+    }
+    if (!fail) {
+        if (keep_p <= keep_m && keep_p < ncand) {
+            keep = keep_p; kept_sum = mass_p; last_key = key_p;
+        } else if (keep_m < keep_p) {
+            keep = keep_m; kept_sum = mass_m; last_key = key_m;
+            if (key_m == ~0ull) fail = true;
+        } else {
+            keep = ncand; kept_sum = Stot; last_key = ~0ull;
+        }
+    }
+    // draw (sampling.cpp:135-147): r = u * kept_sum; the first kept candidate
+    // whose inclusive prefix reaches r, else the last kept one
+    int32_t chosen = -1;
+    if (!fail) {
+        const double r0 = a.u[row] * (kept_sum - 0.0) + 0.0;
+        uint32_t k0, s0, k1, s1;
+        const bool f0 = find_mass(r0 * (1.0 - kGuard), k0, s0);
+        bool f1 = find_mass(r0 * (1.0 + kGuard), k1, s1);
+        if (f1 && k1 != k0) { k1 = k0; s1 = kNucSub - 1; }
+        if (!f0) {
+            fail = true;
+        } else {
+            if (!f1) { k1 = k0; s1 = kNucSub - 1; }
+            const uint32_t ng = gather(k0, s0, s1);
+            if (ng > kGroupMax) {
+                fail = true;
+            } else {
+                if (tid == 0) {
+                    double r = r0 - m_before(k0, s0);
+                    const uint32_t cb0 = c_before(k0, s0);
+                    int32_t id = -1;
+                    for (uint32_t i = 0; i < ng && cb0 + i < keep; ++i) {
+                        r -= sm.u.fc.gw[i];
+                        if (r <= 0.0) { id = (int32_t)rank_idx(sm.u.fc.gsorted[i]); break; }
+                    }
+                    if (id < 0) {
+                        // ran past the group: the reference's fallback is the last
+                        // kept candidate, known when a cut produced `keep`
+                        if (last_key != ~0ull && (cb0 + ng >= keep)) id = (int32_t)rank_idx(last_key);
+                    }
+                    sm.l.ng = (uint32_t)id;
+                }
+                __syncthreads();
+                chosen = (int32_t)sm.l.ng;
+                if (chosen < 0) fail = true;
+            }
+        }
+    }
+    if (fail) {
+        // every thread agrees (all decisions above are block-uniform)
+        exact_row<kSliceThreads, kFbBins, kFbCap, kFbHistCap, G>(sm.l.args, row, sm.u.ex);
+        return;
+    }
+    if (tid == 0) {
+        a.ids[row] = chosen;
+        if (a.flags & LCS_WANT_LOGPROBS) {
+            const int32_t lid = a.lp_ids ? a.lp_ids[row] : chosen;
+            const bool inr = lid >= 0 && (uint32_t)lid < a.vocab;
+            const void* rowp = static_cast<const char*>(a.logits) + (uint64_t)row * a.row_stride * (G == 8 ? 2u : 4u);
+            const float raw = inr ? load_elem(rowp, G == 8 ? LCS_BF16 : LCS_F32, (uint32_t)lid) : 0.0f;
+            a.chosen_lp[row] = inr ? (float)((double)raw - nr->log_z) : 0.0f;
+        }
+        if (a.diag) {
+            lcs_row_diag dg{};
+            dg.n_cand = ncand;
+            dg.keep = keep;
+            dg.maxl = maxl;
+            dg.boundary = last_key != ~0ull ? rank_val(last_key) : maxl;
+            dg.path = LCS_PATH_NUCLEUS;
+            dg.sum = Stot;
+            dg.kept_sum = kept_sum;
+            a.diag[row] = dg;
+        }
+    }
+}
+
+
+template <int G>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nuc_select(SampleArgs a) {
+    NucSmem& sm = g_nuc;
+    uint32_t row, slice;
+    lcs_params P;
+    bool masked;
+    if (!nuc_row(a, row, slice, P, masked)) return;
+    const uint32_t tid = threadIdx.x, S = a.slices;
+    const int lane = lane_id(), wv = (int)(tid / kWave);
+    const uint32_t wrow = row - a.nuc_row0;
+    NucRow* nr = a.nrow + wrow;
+    const uint32_t flags = scalar_load(&nr->flags);
+    const bool exact = (flags & kNucFallback) != 0u;
+    if (exact && slice != 0) return;   // slice 0 resolves the row by the exact path
+    bool run_fin = exact;
+    if (!exact) {
+    const float maxl = scalar_load(&nr->maxl);
+    const float sx = scalar_load(&nr->sx);
+    const bool use_mask = scalar_load(&nr->use_mask) != 0u;
+    SliceIn<G> in;
+    in.start(a, row, slice, P, masked);
+    in.penalise(sm, P);
+    if (use_mask) in.load_mask();
+    // the planned bins as a bitmap in LDS
+    if (tid < kNucBins / 32) {
+        const uint32_t nrg = scalar_load(&nr->nr);
+        uint32_t w = 0;
+        for (uint32_t k = 0; k < nrg && k < kNucRanges; ++k) {
+            const uint32_t b0 = scalar_load(&nr->r[k].b0), b1 = scalar_load(&nr->r[k].b1);
+            for (uint32_t j = 0; j < 32; ++j) {
+                const uint32_t b = tid * 32 + j;
+                if (b >= b0 && b <= b1) w |= 1u << j;
+            }
+        }
+        sm.l.bmap[tid] = w;
+    }
+    if (tid == 0) sm.l.nloc = 0u;
+    __syncthreads();
+    const float inv_t = fdiv(1.0f, P.temperature);
+#pragma unroll
+    for (int q = 0; q < kSliceElems; ++q) {
+        if (in.cand(q, use_mask)) {
+            const uint32_t b = nuc_bin(nuc_f(tempered(in.v[q], maxl, inv_t), sx));
+            if ((sm.l.bmap[b >> 5] >> (b & 31u)) & 1u) {
+                const uint32_t s = atomicAdd(&sm.l.nloc, 1u);
+                if (s < kNucList) sm.u.lkeys[s] = rank_key(in.v[q], in.eid(q));
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t nloc = min(sm.l.nloc, kNucList);
+    if (tid == 0) {
+        sm.l.gbase = __hip_atomic_fetch_add(&nr->list_n, nloc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    uint64_t* list = a.nlist + (uint64_t)wrow * kNucList;
+    {
+        const uint32_t base = sm.l.gbase;
+        for (uint32_t i = tid; i < nloc; i += NT) {
+            if (base + i < kNucList) st_dev_u64(list + base + i, sm.u.lkeys[i]);
+        }
+    }
+    run_fin = nuc_arrive(a.counters + row, S, sm);
+    }
+    if (!run_fin) return;
+    if (tid == 0) stash_args(&sm.l.args);
+    __syncthreads();
+    nuc_select_fin<G>(row, exact);
+}
+
+// Host launchers: three passes per chunk of kNucRows rows.
+hipError_t launch_nucleus(const SampleArgs& a0, hipStream_t st) {
+    for (uint32_t r0 = 0; r0 < a0.rows; r0 += kNucRows) {
+        SampleArgs a = a0;
+        a.nuc_row0 = r0;
+        const uint32_t nrows = min(kNucRows, a0.rows - r0);
+        const dim3 grid(nrows * a.slices), block(NT);
+        if (a.dtype == LCS_BF16) {
+            hipLaunchKernelGGL(nuc_stats<8>, grid, block, 0, st, a);
+            hipLaunchKernelGGL(nuc_hist<8>, grid, block, 0, st, a);
+            hipLaunchKernelGGL(nuc_select<8>, grid, block, 0, st, a);
+        } else {
+            hipLaunchKernelGGL(nuc_stats<4>, grid, block, 0, st, a);
+            hipLaunchKernelGGL(nuc_hist<4>, grid, block, 0, st, a);
+            hipLaunchKernelGGL(nuc_select<4>, grid, block, 0, st, a);
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace lcs

@@ -271,3 +271,53 @@ def test_topk_rows_on_the_sliced_path(sampler):
     paths = g["diag"]["path"]
     assert (paths[[i for i, k in enumerate(ks) if k <= 64]] == 5).all(), paths.tolist()
     assert paths[ks.index(65)] == 4
+
+
+def test_nucleus_rows(sampler):
+    """Stochastic rows without top_k run on the sliced nucleus path (path 6):
+    top-p only, constrained rows (with and without min-p), plain temperature,
+    penalties, extreme temperatures, a mask that allows nothing, f32 and bf16.
+    Rows whose decisive group is too large finish on the exact path (4)."""
+    for name, rows in (("c3", 40), ("c4", 24)):
+        w = W.make(name, rows=rows, set_index=21)
+        g = run(sampler, w)
+        compare(w, g, O.sample_batch(w, threads=16), f"nucleus-{name}", expect_paths={4, 6})
+        assert (g["diag"]["path"] == 6).mean() >= 0.9, g["diag"]["path"].tolist()
+
+    base = W.make("c2", rows=16, set_index=23)
+    V = base.vocab
+    p = base.params.copy()
+    p["top_k"] = 0
+    p["min_p"] = 0.0
+    cfg = [  # temperature, top_p, min_p, penalties on, masked (fraction allowed)
+        (0.7, 0.9, 0.0, True, None), (1.0, 1.0, 0.0, True, None), (1.5, 0.5, 0.0, False, None),
+        (0.05, 0.9, 0.0, False, None), (4.0, 0.99, 0.0, True, None), (1.0, 0.1, 0.0, False, None),
+        (0.7, 0.9, 0.05, True, 0.3), (1.0, 1.0, 0.2, False, 0.02), (0.8, 0.95, 0.0, True, 0.0),
+        (1.0, 0.95, 0.0, False, 1e-4), (1.2, 1.0, 0.0, False, 0.5), (0.9, 0.8, 0.01, True, 0.1),
+        (2.0, 0.999, 0.0, False, None), (0.3, 0.7, 0.0, True, 0.05), (1.0, 0.9, 0.0, True, None),
+        (0.6, 1.0, 0.3, True, 1.0),
+    ]
+    bits = np.ones((base.rows, V), dtype=bool)
+    has = np.zeros(base.rows, dtype=bool)
+    rng = np.random.default_rng(31)
+    for r, (t, tp, mp, pen, frac) in enumerate(cfg):
+        p["temperature"][r], p["top_p"][r], p["min_p"][r] = t, tp, mp
+        if not pen:
+            p["repeat_penalty"][r], p["frequency_penalty"][r], p["presence_penalty"][r] = 1.0, 0.0, 0.0
+        if frac is not None:
+            has[r] = True
+            bits[r] = rng.random(V) < frac
+    masked = W.Workload("nucleus-mix", base.rows, V, "f32", base.logits, p, base.seeds, base.u,
+                        base.hist_off, base.hist_ids, W.pack_mask(bits), 5, True)
+    hm = has.astype(np.uint8)
+    g = run(sampler, masked, has_mask=sampler.torch.from_numpy(hm).cuda())
+    compare(masked, g, O.sample_batch(masked, threads=16, has_mask=hm), "nucleus-mix", expect_paths={4, 6})
+    assert (g["diag"]["path"] == 6).sum() >= 12, g["diag"]["path"].tolist()
+
+    bf = W.make("c3", rows=8, set_index=25)
+    b16 = W.bf16_rne(bf.logits)
+    wb = W.Workload("nucleus-bf16", bf.rows, bf.vocab, "bf16", b16, bf.params, bf.seeds, bf.u,
+                    n_top=2, want_logprobs=True)
+    w32 = W.Workload("nucleus-bf16-as-f32", bf.rows, bf.vocab, "f32", W.bf16_to_f32(b16), bf.params,
+                     bf.seeds, bf.u, n_top=2, want_logprobs=True)
+    compare(w32, run(sampler, wb), O.sample_batch(w32, threads=16), "nucleus-bf16", expect_paths={4, 6})
