@@ -83,6 +83,41 @@ __device__ __forceinline__ float tempered(float p, float maxl, float inv_t) {
     return fmul(fsub(p, maxl), inv_t);
 }
 
+// exp(x) in f64, inline and branch-free, for the weights exp((double)x) of
+// tempered offsets x <= 0 (sampling.cpp:104-105). x = n ln2 + r with
+// n = rint(x / ln2), |r| <= ln2 / 2; ln2 is split Cody-Waite style into a
+// 32-bit head (n * head exact for |n| < 2^21) and a tail. exp(r) is the
+// Taylor polynomial of degree 13 (truncation below 5e-18 relative) in Horner
+// form, scaled by 2^n. Results are within 1 ulp of a correctly rounded exp
+// for x >= -708; x < -745 gives 0 (also -inf).
+__device__ __forceinline__ double exp_f64(double x) {
+    constexpr double kLn2Hi = 0x1.62e42ff000000p-1;
+    constexpr double kLn2Lo = -0x1.718432a1b0e26p-35;
+    constexpr double kInvLn2 = 1.4426950408889634;
+    constexpr double f2 = 2.0, f3 = f2 * 3, f4 = f3 * 4, f5 = f4 * 5, f6 = f5 * 6, f7 = f6 * 7,
+                     f8 = f7 * 8, f9 = f8 * 9, f10 = f9 * 10, f11 = f10 * 11, f12 = f11 * 12, f13 = f12 * 13;
+    const double n = __builtin_rint(x * kInvLn2);
+    double r = __builtin_fma(-n, kLn2Hi, x);
+    r = __builtin_fma(-n, kLn2Lo, r);
+    double p = 1.0 / f13;
+    p = __builtin_fma(p, r, 1.0 / f12);
+    p = __builtin_fma(p, r, 1.0 / f11);
+    p = __builtin_fma(p, r, 1.0 / f10);
+    p = __builtin_fma(p, r, 1.0 / f9);
+    p = __builtin_fma(p, r, 1.0 / f8);
+    p = __builtin_fma(p, r, 1.0 / f7);
+    p = __builtin_fma(p, r, 1.0 / f6);
+    p = __builtin_fma(p, r, 1.0 / f5);
+    p = __builtin_fma(p, r, 1.0 / f4);
+    p = __builtin_fma(p, r, 1.0 / f3);
+    p = __builtin_fma(p, r, 0.5);
+    p = __builtin_fma(p, r, 1.0);
+    p = __builtin_fma(p, r, 1.0);
+    const int e = x < -745.0 ? 0 : (int)n;
+    const double y = __builtin_ldexp(p, e);
+    return x < -745.0 ? 0.0 : y;
+}
+
 // ------------------------------------------------------ wave reductions ----
 // Wave64 reductions and scans on DPP lane moves (VALU, no LDS round trip):
 // quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror and row_mirror give every

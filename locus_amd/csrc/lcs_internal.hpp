@@ -84,7 +84,7 @@ struct NucRange {
 };
 struct NucRow {
     float maxl;        // penalised candidate max (pass A)
-    float sx;          // bins per unit of -x: kNucBins / -x_lo
+    float sx;          // bins per unit of -x: a power of two <= kNucBins / -x_lo
     uint32_t n_cand;   // candidates after the constraint
     uint32_t use_mask; // the row's mask allows at least one id
     uint32_t maxi;     // index of maxl (first)

@@ -47,12 +47,15 @@ constexpr uint32_t kGroupMax = 4 * kWave;  // candidates one decisive group may 
 constexpr float kL2E = 1.4426950408889634f;
 constexpr double kGuard = 1e-10;
 }  // namespace
+// 1/k! for k = 10, 9, ..., 3
+__constant__ double kInvFact[8] = {1.0 / 3628800.0, 1.0 / 362880.0, 1.0 / 40320.0, 1.0 / 5040.0,
+                                   1.0 / 720.0,     1.0 / 120.0,    1.0 / 24.0,    1.0 / 6.0};
 
 // ------------------------------------------------------------------ LDS ----
 struct NucLocal {
     float lmax[NT];
     float t_s;
-    uint32_t ncand, nloc, last, gbase;
+    uint32_t ncand, last, gbase;
     uint32_t bmap[kNucBins / 32];   // planned bins (select pass)
     float mraw[kNW];
     double sraw[kNW];
@@ -80,8 +83,8 @@ struct NucSmem {
             uint32_t cnt[kNucBins];
             double mass[kNucBins];
         } h;                              // histogram (pass B)
-        uint64_t lkeys[kNucList];         // compacted candidates (pass C)
         uint64_t top[kMaxSlices * kTopMax];   // top-n merge (pass A finalize)
+        uint64_t lkeys[kNucList];         // the slice's selections (pass C), thread order
         NucFinC fc;                       // select finalize
         ExactSmem<kSliceThreads, kFbBins, kFbCap, kFbHistCap> ex;
     } u;
@@ -191,6 +194,16 @@ struct SliceIn {
     __device__ __forceinline__ uint32_t eid(int q) const {
         return lo + ((q / G) * NT + threadIdx.x) * G + (uint32_t)(q % G);
     }
+    // bit q: element q is a candidate (in the slice and, when the row's mask
+    // is used, allowed)
+    __device__ __forceinline__ uint32_t cand_bits(bool use_mask) const {
+        uint32_t cm = use_mask ? mbits : 0xffffffffu;
+        if (lo + kSliceMax > hi) {
+#pragma unroll
+            for (int q = 0; q < kSliceElems; ++q) cm &= eid(q) < hi ? 0xffffffffu : ~(1u << q);
+        }
+        return cm;
+    }
     // a candidate: inside the slice and, when the row's mask is used, allowed
     __device__ __forceinline__ bool cand(int q, bool use_mask) const {
         const bool in = eid(q) < hi;
@@ -263,8 +276,9 @@ struct SliceIn {
     }
 };
 
-// Bins over the tempered offset x in [x_lo, 0]: f = -x * sx, bin 0 holds
-// the largest offsets.
+// Bins over the tempered offset x: f = -x * sx with sx a power of two (so f
+// is exact and the bin edges -b / sx lie on a dyadic grid), bin 0 holds the
+// largest offsets; sx <= kNucBins / -x_lo keeps every candidate at f <= kNucBins.
 __device__ __forceinline__ float nuc_f(float x, float sx) { return fmul(-x, sx); }
 __device__ __forceinline__ uint32_t nuc_bin(float f) {
     f = fminf(f, (float)(kNucBins - 1));
@@ -430,7 +444,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         const float mr = wave_max(lw ? sm.l.mraw[wl] : NEG);
         // waves' raw sums rescaled to the slice max
         const float mrw = lw ? sm.l.mraw[wl] : NEG;
-        const double ses = wave_sum(lw && want_lp && mrw != NEG ? sm.l.sraw[wl] * exp((double)mrw - (double)mr) : 0.0);
+        const double ses = wave_sum(lw && want_lp && mrw != NEG ? sm.l.sraw[wl] * exp_f64((double)mrw - (double)mr) : 0.0);
         float ma = lw ? sm.l.mpen[wl] : NEG;
         uint32_t ia = lw ? sm.l.ipen[wl] : kNone;
         float mm = lw ? sm.l.mmsk[wl] : NEG;
@@ -494,7 +508,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
             if (!(x_lo >= kNucXFloor)) x_lo = kNucXFloor;   // also NaN
             nr->maxl = mx;
             nr->maxi = mi;
-            nr->sx = x_lo < 0.0f ? fdiv((float)kNucBins, -x_lo) : 0.0f;
+            // bins per unit offset: the largest power of two in [4, 2^20]
+            // with kNucBins / sx >= -x_lo
+            float sxv = 1048576.0f;
+            if (x_lo < 0.0f) {
+                const float q = fdiv((float)kNucBins, -x_lo);
+                sxv = fminf(__uint_as_float(__float_as_uint(q) & 0xff800000u), 1048576.0f);
+            }
+            nr->sx = sxv;
             nr->n_cand = use_mask ? na : a.vocab;
             nr->use_mask = use_mask ? 1u : 0u;
             nr->flags = ovf ? kNucFallback : 0u;
@@ -511,7 +532,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         const uint32_t flags = mine ? (uint32_t)(h0 >> 48) : 0u;
         const double s_raw = mine ? bits_d(h1) : 0.0;
         const float M = wave_max(m_raw);
-        const double z = wave_sum(mine && m_raw != NEG ? s_raw * exp((double)m_raw - (double)M) : 0.0);
+        const double z = wave_sum(mine && m_raw != NEG ? s_raw * exp_f64((double)m_raw - (double)M) : 0.0);
         const double log_z = log(z) + (double)M;
         if (lane == 0) nr->log_z = log_z;
         if (ntop && !ballot(mine && (flags & rec::kFlagCandOverflow))) {
@@ -563,14 +584,53 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     for (uint32_t b = tid; b < kNucBins; b += NT) { sm.u.h.cnt[b] = 0u; sm.u.h.mass[b] = 0.0; }
     __syncthreads();
     const float inv_t = fdiv(1.0f, P.temperature);
+    // Bin b holds sum exp(d), d = x + (b + 1/2) / sx, |d| <= 1 / (2 sx); the
+    // finalize scales it by exp(-(b + 1/2) / sx). exp(d) is a Taylor
+    // polynomial: degree 7 for sx >= 16 (|d| <= 1/32), degree 10 otherwise
+    // (sx >= 4, |d| <= 1/8), truncation below 5e-17 relative. Candidates past
+    // the grid (f > kNucBins: x < -128, weight below e^-128) count with no
+    // mass. A wave skips an element position none of its lanes holds a
+    // candidate at (sparse constraint masks).
+    const double inv_sx = 1.0 / (double)sx;
+    const uint32_t cm = in.cand_bits(use_mask);
+    // Taylor coefficients 1/k! (k = 10 .. 3) from the scalar cache: each
+    // Horner step is one FMA with a scalar operand
+    double ck[8];
 #pragma unroll
-    for (int q = 0; q < kSliceElems; ++q) {
-        if (in.cand(q, use_mask)) {
-            const float x = tempered(in.v[q], maxl, inv_t);
-            const uint32_t b = nuc_bin(nuc_f(x, sx));
-            atomicAdd(&sm.u.h.cnt[b], 1u);
-            atomicAdd(&sm.u.h.mass[b], exp((double)x));
+    for (int k = 0; k < 8; ++k) ck[k] = scalar_load(&kInvFact[k]);
+    auto fill = [&](auto poly) {
+#pragma unroll
+        for (int q = 0; q < kSliceElems; ++q) {
+            if ((cm >> q) & 1u) {
+                const float x = tempered(in.v[q], maxl, inv_t);
+                const float f = nuc_f(x, sx);
+                const uint32_t b = nuc_bin(f);
+                const bool on = f <= (float)kNucBins;
+                const double d = on ? __builtin_fma((double)b + 0.5, inv_sx, (double)x) : 0.0;
+                const double pe = poly(d);
+                atomicAdd(&g_nuc.u.h.cnt[b], 1u);
+                atomicAdd(&g_nuc.u.h.mass[b], on ? pe : 0.0);
+            }
         }
+    };
+    if (sx >= 16.0f) {
+        fill([&](double d) {
+            double p = ck[3];
+#pragma unroll
+            for (int k = 4; k < 8; ++k) p = __builtin_fma(p, d, ck[k]);
+            p = __builtin_fma(p, d, 0.5);
+            p = __builtin_fma(p, d, 1.0);
+            return __builtin_fma(p, d, 1.0);
+        });
+    } else {
+        fill([&](double d) {
+            double p = ck[0];
+#pragma unroll
+            for (int k = 1; k < 8; ++k) p = __builtin_fma(p, d, ck[k]);
+            p = __builtin_fma(p, d, 0.5);
+            p = __builtin_fma(p, d, 1.0);
+            return __builtin_fma(p, d, 1.0);
+        });
     }
     __syncthreads();
     uint32_t* gc = a.nh_cnt + ((uint64_t)wrow * kMaxSlices + slice) * kNucBins;
@@ -616,6 +676,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
             }
         }
     }
+#pragma unroll
+    for (uint32_t k = 0; k < BPT; ++k) m[k] *= exp_f64(-((double)(tid * BPT + k) + 0.5) * inv_sx);
     {
         uint32_t cs = 0;
         double ms = 0.0;
@@ -638,30 +700,35 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         }
         __syncthreads();
     }
-    if (tid != 0) return;
-    // ---- plan (thread 0): the bin ranges each decision can need ----
+    if (tid >= kWave) return;
+    // ---- plan (wave 0, every lane computes the same plan): the bin ranges
+    // each decision can need ----
+    const int lane = lane_id();
     const uint32_t* hc = sm.u.h.cnt;
     const double* hm = sm.u.h.mass;
     constexpr int NB = (int)kNucBins;
+    constexpr int BL = NB / kWave;   // bins per lane, held in registers for the searches
+    double lm[BL];
+    uint32_t lc[BL];
+#pragma unroll
+    for (int j = 0; j < BL; ++j) { lm[j] = hm[lane * BL + j]; lc[j] = hc[lane * BL + j]; }
     const double Stot = hm[NB - 1];
     const uint32_t ncand = hc[NB - 1];
     auto cb = [&](int b) -> uint32_t { return b > 0 ? hc[b - 1] : 0u; };
     auto mb = [&](int b) -> double { return b > 0 ? hm[b - 1] : 0.0; };
-    auto first_mass = [&](double t) -> int {   // first bin whose inclusive mass >= t
-        int lo = 0, hi = NB - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (hm[mid] >= t) hi = mid; else lo = mid + 1;
-        }
-        return lo;
+    // the first bin whose inclusive mass (count) reaches t; the last bin when none does
+    auto first_of = [&](auto reach) -> int {
+        int f = BL;
+#pragma unroll
+        for (int j = BL - 1; j >= 0; --j) f = reach(j) ? j : f;
+        const uint64_t bal = ballot(f < BL);
+        if (!bal) return NB - 1;
+        const int L = __builtin_ctzll(bal);
+        return L * BL + __builtin_amdgcn_readlane(f, L);
     };
+    auto first_mass = [&](double t) -> int { return first_of([&](int j) { return lm[j] >= t; }); };
     auto first_count = [&](uint32_t n) -> int {   // bin holding candidate position n - 1
-        int lo = 0, hi = NB - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (hc[mid] >= n) hi = mid; else lo = mid + 1;
-        }
-        return lo;
+        return first_of([&](int j) { return lc[j] >= n; });
     };
     int ivl[kNucRanges + 3][2];
     int niv = 0;
@@ -709,6 +776,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     }
     uint32_t total = 0;
     for (int i = 0; i < nm_; ++i) total += hc[ivl[i][1]] - cb(ivl[i][0]);
+    if (lane != 0) return;
     nr->S = Stot;
     nr->nr = (uint32_t)nm_;
     for (int i = 0; i < nm_ && i < (int)kNucRanges; ++i) {
@@ -800,7 +868,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
         const float x = locate(ld_dev_u64(list + i), k, s);
         if (k < kNucRanges) {
             atomicAdd(&sm.u.fc.scnt[k][s], 1u);
-            atomicAdd(&sm.u.fc.smass[k][s], exp((double)x));
+            atomicAdd(&sm.u.fc.smass[k][s], exp_f64((double)x));
         }
     }
     __syncthreads();
@@ -863,12 +931,52 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
                 const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
                 if (e < ng) {
                     sm.u.fc.gsorted[rk[c]] = kk[c];
-                    sm.u.fc.gw[rk[c]] = exp((double)tempered(rank_val(kk[c]), maxl, inv_t));
+                    sm.u.fc.gw[rk[c]] = exp_f64((double)tempered(rank_val(kk[c]), maxl, inv_t));
                 }
             }
         }
         __syncthreads();
         return ng;
+    };
+
+    // First position i < ng of the ranked group (gsorted / gw) whose
+    // inclusive prefix weight P_i satisfies hit(i, P_i). Wave 0 scans four
+    // consecutive positions per lane; every thread gets the position (kNone
+    // when there is none) and P at it.
+    auto first_prefix = [&](uint32_t ng, auto hit, double& p_at) -> uint32_t {
+        if (wv == 0) {
+            double pre[4];
+            double run = 0.0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t i = 4u * (uint32_t)lane + (uint32_t)c;
+                run += i < ng ? g_nuc.u.fc.gw[i] : 0.0;
+                pre[c] = run;
+            }
+            const double incl = wave_scan_incl(run);
+            double base = __shfl_up(incl, 1);
+            base = lane == 0 ? 0.0 : base;
+            uint32_t first = 4u;
+#pragma unroll
+            for (int c = 3; c >= 0; --c) {
+                const uint32_t i = 4u * (uint32_t)lane + (uint32_t)c;
+                if (i < ng && hit(i, base + pre[c])) first = (uint32_t)c;
+            }
+            const uint64_t bal = ballot(first < 4u);
+            const int L = bal ? __builtin_ctzll(bal) : 0;
+            if (lane == L) {
+                double pa = 0.0;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) pa = (uint32_t)c == first ? base + pre[c] : pa;
+                g_nuc.l.ng = bal ? 4u * (uint32_t)L + first : kNone;
+                g_nuc.l.out_m = pa;
+            }
+        }
+        __syncthreads();
+        const uint32_t pos = g_nuc.l.ng;
+        p_at = g_nuc.l.out_m;
+        __syncthreads();
+        return pos;
     };
 
     // ---- decisions; `fail` sends the row to the exact path ----
@@ -892,27 +1000,17 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
             if (ng > kGroupMax) {
                 fail = true;
             } else {
-                // walk (one thread: the group is small)
-                if (tid == 0) {
-                    double m = m_before(k0, s0);
-                    uint32_t pos = kNone;
-                    for (uint32_t i = 0; i < ng; ++i) {
-                        m += sm.u.fc.gw[i];
-                        if (m / Stot >= tp) { pos = i; break; }
-                    }
-                    sm.l.ng = pos;
-                    sm.l.out_m = m;
-                }
-                __syncthreads();
-                const uint32_t pos = sm.l.ng;
+                // cum = (mass before the group + prefix) / S reaches top_p
+                const double mb0 = m_before(k0, s0);
+                double pm = 0.0;
+                const uint32_t pos = first_prefix(ng, [&](uint32_t, double pi) { return (mb0 + pi) / Stot >= tp; }, pm);
                 if (pos == kNone) {
                     fail = true;
                 } else {
                     keep_p = c_before(k0, s0) + pos + 1u;
-                    mass_p = sm.l.out_m;
+                    mass_p = mb0 + pm;
                     key_p = sm.u.fc.gsorted[pos];
                 }
-                __syncthreads();
             }
         }
     }
@@ -939,7 +1037,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
                 const uint64_t key = ld_dev_u64(list + i);
                 uint32_t kk, s;
                 const float x = locate(key, kk, s);
-                const double w = kk == km ? exp((double)x) : 0.0;
+                const double w = kk == km ? exp_f64((double)x) : 0.0;
                 if (kk == km && w / Stot >= thresh) {
                     ++cnt;
                     ms += w;
@@ -982,23 +1080,18 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
             if (ng > kGroupMax) {
                 fail = true;
             } else {
-                if (tid == 0) {
-                    double r = r0 - m_before(k0, s0);
-                    const uint32_t cb0 = c_before(k0, s0);
-                    int32_t id = -1;
-                    for (uint32_t i = 0; i < ng && cb0 + i < keep; ++i) {
-                        r -= sm.u.fc.gw[i];
-                        if (r <= 0.0) { id = (int32_t)rank_idx(sm.u.fc.gsorted[i]); break; }
-                    }
-                    if (id < 0) {
-                        // ran past the group: the reference's fallback is the last
-                        // kept candidate, known when a cut produced `keep`
-                        if (last_key != ~0ull && (cb0 + ng >= keep)) id = (int32_t)rank_idx(last_key);
-                    }
-                    sm.l.ng = (uint32_t)id;
+                // the first kept position whose prefix reaches r
+                const double r = r0 - m_before(k0, s0);
+                const uint32_t cb0 = c_before(k0, s0);
+                double pm = 0.0;
+                const uint32_t pos = first_prefix(ng, [&](uint32_t i, double pi) { return cb0 + i < keep && r - pi <= 0.0; }, pm);
+                if (pos != kNone) {
+                    chosen = (int32_t)rank_idx(sm.u.fc.gsorted[pos]);
+                } else if (last_key != ~0ull && cb0 + ng >= keep) {
+                    // ran past the group: the reference's fallback is the last
+                    // kept candidate, known when a cut produced `keep`
+                    chosen = (int32_t)rank_idx(last_key);
                 }
-                __syncthreads();
-                chosen = (int32_t)sm.l.ng;
                 if (chosen < 0) fail = true;
             }
         }
@@ -1068,29 +1161,51 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         }
         sm.l.bmap[tid] = w;
     }
-    if (tid == 0) sm.l.nloc = 0u;
     __syncthreads();
     const float inv_t = fdiv(1.0f, P.temperature);
+    // bit q: element q is a candidate inside a planned range
+    const uint32_t cm = in.cand_bits(use_mask);
+    uint32_t sel = 0;
 #pragma unroll
     for (int q = 0; q < kSliceElems; ++q) {
-        if (in.cand(q, use_mask)) {
+        if ((cm >> q) & 1u) {
             const uint32_t b = nuc_bin(nuc_f(tempered(in.v[q], maxl, inv_t), sx));
-            if ((sm.l.bmap[b >> 5] >> (b & 31u)) & 1u) {
-                const uint32_t s = atomicAdd(&sm.l.nloc, 1u);
-                if (s < kNucList) sm.u.lkeys[s] = rank_key(in.v[q], in.eid(q));
+            sel |= ((sm.l.bmap[b >> 5] >> (b & 31u)) & 1u) << q;
+        }
+    }
+    // the workgroup's selections in thread order (one block scan) staged in
+    // LDS, one reservation in the row list, coalesced stores; positions past
+    // kNucList are dropped (the finalize then sees list_n > kNucList and
+    // takes the exact path)
+    const uint32_t cnt = (uint32_t)__popc(sel);
+    const uint32_t incl = wave_scan_incl_u(cnt);
+    if (lane == kWave - 1) sm.l.nall[wv] = incl;
+    __syncthreads();
+    uint32_t pos = incl - cnt, tot = 0;
+#pragma unroll
+    for (int k = 0; k < kNW; ++k) {
+        const uint32_t t = sm.l.nall[k];
+        pos += k < wv ? t : 0u;
+        tot += t;
+    }
+    if (sel) {
+#pragma unroll
+        for (int q = 0; q < kSliceElems; ++q) {
+            if ((sel >> q) & 1u) {
+                if (pos < kNucList) sm.u.lkeys[pos] = rank_key(in.v[q], in.eid(q));
+                ++pos;
             }
         }
     }
-    __syncthreads();
-    const uint32_t nloc = min(sm.l.nloc, kNucList);
     if (tid == 0) {
-        sm.l.gbase = __hip_atomic_fetch_add(&nr->list_n, nloc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sm.l.gbase = tot ? __hip_atomic_fetch_add(&nr->list_n, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
     }
     __syncthreads();
-    uint64_t* list = a.nlist + (uint64_t)wrow * kNucList;
     {
         const uint32_t base = sm.l.gbase;
-        for (uint32_t i = tid; i < nloc; i += NT) {
+        const uint32_t n = min(tot, kNucList);
+        uint64_t* list = a.nlist + (uint64_t)wrow * kNucList;
+        for (uint32_t i = tid; i < n; i += NT) {
             if (base + i < kNucList) st_dev_u64(list + base + i, sm.u.lkeys[i]);
         }
     }
