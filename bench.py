@@ -102,24 +102,47 @@ def gpu_bench(name, steps, warmup):
     return w0, ev_ms / steps, wall / steps * 1e3, float(np.median(per)), nsets
 
 
-def cpu_baseline(name, budget_s=10.0):
+def copy_ceiling(mib: int = 1024, reps: int = 10) -> float:
+    """Measured HBM ceiling: GB/s of a plain device-to-device copy of `mib` MiB
+    (bytes read + bytes written over the copy's time), well past the 256 MB
+    Infinity Cache."""
+    import torch
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(2):
+        b.copy_(a)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        b.copy_(a)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) / reps * 1e-3
+    del a, b
+    return 2 * n * 4 / sec / 1e9
+
+
+def cpu_baseline(name, budget_s=10.0, threads=1):
     """The reference sampler (compiled from the reference's own sources,
-    oracle/_ref) on this host, one thread, rows in order as the reference
-    engine samples them (engine.cpp:541-557); the C++ restatement when the
-    reference build is absent."""
+    oracle/_ref) on this host, rows in order as the reference engine samples
+    them (engine.cpp:541-557) on one thread, or spread over `threads`
+    threads; the C++ restatement when the reference build is absent."""
     from oracle import pyoracle as O
     kind = "reference" if O.ref_available() else "port"
     w = W.make(name)
+    threads = max(1, min(threads, w.rows))
     rows_done = 0
     t0 = time.perf_counter()
     reps = 0
     while True:
         if w.n_seq:
-            O.verify(w, threads=1)
+            O.verify(w, threads=threads)
         elif kind == "reference":
-            O.ref_sample_batch(w, threads=1)
+            O.ref_sample_batch(w, threads=threads)
         else:
-            O.sample_batch(w, threads=1)
+            O.sample_batch(w, threads=threads)
         rows_done += w.rows
         reps += 1
         el = time.perf_counter() - t0
@@ -127,9 +150,9 @@ def cpu_baseline(name, budget_s=10.0):
             break
     if w.n_seq:
         kind = "port"  # the reference has no batched verify; the oracle restates its loop
-    return {"value": rows_done / el, "unit": "rows/s", "cores": 1, "kind": kind,
-            "sample": f"{reps} x {name} batch ({w.rows} rows, V={w.vocab}), single thread, "
-                      f"{el:.1f} s"}
+    return {"value": rows_done / el, "unit": "rows/s", "cores": threads, "kind": kind,
+            "sample": f"{reps} x {name} batch ({w.rows} rows, V={w.vocab}), "
+                      f"{'single thread' if threads == 1 else f'{threads} threads'}, {el:.1f} s"}
 
 
 def copy_calibration(mib: int, reps: int = 20):
@@ -187,6 +210,19 @@ def _pmc_avg(path, kernel, counter):
     return min(r[1] for r in rs), float(sum(r[2] for r in rs))
 
 
+def summarize_counters(path, kernel):
+    """Per-kernel average per dispatch of every counter in a `rocprofv3 --pmc`
+    database, for the kernels matching `kernel`."""
+    c, f = _db(path)
+    rs = c.execute("select kernel_name, counter_name, count(*), avg(value) from counters_collection "
+                   "where kernel_name like ? group by kernel_name, counter_name "
+                   "order by kernel_name, counter_name", (f"%{kernel}%",)).fetchall()
+    out = [f"# source: {os.path.basename(f)} (counters_collection; average per dispatch)"]
+    for kname, cname, n, avg in rs:
+        out.append(f"{cname:<24} {avg:>16.1f}  (n={n})  {kname}")
+    return "\n".join(out)
+
+
 def summarize_traffic(kernel, fetch, write, copy_fetch, copy_write, copy_bytes):
     """HBM traffic per dispatch of `kernel` from FETCH_SIZE / WRITE_SIZE passes
     (KiB per dispatch), each scaled by the same counter's reading for a plain
@@ -233,11 +269,18 @@ def main():
     ap.add_argument("--summarize-traffic", nargs=4,
                     metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
                     help="print HBM traffic per launch from four rocprofv3 --pmc outputs")
+    ap.add_argument("--summarize-counters", metavar="DIR",
+                    help="print per-kernel averages of every counter of a rocprofv3 --pmc output")
+    ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "16")),
+                    help="threads of the all-cores CPU baseline (0: skip it)")
     ap.add_argument("--kernel", default="slice_kernel")
     ap.add_argument("--copy-bytes", type=int, default=256 << 20)
     args = ap.parse_args()
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace, args.kernel))
+        return
+    if args.summarize_counters:
+        print(summarize_counters(args.summarize_counters, args.kernel))
         return
     if args.summarize_traffic:
         print(summarize_traffic(args.kernel, *args.summarize_traffic, args.copy_bytes))
@@ -250,6 +293,7 @@ def main():
               "rows shard across GPUs with no exchange, see DESIGN.md", file=sys.stderr)
         sys.exit(2)
     w, ms_step, wall_ms, ms_launch, nsets = gpu_bench(args.workload, args.steps, args.warmup)
+    ceiling = copy_ceiling()
     rows = w.rows
     alg = w.algorithmic_bytes()
     # the timed region's average call duration (one kernel per call, three
@@ -278,12 +322,14 @@ def main():
                      "kernel": kernel, "algorithmic_bytes": alg, "us_per_launch": ms_step * 1e3,
                      "us_per_launch_bracketed_median": ms_launch * 1e3,
                      "traffic_source": f"profiles/{stem}_{args.workload}_traffic.txt"
-                     if traffic is not None else None},
+                     if traffic is not None else None,
+                     "copy_ceiling": ceiling, "frac_of_copy": achieved / ceiling},
         "wall_ms_per_step": wall_ms,
     }
     if not args.no_cpu:
-        cb = cpu_baseline(args.workload, args.cpu_seconds)
-        line["cpu_baseline"] = cb
+        line["cpu_baseline"] = cpu_baseline(args.workload, args.cpu_seconds)
+        if args.cpu_threads > 1 and w.rows > 1:
+            line["cpu_baseline_all_cores"] = cpu_baseline(args.workload, args.cpu_seconds, args.cpu_threads)
     print(json.dumps(line), flush=True)
 
 
