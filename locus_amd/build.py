@@ -32,7 +32,8 @@ HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contra
 HIP_SOURCES = ["lcs_api.hip", "lcs_sample.hip", "lcs_nucleus.hip", "lcs_verify.hip"]
 SAMPLER_SO = os.path.join(HERE, "liblocus_sampler.so")
 HOST_SO = os.path.join(HERE, "liblocus_host.so")
-HOST_SOURCES = ["grammar.cpp", "speculative.cpp", "sampler_registry.cpp", "host_capi.cpp", "sampling.cpp"]
+HOST_SOURCES = ["grammar.cpp", "speculative.cpp", "sampler_registry.cpp", "host_capi.cpp", "sampling.cpp",
+                "batch_sampler.cpp"]
 HOST_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-Wall", "-I" + INCLUDE]
 TEST_HOST = os.path.join(ROOT, "tests", "cpp", "test_host")
 

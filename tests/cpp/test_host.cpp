@@ -4,7 +4,8 @@
 // test_speculative.cpp), restated with a minimal harness, plus the mask
 // builder against per-token allows() and the backend-resolution rules.
 //   test_host cpu   grammar, mask builder, n-gram draft, registry (no device)
-//   test_host gpu   sampling API on the device, registry with a device
+//   test_host gpu   sampling API on the device, registry with a device, and
+//                   the batched engine step against the per-row API
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -15,7 +16,10 @@
 #include <string>
 #include <vector>
 
+#include <hip/hip_runtime.h>
+
 #include "locus/backend/sampler_registry.hpp"
+#include "locus/engine/batch_sampler.hpp"
 #include "locus/model/grammar.hpp"
 #include "locus/model/sampling.hpp"
 #include "locus/model/speculative.hpp"
@@ -289,6 +293,96 @@ static void test_sampling_gpu() {
     }
 }
 
+// BatchSampler (one lcs_sample per step) against the per-row API driven the
+// way Engine::sample_from drives it (engine.cpp:423-450): same requests, seeds
+// and logits; ids, histories and constraint states must agree step by step,
+// logprobs within 1e-5. The per-row API runs the exact path (it writes the
+// penalised logits back), the batch the sliced paths, so this also checks
+// the paths against each other.
+static void test_batch_gpu() {
+    using locus::engine::BatchSampler;
+    using locus::engine::SampleRequest;
+    constexpr std::uint32_t V = 5003, B = 8, K = 5, STRIDE = (V + 3) / 4 * 4;
+    std::vector<std::string> pieces = synthetic_pieces();
+    std::mt19937_64 pr(11);
+    const char alpha[] = "{}[]\":,. -+eE0123456789tfnrulsa\\bx \n";
+    while (pieces.size() < V) {
+        std::string t;
+        const int n = 1 + static_cast<int>(pr() % 6);
+        for (int k = 0; k < n; ++k) t.push_back(alpha[pr() % (sizeof(alpha) - 1)]);
+        pieces.push_back(t);
+    }
+    auto mb = std::make_shared<const JsonMaskBuilder>(pieces);
+    JsonTokenConstraint ca(mb), cb(mb);
+    std::vector<SampleRequest> a(B), b(B);
+    for (std::uint32_t r = 0; r < B; ++r) {
+        SamplingParams& p = a[r].sampling;
+        switch (r) {
+            case 0: break;   // greedy
+            case 1: p.temperature = 0.8f; p.top_k = 40; p.top_p = 0.95f; break;
+            case 2: p.temperature = 0.7f; p.min_p = 0.05f; p.top_p = 0.9f; p.repeat_penalty = 1.1f;
+                    p.frequency_penalty = 0.5f; p.presence_penalty = 0.3f; p.repeat_last_n = 2048; break;
+            case 3: p.temperature = 1.5f; p.top_p = 0.98f; break;
+            case 4: p.temperature = 1.0f; p.top_p = 0.95f; break;   // JSON constraint
+            case 5: p.temperature = 1.0f; p.repeat_penalty = 1.3f; break;
+            case 6: p.repeat_penalty = 1.2f; p.presence_penalty = 0.5f; break;   // greedy, penalties
+            default: p.temperature = 0.9f; p.top_k = 100; break;   // exact path in both
+        }
+        a[r].rng.seed(1000 + r);
+        for (int i = 0; i < 30; ++i) a[r].generated.push_back(static_cast<TokenId>(pr() % V));
+        if (r == 1 || r == 2 || r == 6) a[r].logprobs_opt = {true, r == 1 ? 5u : (r == 2 ? 3u : 1u)};
+        b[r] = a[r];
+    }
+    a[4].constraint = &ca;
+    b[4].constraint = &cb;
+    std::vector<SampleRequest*> ap(B);
+    for (std::uint32_t r = 0; r < B; ++r) ap[r] = &a[r];
+    BatchSampler bs(0, B, V, 4096, 20);
+    float* dlog = nullptr;
+    CHECK(hipMalloc(&dlog, (std::size_t)B * STRIDE * sizeof(float)) == hipSuccess);
+    std::mt19937 lr(99);
+    std::normal_distribution<float> nd(0.0f, 2.0f);
+    std::vector<float> host((std::size_t)B * STRIDE, 0.0f);
+    for (std::uint32_t step = 0; step < K; ++step) {
+        for (std::uint32_t r = 0; r < B; ++r)
+            for (std::uint32_t i = 0; i < V; ++i) host[(std::size_t)r * STRIDE + i] = nd(lr);
+        CHECK(hipMemcpy(dlog, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice) == hipSuccess);
+        const std::vector<TokenId> ids = bs.sample_step(dlog, LCS_F32, STRIDE, ap);
+        CHECK(ids.size() == B);
+        for (std::uint32_t r = 0; r < B; ++r) {
+            // Engine::sample_from on request b[r]
+            SampleRequest& q = b[r];
+            std::vector<float> row(host.begin() + (std::ptrdiff_t)r * STRIDE, host.begin() + (std::ptrdiff_t)r * STRIDE + V);
+            const std::vector<float> raw = row;
+            const TokenId next = sample(row, q.sampling, q.generated, q.rng, q.constraint);
+            if (q.constraint) q.constraint->commit(next);
+            q.generated.push_back(next);
+            if (next != ids[r]) std::fprintf(stderr, "batch step %u row %u: batch %d per-row %d\n", step, r, ids[r], next);
+            CHECK(next == ids[r]);
+            CHECK(a[r].generated == q.generated);
+            if (q.logprobs_opt.enabled) {
+                float lp = 0.0f;
+                std::vector<TokenLogprob> top;
+                logprobs_from(raw, next, q.logprobs_opt.top, lp, top);
+                const auto& e = a[r].logprobs.back();
+                CHECK(e.token == next && std::fabs(e.logprob - lp) <= 1e-5f);
+                CHECK(e.top.size() == top.size());
+                for (std::size_t j = 0; j < top.size() && j < e.top.size(); ++j)
+                    CHECK(e.top[j].token == top[j].token && std::fabs(e.top[j].logprob - top[j].logprob) <= 1e-5f);
+            }
+        }
+        CHECK(a[3].rng() == b[3].rng());   // one engine output per stochastic row and step
+        CHECK(a[0].rng() == b[0].rng());   // none for greedy
+    }
+    for (std::uint32_t t = 0; t < V; t += 97) CHECK(ca.allows(static_cast<TokenId>(t)) == cb.allows(static_cast<TokenId>(t)));
+    (void)hipFree(dlog);
+    // limits
+    std::vector<SampleRequest> many(B + 1);
+    std::vector<SampleRequest*> mp;
+    for (auto& q : many) mp.push_back(&q);
+    CHECK(throws<std::invalid_argument>([&] { bs.sample_step(nullptr, LCS_F32, STRIDE, mp); }));
+}
+
 int main(int argc, char** argv) {
     const std::string mode = argc > 1 ? argv[1] : "cpu";
     try {
@@ -300,6 +394,7 @@ int main(int argc, char** argv) {
         } else if (mode == "gpu") {
             test_registry(true);
             test_sampling_gpu();
+            test_batch_gpu();
         } else {
             std::fprintf(stderr, "usage: test_host cpu|gpu\n");
             return 2;
