@@ -91,6 +91,9 @@ struct SliceLocal {
     double win_delta;                    // T (ln(1/min_p) + 1e-3), sampled rows
     float chosen_raw, fin_maxl;
     uint32_t fin_fb, fin_L0;
+    uint32_t tk_ns[kMaxSlices];          // top-k rows: entries of each slice's list,
+    uint32_t tk_cs[kMaxSlices], tk_base[kMaxSlices];   // its candidates (keys <= U) and their offset
+    uint32_t tk_ke, tk_nc;
     uint64_t ck[kCandCap];               // top-n candidates (rank keys)
     uint64_t wk[kWinLds];                // window entries (rank keys)
     SampleArgs args;                     // the kernel arguments, for the finalize
@@ -385,31 +388,128 @@ __device__ __forceinline__ void fin_fetch_topk(const uint64_t* recs, uint32_t S,
     }
 }
 
-// Top-k rows (sampling.cpp:87-97): the k-way merge of the slices' top-k lists
-// (h0: this lane's slice header word 0), then the exact normaliser over those
-// k. Returns true when a slice could not rank its list.
-__device__ __forceinline__ bool fin_merge_topk(uint32_t S, uint32_t K, SliceSmem& sm, float inv_t, uint64_t h0) {
+// Top-k rows, wave 0 before the merge: each slice's list length into LDS (h0:
+// this lane's slice header word 0). Returns true when a slice could not rank
+// its list.
+__device__ __forceinline__ bool fin_topk_lengths(uint32_t S, uint32_t K, SliceSmem& sm, uint64_t h0) {
     const int lane = lane_id();
     const bool mine = (uint32_t)lane < S;
-    const uint32_t s = mine ? (uint32_t)lane : 0u;
     const uint32_t flags = mine ? (uint32_t)(h0 >> 48) : 0u;
-    if (ballot(mine && (flags & rec::kFlagWinLost))) return true;
-    const uint32_t ns = mine ? min((uint32_t)(h0 >> 32) & 0xffffu, K) : 0u;
-    const uint32_t Ke = min(K, wave_sum_u(ns));
-    uint32_t p = 0;
-    for (uint32_t r = 0; r < Ke; ++r) {
-        const uint64_t head = p < ns ? sm.u.f.tkey[s * K + p] : ~0ull;
-        const uint32_t hk = (uint32_t)(head >> 32);
-        const uint32_t mk = wave_min_u(hk);
-        const uint64_t hit = ballot(head != ~0ull && hk == mk);
-        const int wl = hit ? __builtin_ctzll(hit) : 0;
-        if (lane == wl) {
-            sm.u.f.sorted[r] = head;
-            sm.u.f.sortedraw[r] = sm.u.f.traw[s * K + p];
-            ++p;
+    if (mine) sm.l.tk_ns[lane] = min((uint32_t)(h0 >> 32) & 0xffffu, K);
+    return ballot(mine && (flags & rec::kFlagWinLost)) != 0;
+}
+
+// Top-k rows (sampling.cpp:87-97): the merge of the slices' top-k lists (each
+// in ascending rank-key order), then the exact normaliser over those k.
+// Called by every thread after the barrier that follows the fetch.
+//   1. (wave 0, lane t for list t) A bound U: with m = ceil(Ke / S), the
+//      first m keys of every list hold at least Ke keys, so the Ke-th smallest
+//      key overall is at most the largest of the lists' m-th keys; only keys
+//      <= U can rank below Ke. Each list's keys <= U are a prefix; its length
+//      and offset go to LDS.
+//   2. (every thread) A candidate's rank is the count of keys below it. Every
+//      key below a candidate x <= U is itself <= U, so it is a candidate too:
+//      with at most kRowWin candidates, they are copied together and each is
+//      ranked against the others with LDS broadcast reads. With more, the
+//      count runs over the lists: branch-free lower bounds, 7 halving steps
+//      over 16 lists at a time in lockstep (loads always in bounds). Rank keys
+//      are unique, so ranks below Ke are distinct.
+__device__ __forceinline__ void fin_merge_topk(uint32_t S, uint32_t K, SliceSmem& sm, float inv_t) {
+    const uint32_t tid = threadIdx.x;
+    const int lane = lane_id();
+    static_assert(kTopKMerge <= 4 * kSliceThreads && kTopKMax <= 64 && kMaxSlices <= kWave, "merge shape");
+    if (tid < kWave) {
+        const bool mine = (uint32_t)lane < S;
+        const uint32_t t = mine ? (uint32_t)lane : 0u;
+        const uint32_t n = mine ? sm.l.tk_ns[t] : 0u;
+        const uint32_t Ke = min(K, wave_sum_u(n));
+        const uint32_t m = (Ke + S - 1) / S;
+        const uint32_t c = min(m, n);
+        const uint32_t sub = wave_sum_u(c);
+        const uint64_t kv = c > 0u ? sm.u.f.tkey[t * K + c - 1] : 0ull;
+        uint64_t U = 0;
+        for (uint32_t l = 0; l < S; ++l) {
+            const uint64_t v = readlane_u64(kv, (int)l);
+            U = v > U ? v : U;
+        }
+        if (sub < Ke) U = ~0ull;
+        uint32_t cs = 0;   // keys <= U in this list
+#pragma unroll
+        for (uint32_t step = 64; step >= 1; step >>= 1) {
+            const uint32_t q = cs + step;
+            const uint32_t qq = q < n ? q : n;
+            const uint64_t v = sm.u.f.tkey[t * K + (qq > 0u ? qq - 1u : 0u)];
+            cs = (q <= n && v <= U) ? q : cs;
+        }
+        const uint32_t incl = wave_scan_incl_u(cs);
+        const uint32_t nc = wave_sum_u(cs);   // (a whole-wave reduction: outside the lane-0 branch)
+        if (mine) { sm.l.tk_cs[t] = cs; sm.l.tk_base[t] = incl - cs; }
+        if (lane == 0) { sm.l.tk_ke = Ke; sm.l.tk_nc = nc; }
+    }
+    __syncthreads();
+    PROF_WMARK(16);
+    const uint32_t Ke = sm.l.tk_ke, ncand = sm.l.tk_nc;
+    auto cand_index = [&](uint32_t k) -> uint32_t {   // k-th candidate's place in tkey
+        uint32_t s = 0;
+        for (uint32_t t = 1; t < S; ++t) s = k >= sm.l.tk_base[t] ? t : s;   // bases ascend
+        return s * K + (k - sm.l.tk_base[s]);
+    };
+    if (ncand <= kRowWin) {   // uniform
+        if (tid < ncand) {
+            const uint32_t i = cand_index(tid);
+            sm.u.f.ent[tid] = sm.u.f.tkey[i];
+            sm.u.f.entraw[tid] = sm.u.f.traw[i];
+        }
+        __syncthreads();
+        if (tid < ncand) {
+            const uint64_t x = sm.u.f.ent[tid];
+            uint32_t rank = 0;
+            for (uint32_t j0 = 0; j0 < ncand; j0 += 8) {   // 8 broadcast reads per LDS round trip
+                uint64_t e[8];
+#pragma unroll
+                for (uint32_t u = 0; u < 8; ++u) e[u] = sm.u.f.ent[min(j0 + u, kRowWin - 1)];
+#pragma unroll
+                for (uint32_t u = 0; u < 8; ++u) rank += (j0 + u < ncand && e[u] < x) ? 1u : 0u;
+            }
+            if (rank < Ke) {
+                sm.u.f.sorted[rank] = x;
+                sm.u.f.sortedraw[rank] = sm.u.f.entraw[tid];
+            }
         }
     }
-    wave_sync();
+    for (uint32_t k = tid; ncand > kRowWin && k < ncand; k += kSliceThreads) {
+        const uint32_t i = cand_index(k);
+        const uint64_t x = sm.u.f.tkey[i];
+        uint32_t rank = 0;
+        for (uint32_t t0 = 0; t0 < S; t0 += 16) {   // uniform
+            uint32_t ns[16], lo[16];
+#pragma unroll
+            for (uint32_t u = 0; u < 16; ++u) {
+                ns[u] = t0 + u < S ? sm.l.tk_ns[t0 + u] : 0u;
+                lo[u] = 0u;
+            }
+#pragma unroll
+            for (uint32_t step = 64; step >= 1; step >>= 1) {
+#pragma unroll
+                for (uint32_t u = 0; u < 16; ++u) {
+                    const uint32_t q = lo[u] + step;
+                    const uint32_t qq = q < ns[u] ? q : ns[u];
+                    const uint32_t t = t0 + u < S ? t0 + u : 0u;
+                    const uint64_t v = sm.u.f.tkey[t * K + (qq > 0u ? qq - 1u : 0u)];
+                    lo[u] = (q <= ns[u] && v < x) ? q : lo[u];
+                }
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 16; ++u) rank += lo[u];
+        }
+        if (rank < Ke) {
+            sm.u.f.sorted[rank] = x;
+            sm.u.f.sortedraw[rank] = sm.u.f.traw[i];
+        }
+    }
+    __syncthreads();
+    PROF_WMARK(17);
+    if (tid >= kWave) return;
     const float maxl = rank_val(sm.u.f.sorted[0]);
     const double w = (uint32_t)lane < Ke ? exp((double)tempered(rank_val(sm.u.f.sorted[lane]), maxl, inv_t)) : 0.0;
     if ((uint32_t)lane < Ke) sm.u.f.sw[lane] = w;
@@ -420,7 +520,6 @@ __device__ __forceinline__ bool fin_merge_topk(uint32_t S, uint32_t K, SliceSmem
         sm.l.fin_L0 = Ke;
         sm.l.fin_maxl = maxl;
     }
-    return false;
 }
 
 // Top-p, then min-p (sampling.cpp order), then the draw, 64 ranked row-window
@@ -537,13 +636,19 @@ __device__ __forceinline__ bool fin_row(uint32_t row, uint32_t mode, const lcs_p
     const float inv_t = fdiv(1.0f, P.temperature);
     bool fb = false;
     if (topk) {
-        uint64_t h0 = 0;
-        if (wv == 0) h0 = ld_dev_u64(recs + ((uint32_t)lane < a.slices ? lane : 0) * rec::kWords64);
-        else if (wv == 1) { if (want_lp) fb = fin_logprobs(a, recs, row, ntop, sm); }
-        else fin_fetch_topk(recs, a.slices, P.top_k, sm);
+        if (wv == 0) {
+            const uint64_t h0 = ld_dev_u64(recs + ((uint32_t)lane < a.slices ? lane : 0) * rec::kWords64);
+            fb = fin_topk_lengths(a.slices, P.top_k, sm, h0);
+        } else if (wv == 1) {
+            if (want_lp) fb = fin_logprobs(a, recs, row, ntop, sm);
+        } else {
+            fin_fetch_topk(recs, a.slices, P.top_k, sm);
+        }
         if (fb && lane == 0) sm.l.fin_fb = 1u;
         __syncthreads();
-        if (wv == 0) fb = fin_merge_topk(a.slices, P.top_k, sm, inv_t, h0);
+        if (sm.l.fin_fb) return true;
+        PROF_WMARK(15);
+        fin_merge_topk(a.slices, P.top_k, sm, inv_t);
     } else if (wv == 0) {
         if (stoch) fb = fin_window(a, recs, P, sm, inv_t);
         else fin_greedy(a, recs, row, masked, sm);
