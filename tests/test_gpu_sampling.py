@@ -321,3 +321,59 @@ def test_nucleus_rows(sampler):
     w32 = W.Workload("nucleus-bf16-as-f32", bf.rows, bf.vocab, "f32", W.bf16_to_f32(b16), bf.params,
                      bf.seeds, bf.u, n_top=2, want_logprobs=True)
     compare(w32, run(sampler, wb), O.sample_batch(w32, threads=16), "nucleus-bf16", expect_paths={4, 6})
+
+
+def _all_paths_workload(V, seed, dtype="f32"):
+    """Eight rows over vocab V, one per row path and filter mix: greedy (also
+    masked), min-p window, sliced top-k, nucleus (top-p, masked, plain
+    temperature) and the exact path (top-k 100), with penalties on half."""
+    g = np.random.default_rng(seed)
+    rows = 8
+    logits = (g.standard_normal((rows, V)) * 2.5).astype(np.float32)
+    p = W.default_params(rows)
+    cfg = [  # temperature, top_k, top_p, min_p, penalties, masked fraction
+        (0.0, 0, 1.0, 0.0, True, None), (0.7, 0, 0.9, 0.05, True, None), (0.8, 20, 0.95, 0.0, False, None),
+        (1.5, 0, 0.98, 0.0, False, None), (1.0, 0, 0.95, 0.0, True, 0.05), (1.0, 0, 1.0, 0.0, False, None),
+        (0.9, 100, 1.0, 0.0, True, None), (0.0, 0, 1.0, 0.0, False, 0.3),
+    ]
+    bits = np.ones((rows, V), dtype=bool)
+    has = np.zeros(rows, dtype=np.uint8)
+    for r, (t, k, tp, mp, pen, frac) in enumerate(cfg):
+        p["temperature"][r], p["top_k"][r], p["top_p"][r], p["min_p"][r] = t, k, tp, mp
+        if pen:
+            p["repeat_penalty"][r], p["frequency_penalty"][r], p["presence_penalty"][r] = 1.2, 0.3, 0.2
+            p["repeat_last_n"][r] = 256
+        if frac is not None:
+            has[r] = 1
+            bits[r] = g.random(V) < frac
+    hlen = 300
+    hist = g.integers(0, V, size=(rows, hlen)).astype(np.int32)
+    seeds = np.array([W.row_seed(seed, r) for r in range(rows)], dtype=np.uint64)
+    u = W.uniforms(seeds)
+    w32 = W.Workload(f"paths-{V}", rows, V, "f32", logits, p, seeds, u,
+                     np.arange(rows + 1, dtype=np.uint32) * hlen, hist.reshape(-1), W.pack_mask(bits), 3, True)
+    if dtype == "f32":
+        return w32, w32, has
+    b16 = W.bf16_rne(logits)
+    wb = W.Workload(f"paths-{V}-bf16", rows, V, "bf16", b16, p, seeds, u, w32.hist_off, w32.hist_ids,
+                    w32.mask, 3, True)
+    w32 = W.Workload(f"paths-{V}-bf16-as-f32", rows, V, "f32", W.bf16_to_f32(b16), p, seeds, u,
+                     w32.hist_off, w32.hist_ids, w32.mask, 3, True)
+    return wb, w32, has
+
+
+@pytest.mark.parametrize("V,dtype", [(8192, "f32"), (8193, "f32"), (16385, "bf16"), (262144, "f32"),
+                                     (262144, "bf16")])
+def test_every_path_at_slice_boundaries_and_max_vocab(sampler, V, dtype):
+    """Every row path at vocabularies that end a slice exactly, leave a
+    one-logit last slice, and fill all 32 slices (the maximum vocabulary)."""
+    wg, w32, has = _all_paths_workload(V, 20261300 + V, dtype)
+    say("paths", V, dtype)
+    g = run(sampler, wg, has_mask=sampler.torch.from_numpy(has).cuda())
+    compare(w32, g, O.sample_batch(w32, threads=16, has_mask=has), f"paths-{V}-{dtype}",
+            expect_paths={1, 2, 3, 4, 5, 6})
+    paths = g["diag"]["path"].tolist()
+    # row 3 (top-p 0.98 over a wide nucleus) may exceed the nucleus list at the
+    # largest vocabularies and finish on the exact path
+    assert paths[0] == 1 and paths[2] == 5 and paths[6] == 4 and paths[4] == 6, paths
+    assert paths[3] in ((4, 6) if V > 131072 else (6,)), paths
