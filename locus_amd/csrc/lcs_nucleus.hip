@@ -84,7 +84,7 @@ struct NucSmem {
             double mass[kNucBins];
         } h;                              // histogram (pass B)
         uint64_t top[kMaxSlices * kTopMax];   // top-n merge (pass A finalize)
-        uint64_t lkeys[kNucList];         // the slice's selections (pass C), thread order
+        uint64_t lkeys[kNucStage];        // the slice's selections (pass C), thread order
         NucFinC fc;                       // select finalize
         ExactSmem<kSliceThreads, kFbBins, kFbCap, kFbHistCap> ex;
     } u;
@@ -1174,9 +1174,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         }
     }
     // the workgroup's selections in thread order (one block scan) staged in
-    // LDS, one reservation in the row list, coalesced stores; positions past
-    // kNucList are dropped (the finalize then sees list_n > kNucList and
-    // takes the exact path)
+    // LDS, one reservation in the row list, coalesced stores; selections past
+    // the LDS stage (rare) go to the list directly; positions past kNucList
+    // are dropped (the finalize then sees list_n > kNucList and takes the
+    // exact path)
     const uint32_t cnt = (uint32_t)__popc(sel);
     const uint32_t incl = wave_scan_incl_u(cnt);
     if (lane == kWave - 1) sm.l.nall[wv] = incl;
@@ -1188,11 +1189,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         pos += k < wv ? t : 0u;
         tot += t;
     }
+    const uint32_t pos0 = pos;
     if (sel) {
 #pragma unroll
         for (int q = 0; q < kSliceElems; ++q) {
             if ((sel >> q) & 1u) {
-                if (pos < kNucList) sm.u.lkeys[pos] = rank_key(in.v[q], in.eid(q));
+                if (pos < kNucStage) sm.u.lkeys[pos] = rank_key(in.v[q], in.eid(q));
                 ++pos;
             }
         }
@@ -1203,10 +1205,20 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     __syncthreads();
     {
         const uint32_t base = sm.l.gbase;
-        const uint32_t n = min(tot, kNucList);
+        const uint32_t n = min(tot, kNucStage);
         uint64_t* list = a.nlist + (uint64_t)wrow * kNucList;
         for (uint32_t i = tid; i < n; i += NT) {
             if (base + i < kNucList) st_dev_u64(list + base + i, sm.u.lkeys[i]);
+        }
+        if (pos > kNucStage) {
+            uint32_t p = pos0;
+#pragma unroll
+            for (int q = 0; q < kSliceElems; ++q) {
+                if ((sel >> q) & 1u) {
+                    if (p >= kNucStage && base + p < kNucList) st_dev_u64(list + base + p, rank_key(in.v[q], in.eid(q)));
+                    ++p;
+                }
+            }
         }
     }
     run_fin = nuc_arrive(a.counters + row, S, sm);
