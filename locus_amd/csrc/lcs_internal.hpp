@@ -65,7 +65,7 @@ __host__ __device__ inline uint32_t row_mode(const lcs_params& p, bool masked, u
         return kModeTopK;
     }
     if (p.min_p > 0.0f && !masked && !topk && pen_ok) return kModeWindow;
-    if (!topk && pen_ok) return kModeNucleus;
+    if (pen_ok) return kModeNucleus;   // incl. top-k rows the sliced top-k path cannot take
     return kModeGeneral;
 }
 

@@ -1,6 +1,7 @@
-// Nucleus path for MI355X (gfx950): stochastic rows without top-k whose
-// candidate set stays large (top-p only, constrained rows, min-p over a flat
-// row), in three slice-parallel passes over device-resident logits.
+// Nucleus path for MI355X (gfx950): stochastic rows whose candidate set
+// stays large (top-p only, constrained rows, min-p over a flat row, top-k
+// beyond the sliced top-k path), in three slice-parallel passes over
+// device-resident logits.
 //
 // Each pass cuts a row into `slices` workgroups of 256 threads (one HBM read
 // of <= 8192 logits each, 32 per thread in registers), as the sliced kernel
@@ -22,7 +23,9 @@
 //                  list; the last arrival rebuilds each range's sub-bin
 //                  masses, sorts only the decisive sub-bins' candidates (rank
 //                  key: logit, then id) and walks them in the reference's
-//                  order: top-p, min-p, kept mass, the draw.
+//                  order: top-k (the K-th candidate and the mass SK of the
+//                  first K, the normaliser of what follows), top-p, min-p,
+//                  kept mass, the draw.
 //
 // Bin-level decisions carry a 1e-10 relative guard (a target that close to
 // a bin or sub-bin edge takes both neighbours). A plan that would compact
@@ -733,13 +736,26 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     int ivl[kNucRanges + 3][2];
     int niv = 0;
     auto add = [&](int b0, int b1) { ivl[niv][0] = b0; ivl[niv][1] = b1; ++niv; };
-    uint32_t kp_lo = ncand, kp_hi = ncand, km_lo = ncand, km_hi = ncand;
+    // top-k (sampling.cpp:87-97): the first K candidates survive and their
+    // mass S_K, which lies in [mass before bin bK, mass through bin bK] for
+    // the bin bK holding position K - 1, is the normaliser of what follows
+    const uint32_t K = (P.top_k > 0u && P.top_k < ncand) ? P.top_k : ncand;
+    int bK = NB - 1;
+    double SK_lo = Stot, SK_hi = Stot;
+    if (K < ncand) {
+        bK = first_count(K);
+        SK_lo = mb(bK);
+        SK_hi = hm[bK];
+        add(bK, bK);
+    }
+    uint32_t kp_lo = K, kp_hi = K, km_lo = K, km_hi = K;
     if (P.top_p < 1.0f) {
-        const double T = (double)P.top_p * Stot;
-        const int b0 = first_mass(T * (1.0 - kGuard)), b1 = first_mass(T * (1.0 + kGuard));
+        const double tp = (double)P.top_p;
+        const int b0 = min(first_mass(tp * SK_lo * (1.0 - kGuard)), bK);
+        const int b1 = min(first_mass(tp * SK_hi * (1.0 + kGuard)), bK);
         add(b0, b1);
-        kp_lo = cb(b0) + 1u;
-        kp_hi = hc[b1];
+        kp_lo = min(cb(b0) + 1u, K);
+        kp_hi = min(hc[b1], K);
     }
     if (P.min_p > 0.0f) {
         // survivors have w >= min_p (w_0 = 1): offsets about ln(min_p) decide
@@ -747,8 +763,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         const float d = 1e-4f * fmaxf(1.0f, fabsf(xm));
         const int b0 = (int)nuc_bin(nuc_f(xm + d, sx)), b1 = (int)nuc_bin(nuc_f(xm - d, sx));
         add(b0, b1);
-        km_lo = max(1u, cb(b0));
-        km_hi = max(1u, hc[b1]);
+        km_lo = min(max(1u, cb(b0)), K);
+        km_hi = min(max(1u, hc[b1]), K);
     }
     const uint32_t keep_lo = max(1u, min(kp_lo, km_lo)), keep_hi = max(1u, min(kp_hi, km_hi));
     const double K_lo = mb(first_count(keep_lo)), K_hi = hm[first_count(keep_hi)];
@@ -906,6 +922,22 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
         }
         return false;
     };
+    // (range, sub-bin) holding candidate position n - 1 (rank order)
+    auto find_count = [&](uint32_t n, uint32_t& k, uint32_t& s) -> bool {
+        for (uint32_t j = 0; j < nrg && j < kNucRanges; ++j) {
+            if (rg[j].c0 < n && rg[j].c0 + rg[j].cnt >= n) {
+                int lo = 0, hi = (int)kNucSub - 1;
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (rg[j].c0 + sm.u.fc.scnt[j][mid] >= n) hi = mid; else lo = mid + 1;
+                }
+                k = j;
+                s = (uint32_t)lo;
+                return true;
+            }
+        }
+        return false;
+    };
     // Gathers the candidates of range k's sub-bins [s0, s1] into gkey and ranks
     // them (wave 0) into gsorted with weights gw. Every thread calls it.
     auto gather = [&](uint32_t k, uint32_t s0, uint32_t s1) -> uint32_t {
@@ -984,15 +1016,37 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     uint32_t keep = ncand;
     double kept_sum = Stot;
     uint64_t last_key = ~0ull;     // the candidate at position keep - 1, when known
-    // top-p (sampling.cpp:113-123): first position with cum = prefix / S >= top_p
-    uint32_t keep_p = ncand;
-    double mass_p = Stot;
-    uint64_t key_p = ~0ull;
+    // top-k (sampling.cpp:87-97): the first K candidates survive; their mass
+    // SK is the normaliser of top-p and min-p (sampling.cpp:101-109)
+    const uint32_t K = (P.top_k > 0u && P.top_k < ncand) ? P.top_k : ncand;
+    double SK = Stot;
+    uint64_t key_k = ~0ull;        // the candidate at position K - 1 (when K < ncand)
+    if (!fail && K < ncand) {
+        uint32_t kk, sk;
+        if (!find_count(K, kk, sk)) {
+            fail = true;
+        } else {
+            const uint32_t ng = gather(kk, sk, sk);
+            const uint32_t pos = K - 1u - c_before(kk, sk);
+            if (ng > kGroupMax || pos >= ng) {
+                fail = true;
+            } else {
+                double pm = 0.0;
+                (void)first_prefix(ng, [&](uint32_t i, double) { return i == pos; }, pm);
+                SK = m_before(kk, sk) + pm;
+                key_k = sm.u.fc.gsorted[pos];
+            }
+        }
+    }
+    // top-p (sampling.cpp:113-123): first position with cum = prefix / SK >= top_p
+    uint32_t keep_p = K;
+    double mass_p = SK;
+    uint64_t key_p = key_k;
     if (!fail && P.top_p < 1.0f) {
         const double tp = (double)P.top_p;
         uint32_t k0, s0, k1, s1;
-        const bool f0 = find_mass(tp * Stot * (1.0 - kGuard), k0, s0);
-        const bool f1 = find_mass(tp * Stot * (1.0 + kGuard), k1, s1);
+        const bool f0 = find_mass(tp * SK * (1.0 - kGuard), k0, s0);
+        const bool f1 = find_mass(tp * SK * (1.0 + kGuard), k1, s1);
         if (!f0 || !f1 || k0 != k1) {
             fail = true;
         } else {
@@ -1003,8 +1057,8 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
                 // cum = (mass before the group + prefix) / S reaches top_p
                 const double mb0 = m_before(k0, s0);
                 double pm = 0.0;
-                const uint32_t pos = first_prefix(ng, [&](uint32_t, double pi) { return (mb0 + pi) / Stot >= tp; }, pm);
-                if (pos == kNone) {
+                const uint32_t pos = first_prefix(ng, [&](uint32_t, double pi) { return (mb0 + pi) / SK >= tp; }, pm);
+                if (pos == kNone || c_before(k0, s0) + pos + 1u > K) {
                     fail = true;
                 } else {
                     keep_p = c_before(k0, s0) + pos + 1u;
@@ -1017,11 +1071,11 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     // min-p (sampling.cpp:125-133): survivors are the leading candidates with
     // w / S >= min_p * (w_0 / S); w is non-increasing in rank order, so the
     // survivors of the deciding range are counted without ordering them
-    uint32_t keep_m = ncand;
-    double mass_m = Stot;
-    uint64_t key_m = ~0ull;
+    uint32_t keep_m = K;
+    double mass_m = SK;
+    uint64_t key_m = key_k;
     if (!fail && P.min_p > 0.0f) {
-        const double thresh = (double)P.min_p * (1.0 / Stot);
+        const double thresh = (double)P.min_p * (1.0 / SK);
         const float xm = (float)log((double)P.min_p);
         const uint32_t bm = nuc_bin(nuc_f(xm, sx));
         uint32_t km = kNucRanges;
@@ -1038,7 +1092,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
                 uint32_t kk, s;
                 const float x = locate(key, kk, s);
                 const double w = kk == km ? exp_f64((double)x) : 0.0;
-                if (kk == km && w / Stot >= thresh) {
+                if (kk == km && w / SK >= thresh) {
                     ++cnt;
                     ms += w;
                     kl = key > kl ? key : kl;
@@ -1051,16 +1105,17 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
             mass_m = rg[km].m0 + tm;
             key_m = tc > 0 ? tk : ~0ull;
             if (rg[km].c0 + tc == 0) fail = true;   // (w_0 always survives)
+            if (keep_m >= K) { keep_m = K; mass_m = SK; key_m = key_k; }   // top-k cut first
         }
     }
     if (!fail) {
-        if (keep_p <= keep_m && keep_p < ncand) {
+        if (keep_p <= keep_m && keep_p < K) {
             keep = keep_p; kept_sum = mass_p; last_key = key_p;
         } else if (keep_m < keep_p) {
             keep = keep_m; kept_sum = mass_m; last_key = key_m;
             if (key_m == ~0ull) fail = true;
         } else {
-            keep = ncand; kept_sum = Stot; last_key = ~0ull;
+            keep = K; kept_sum = SK; last_key = key_k;   // ~0 when no top-k cut
         }
     }
     // draw (sampling.cpp:135-147): r = u * kept_sum; the first kept candidate
@@ -1117,7 +1172,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
             dg.maxl = maxl;
             dg.boundary = last_key != ~0ull ? rank_val(last_key) : maxl;
             dg.path = LCS_PATH_NUCLEUS;
-            dg.sum = Stot;
+            dg.sum = SK;
             dg.kept_sum = kept_sum;
             a.diag[row] = dg;
         }
