@@ -810,19 +810,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
 }
 
 // ========================================================= C: nuc_select ==
-// Resolves one decision: the first candidate position, in rank order, whose
-// inclusive prefix mass reaches `target` (ranges and sub-bins give the mass
-// before each sub-bin; the sub-bins within kGuard of the target are
-// gathered and ranked). On return (every thread): sm.l.ng candidates in
-// gsorted with weights gw, and the group's count/mass before it.
-struct NucGroup {
-    uint32_t k;      // range
-    uint32_t s0, s1; // sub-bins
-    uint32_t c_before;
-    double m_before;
-    bool ok;
-};
-
 // The select pass's last arrival: exact decisions over the compacted ranges.
 // Every thread of the workgroup calls it, with the kernel arguments staged
 // in g_nuc.l.args; out of line so that its live values do not crowd the
