@@ -378,3 +378,61 @@ def test_every_path_at_slice_boundaries_and_max_vocab(sampler, V, dtype):
     # bf16 rows of the largest vocabulary hold so many equal logits that a
     # decisive sub-bin can exceed one wave's ranking (the exact path then)
     assert paths[3] in ((4, 6) if dtype == "bf16" and V > 131072 else (6,)), paths
+
+
+def _random_batch(seed):
+    """A seeded random batch: vocab, dtype, per-row parameters, history,
+    masks and logprob counts drawn so that every row path and filter mix
+    appears across seeds."""
+    g = np.random.default_rng([20261400, seed])
+    V = int(g.choice([1, 7, 64, 1000, 8191, 8192, 8193, 20000, 65537, 128256]))
+    rows = int(g.integers(1, 13))
+    scale = float(g.choice([0.3, 1.0, 3.0, 8.0]))
+    logits = (g.standard_normal((rows, V)) * scale).astype(np.float32)
+    if g.random() < 0.2:   # integer logits: exact ties
+        logits = np.round(logits).astype(np.float32)
+    p = W.default_params(rows)
+    for r in range(rows):
+        p["temperature"][r] = g.choice([0.0, 0.05, 0.5, 0.8, 1.0, 1.5, 3.0])
+        p["top_k"][r] = g.choice([0, 0, 1, 5, 40, 64, 65, 200, 5000])
+        p["top_p"][r] = g.choice([1.0, 1.0, 0.5, 0.9, 0.95, 0.99])
+        p["min_p"][r] = g.choice([0.0, 0.0, 0.01, 0.05, 0.3])
+        if g.random() < 0.5:
+            p["repeat_penalty"][r] = g.choice([0.8, 1.1, 1.5])
+            p["frequency_penalty"][r] = g.choice([0.0, 0.5, -0.3])
+            p["presence_penalty"][r] = g.choice([0.0, 0.3])
+            p["repeat_last_n"][r] = g.choice([0, 16, 64, 2048])
+    hlen = int(g.integers(0, 200))
+    hist = g.integers(-3, V + 3, size=(rows, hlen)).astype(np.int32)
+    mask, has = None, None
+    if g.random() < 0.4:
+        bits = g.random((rows, V)) < g.choice([0.0, 0.001, 0.05, 0.5, 1.0])
+        mask = W.pack_mask(bits)
+        has = (g.random(rows) < 0.7).astype(np.uint8)
+    n_top = int(g.choice([0, 1, 5, 20])) if g.random() < 0.6 else 0
+    seeds = np.array([W.row_seed(20261400 + seed, r) for r in range(rows)], dtype=np.uint64)
+    u = W.uniforms(seeds)
+    hoff = np.arange(rows + 1, dtype=np.uint32) * hlen
+    w32 = W.Workload(f"rand{seed}", rows, V, "f32", logits, p, seeds, u, hoff, hist.reshape(-1), mask,
+                     min(n_top, V), n_top > 0)
+    if g.random() < 0.3:   # bf16 logits, compared as their f32 values
+        b16 = W.bf16_rne(logits)
+        wg = W.Workload(f"rand{seed}-bf16", rows, V, "bf16", b16, p, seeds, u, hoff, hist.reshape(-1), mask,
+                        min(n_top, V), n_top > 0)
+        w32 = W.Workload(f"rand{seed}-bf16-as-f32", rows, V, "f32", W.bf16_to_f32(b16), p, seeds, u, hoff,
+                         hist.reshape(-1), mask, min(n_top, V), n_top > 0)
+        return wg, w32, has
+    return w32, w32, has
+
+
+def test_random_batches(sampler):
+    """100 seeded random batches across every path, against the oracle."""
+    seen = set()
+    for seed in range(100):
+        wg, w32, has = _random_batch(seed)
+        say("random", seed, wg.name, wg.rows, wg.vocab)
+        kw = {} if has is None else {"has_mask": sampler.torch.from_numpy(has).cuda()}
+        g = run(sampler, wg, **kw)
+        compare(w32, g, O.sample_batch(w32, threads=16, has_mask=has), f"random-{seed}")
+        seen.update(np.unique(g["diag"]["path"]).tolist())
+    assert {1, 2, 4, 5, 6} <= seen, seen
