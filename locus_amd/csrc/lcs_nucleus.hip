@@ -346,6 +346,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     const float NEG = -__builtin_huge_valf();
     SliceIn<G> in;
     in.start(a, row, slice, P, masked);
+    in.load_mask();   // (its loads arrive with the logits')
     if (tid == 0) sm.l.ncand = 0;
     if (in.hany) {
         in.clear(sm);
@@ -405,7 +406,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         }
     }
     if (in.hany) in.apply(sm);
-    in.load_mask();
     // penalised candidate statistics over all ids and over the allowed ids
     {
         float bv = NEG, mv = NEG, nb = __builtin_huge_valf(), nm = __builtin_huge_valf();
@@ -582,8 +582,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     const bool use_mask = scalar_load(&nr->use_mask) != 0u;
     SliceIn<G> in;
     in.start(a, row, slice, P, masked);
+    if (use_mask) in.load_mask();   // (its loads arrive with the logits')
     in.penalise(sm, P);   // (ends on a barrier when it used the LDS)
-    if (use_mask) in.load_mask();
     for (uint32_t b = tid; b < kNucBins; b += NT) { sm.u.h.cnt[b] = 0u; sm.u.h.mass[b] = 0.0; }
     __syncthreads();
     const float inv_t = fdiv(1.0f, P.temperature);
@@ -1188,8 +1188,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     const bool use_mask = scalar_load(&nr->use_mask) != 0u;
     SliceIn<G> in;
     in.start(a, row, slice, P, masked);
+    if (use_mask) in.load_mask();   // (its loads arrive with the logits')
     in.penalise(sm, P);
-    if (use_mask) in.load_mask();
     // the planned bins as a bitmap in LDS
     if (tid < kNucBins / 32) {
         const uint32_t nrg = scalar_load(&nr->nr);
