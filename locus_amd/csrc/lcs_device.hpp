@@ -10,6 +10,13 @@ namespace lcs {
 
 constexpr int kWave = 64;
 
+// Work-item and workgroup ids read straight from the hardware registers. In
+// kernels this large HIP's threadIdx / blockIdx can compile to library calls,
+// and a call's result counts as divergent: row-uniform loads would then become
+// vector loads queued behind the logits instead of scalar loads.
+__device__ __forceinline__ uint32_t tid_x() { return __builtin_amdgcn_workitem_id_x(); }
+__device__ __forceinline__ uint32_t wg_x() { return __builtin_amdgcn_workgroup_id_x(); }
+
 // ---------------------------------------------------------------- keys ----
 // Order-preserving 32-bit key of a float; -0.0 is folded onto +0.0 so the two
 // compare equal, as `a.first > b.first` treats them (sampling.cpp:178-180).
@@ -74,6 +81,18 @@ __device__ __forceinline__ float penalize_fast(float l, uint32_t count, const lc
     const float sub = fadd(fmul(p.frequency_penalty, static_cast<float>(count)), p.presence_penalty);
     return fsub(l, sub);
 }
+// penalize_fast() without branches, for callers that handle a tiny positive
+// quotient (where the f64 product may round differently from the divide)
+// themselves: returns false for such an l. rp1: repeat_penalty == 1.
+__device__ __forceinline__ float penalize_nb(float l, uint32_t count, const lcs_params& p, double inv_rp, bool rp1,
+                                             bool& ok) {
+    const double y = (double)l * inv_rp;
+    const float q = l > 0.0f ? (float)y : fmul(l, p.repeat_penalty);
+    ok = rp1 || !(l > 0.0f) || y >= 0x1p-125;
+    const float m = rp1 ? l : q;
+    const float sub = fadd(fmul(p.frequency_penalty, static_cast<float>(count)), p.presence_penalty);
+    return fsub(m, sub);
+}
 __device__ __forceinline__ bool penalties_active(const lcs_params& p) {
     return !(p.repeat_penalty == 1.0f && p.frequency_penalty == 0.0f &&
              p.presence_penalty == 0.0f);
@@ -116,6 +135,36 @@ __device__ __forceinline__ double exp_f64(double x) {
     const int e = x < -745.0 ? 0 : (int)n;
     const double y = __builtin_ldexp(p, e);
     return x < -745.0 ? 0.0 : y;
+}
+
+// log(x) in f64 for finite x > 0, inline: x = m 2^e with m in [sqrt(1/2),
+// sqrt(2)), log m = 2 atanh(s), s = (m - 1) / (m + 1), |s| < 0.1716, by its
+// odd series to s^23 (truncation below 1e-19 relative); ln 2 split in a head
+// exact under multiplication by e and a tail. Within a few ulp.
+__device__ __forceinline__ double log_f64(double x) {
+    constexpr double kLn2Hi = 0x1.62e42fefa3800p-1;
+    constexpr double kLn2Lo = 0x1.ef35793c76730p-45;
+    int e = 0;
+    double m = __builtin_frexp(x, &e);   // [0.5, 1)
+    if (m < 0.70710678118654752) {
+        m *= 2.0;
+        e -= 1;
+    }
+    const double s = (m - 1.0) / (m + 1.0);
+    const double s2 = s * s;
+    double p = 1.0 / 23;
+    p = __builtin_fma(p, s2, 1.0 / 21);
+    p = __builtin_fma(p, s2, 1.0 / 19);
+    p = __builtin_fma(p, s2, 1.0 / 17);
+    p = __builtin_fma(p, s2, 1.0 / 15);
+    p = __builtin_fma(p, s2, 1.0 / 13);
+    p = __builtin_fma(p, s2, 1.0 / 11);
+    p = __builtin_fma(p, s2, 1.0 / 9);
+    p = __builtin_fma(p, s2, 1.0 / 7);
+    p = __builtin_fma(p, s2, 1.0 / 5);
+    p = __builtin_fma(p, s2, 1.0 / 3);
+    const double de = (double)e;
+    return de * kLn2Hi + (2.0 * s + (2.0 * s * s2 * p + de * kLn2Lo));
 }
 
 // ------------------------------------------------------ wave reductions ----
@@ -258,7 +307,16 @@ __device__ __forceinline__ uint32_t wave_kth_largest4(const uint32_t (&k)[4], ui
     }
     return T;
 }
-__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
+// The n-th largest of the wave's 64 keys (1 <= n <= 64), as above.
+__device__ __forceinline__ uint32_t wave_kth_largest1(uint32_t k, uint32_t n) {
+    uint32_t T = 0;
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t Tb = T | (1u << b);
+        if ((uint32_t)__builtin_popcountll(__ballot(k >= Tb)) >= n) T = Tb;
+    }
+    return T;
+}
+__device__ __forceinline__ int lane_id() { return (int)(tid_x() & 63u); }
 // Orders LDS traffic between lanes of one wave (no cross-wave barrier).
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -270,8 +328,8 @@ __device__ __forceinline__ void wave_sync() {
 template <int NT>
 __device__ __forceinline__ float block_max(float v, float* red) {
     v = wave_max(v);
-    const int w = threadIdx.x / kWave;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+    const int w = tid_x() / kWave;
+    if ((tid_x() & 63) == 0) red[w] = v;
     __syncthreads();
     float r = red[0];
 #pragma unroll
@@ -282,8 +340,8 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 template <int NT>
 __device__ __forceinline__ float block_min(float v, float* red) {
     v = wave_min(v);
-    const int w = threadIdx.x / kWave;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+    const int w = tid_x() / kWave;
+    if ((tid_x() & 63) == 0) red[w] = v;
     __syncthreads();
     float r = red[0];
 #pragma unroll
@@ -295,8 +353,8 @@ __device__ __forceinline__ float block_min(float v, float* red) {
 template <int NT>
 __device__ __forceinline__ double block_sum(double v, double* red) {
     v = wave_sum(v);
-    const int w = threadIdx.x / kWave;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+    const int w = tid_x() / kWave;
+    if ((tid_x() & 63) == 0) red[w] = v;
     __syncthreads();
     double r = 0.0;
 #pragma unroll
@@ -307,8 +365,8 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
 template <int NT>
 __device__ __forceinline__ uint32_t block_sum_u(uint32_t v, uint32_t* red) {
     v = wave_sum_u(v);
-    const int w = threadIdx.x / kWave;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+    const int w = tid_x() / kWave;
+    if ((tid_x() & 63) == 0) red[w] = v;
     __syncthreads();
     uint32_t r = 0;
 #pragma unroll
@@ -319,8 +377,8 @@ __device__ __forceinline__ uint32_t block_sum_u(uint32_t v, uint32_t* red) {
 template <int NT>
 __device__ __forceinline__ void block_argmax(float& v, uint32_t& i, float* redv, uint32_t* redi) {
     wave_argmax(v, i);
-    const int w = threadIdx.x / kWave;
-    if ((threadIdx.x & 63) == 0) { redv[w] = v; redi[w] = i; }
+    const int w = tid_x() / kWave;
+    if ((tid_x() & 63) == 0) { redv[w] = v; redi[w] = i; }
     __syncthreads();
     float bv = redv[0];
     uint32_t bi = redi[0];
@@ -335,8 +393,8 @@ __device__ __forceinline__ void block_argmax(float& v, uint32_t& i, float* redv,
 template <int NT>
 __device__ __forceinline__ uint64_t block_min_u64(uint64_t v, uint64_t* red) {
     v = wave_min_u64(v);
-    const int w = threadIdx.x / kWave;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+    const int w = tid_x() / kWave;
+    if ((tid_x() & 63) == 0) red[w] = v;
     __syncthreads();
     uint64_t r = red[0];
 #pragma unroll
@@ -348,7 +406,7 @@ __device__ __forceinline__ uint64_t block_min_u64(uint64_t v, uint64_t* red) {
 // Exclusive prefix sum of one uint32 per thread; returns the block total.
 template <int NT>
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t& excl, uint32_t* red) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x / kWave;
+    const int lane = tid_x() & 63, w = tid_x() / kWave;
     const uint32_t inc = wave_scan_incl_u(v);
     if (lane == 63) red[w] = inc;
     __syncthreads();
@@ -369,7 +427,7 @@ template <int NT>
 __device__ void bitonic_sort(uint64_t* a, uint32_t n) {
     for (uint32_t k = 2; k <= n; k <<= 1) {
         for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-            for (uint32_t i = threadIdx.x; i < n; i += NT) {
+            for (uint32_t i = tid_x(); i < n; i += NT) {
                 const uint32_t ixj = i ^ j;
                 if (ixj > i) {
                     const uint64_t x = a[i], y = a[ixj];
@@ -424,7 +482,7 @@ __device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0
 __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected, uint32_t* flag_lds) {
     wait_all_memory();
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid_x() == 0) {
         const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const bool last = prev == expected - 1;
         if (last) st_dev(counter, 0u);
@@ -458,6 +516,16 @@ __device__ __forceinline__ uint32_t scalar_load_u8(const uint8_t* p) {
 }
 
 // ------------------------------------------------------- vector loads ----
+// Raw buffer loads: a scalar resource over [base, base + bytes) and one
+// 32-bit lane offset; a load that does not fit in the range reads as 0
+// instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    return make_uint4(x[0], x[1], x[2], x[3]);
+}
 // 16-byte group loads: 4 f32 or 8 bf16 elements.
 __device__ __forceinline__ uint4 load16(const void* base, uint64_t group) {
     return reinterpret_cast<const uint4*>(base)[group];
@@ -498,12 +566,12 @@ __device__ __forceinline__ void stream_groups(const void* rowp, uint32_t V, F&& 
         uint4 r[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const uint32_t gi = g0 + u * NT + threadIdx.x;
+            const uint32_t gi = g0 + u * NT + tid_x();
             r[u] = load16(rowp, gi < ng ? gi : 0u);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const uint32_t gi = g0 + u * NT + threadIdx.x;
+            const uint32_t gi = g0 + u * NT + tid_x();
             if (gi < ng) {
                 float v[G];
                 decode<G>(r[u], v);

@@ -64,9 +64,9 @@ template <int NT>
 __device__ void block_topn(TopList& t, uint32_t n, uint64_t* buf) {
     constexpr uint32_t kSlots = (NT / kWave) * kTopMax;
     const uint32_t p2 = next_pow2(kSlots);
-    for (uint32_t i = threadIdx.x; i < p2; i += NT) buf[i] = ~0ull;
+    for (uint32_t i = tid_x(); i < p2; i += NT) buf[i] = ~0ull;
     __syncthreads();
-    const int lane = threadIdx.x & 63, w = threadIdx.x / kWave;
+    const int lane = tid_x() & 63, w = tid_x() / kWave;
     for (uint32_t r = 0; r < n; ++r) {
         float bv = t.v[0];
         uint32_t bi = t.i[0];
@@ -149,7 +149,7 @@ template <int NT>
 __device__ void bitonic_sort_u32(uint32_t* a, uint32_t n) {
     for (uint32_t k = 2; k <= n; k <<= 1) {
         for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-            for (uint32_t i = threadIdx.x; i < n; i += NT) {
+            for (uint32_t i = tid_x(); i < n; i += NT) {
                 const uint32_t ixj = i ^ j;
                 if (ixj > i) {
                     const uint32_t x = a[i], y = a[ixj];
@@ -180,7 +180,7 @@ __device__ __forceinline__ void write_logprobs(const SampleArgs& a, uint32_t row
 template <int NT, uint32_t NB, uint32_t CAP, uint32_t DCAP, int G>
 __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_t row, ExactSmem<NT, NB, CAP, DCAP>& sm) {
     static_assert(NB % NT == 0 || NT % NB == 0, "bins vs threads");
-    const uint32_t tid = threadIdx.x;
+    const uint32_t tid = tid_x();
     const lcs_params P = a.params[row];
     const uint32_t V = a.vocab;
     const uint32_t esz = a.dtype == LCS_BF16 ? 2u : 4u;
@@ -927,7 +927,7 @@ __device__ __forceinline__ SampleArgs uniform_args(const SampleArgs& s) {
 __device__ __forceinline__ void stage_args(SampleArgs* dst) {
     static_assert(sizeof(SampleArgs) % 4 == 0 && sizeof(SampleArgs) / 4 <= 64, "args size");
     const uint32_t* src = (const uint32_t*)__builtin_amdgcn_kernarg_segment_ptr();
-    if (threadIdx.x < sizeof(SampleArgs) / 4) reinterpret_cast<uint32_t*>(dst)[threadIdx.x] = src[threadIdx.x];
+    if (tid_x() < sizeof(SampleArgs) / 4) reinterpret_cast<uint32_t*>(dst)[tid_x()] = src[tid_x()];
     __syncthreads();
 }
 

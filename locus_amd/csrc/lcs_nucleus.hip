@@ -117,7 +117,7 @@ struct SliceIn {
     // logits first, then the history window ids and the mask words
     __device__ __forceinline__ void start(const SampleArgs& a, uint32_t row, uint32_t slice,
                                           const lcs_params& P, bool masked) {
-        const uint32_t tid = threadIdx.x;
+        const uint32_t tid = tid_x();
         V = a.vocab;
         rowp = static_cast<const char*>(a.logits) + (uint64_t)row * a.row_stride * (G == 8 ? 2u : 4u);
         lo = slice * a.slice_len;
@@ -164,7 +164,7 @@ struct SliceIn {
         uint32_t w[NG];
 #pragma unroll
         for (int j = 0; j < NG; ++j) {
-            const uint32_t e0 = lo + (j * NT + threadIdx.x) * G;
+            const uint32_t e0 = lo + (j * NT + tid_x()) * G;
             const uint32_t ee = e0 < hi ? e0 : lo;
             w[j] = mrow[ee >> 5] >> (ee & 31u);
         }
@@ -175,11 +175,11 @@ struct SliceIn {
     }
     __device__ __forceinline__ void clear(NucSmem& sm) const {
 #pragma unroll
-        for (int i = 0; i < (int)(kSliceMax / 4 / NT); ++i) sm.u.ovr4[i * NT + threadIdx.x] = make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < (int)(kSliceMax / 4 / NT); ++i) sm.u.ovr4[i * NT + tid_x()] = make_uint4(0, 0, 0, 0);
     }
     // values; positions past the slice read as -inf
     __device__ __forceinline__ void decode() {
-        const uint32_t tid = threadIdx.x, wv = tid / kWave;
+        const uint32_t tid = tid_x(), wv = tid / kWave;
         const float NEG = -__builtin_huge_valf();
 #pragma unroll
         for (int j = 0; j < NG; ++j) {
@@ -195,7 +195,7 @@ struct SliceIn {
         }
     }
     __device__ __forceinline__ uint32_t eid(int q) const {
-        return lo + ((q / G) * NT + threadIdx.x) * G + (uint32_t)(q % G);
+        return lo + ((q / G) * NT + tid_x()) * G + (uint32_t)(q % G);
     }
     // bit q: element q is a candidate (in the slice and, when the row's mask
     // is used, allowed)
@@ -215,7 +215,7 @@ struct SliceIn {
     // counts of the in-slice history ids; the thread whose increment finds 0
     // owns the id and fetches its raw logit
     __device__ __forceinline__ void count_gather(NucSmem& sm) {
-        const uint32_t tid = threadIdx.x;
+        const uint32_t tid = tid_x();
         auto one = [&](const uint32_t (&h)[HC], uint32_t c0, uint32_t& own, float (&r)[HC]) {
 #pragma unroll
             for (int k = 0; k < HC; ++k) {
@@ -251,7 +251,7 @@ struct SliceIn {
         for (int j = 0; j < NG; ++j) {
 #pragma unroll
             for (int h4 = 0; h4 < G / 4; ++h4) {
-                const uint4 o = sm.u.ovr4[((j * NT + threadIdx.x) * G) / 4 + h4];
+                const uint4 o = sm.u.ovr4[((j * NT + tid_x()) * G) / 4 + h4];
                 const uint32_t ob[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
@@ -299,7 +299,7 @@ __device__ __forceinline__ uint32_t nuc_sub(float f, uint32_t b0, uint32_t b1) {
 __device__ __forceinline__ bool nuc_arrive(uint32_t* counter, uint32_t S, NucSmem& sm) {
     wait_all_memory();
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid_x() == 0) {
         const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const bool last = prev == S - 1;
         if (last) st_dev(counter, 0u);
@@ -313,9 +313,9 @@ __device__ __forceinline__ bool nuc_arrive(uint32_t* counter, uint32_t S, NucSme
 __device__ __forceinline__ bool nuc_row(const SampleArgs& a, uint32_t& row, uint32_t& slice, lcs_params& P,
                                         bool& masked) {
     const uint32_t S = a.slices;
-    row = a.nuc_row0 + blockIdx.x / S;
-    slice = blockIdx.x % S;
-    if (row >= a.rows || blockIdx.x / S >= kNucRows) return false;
+    row = a.nuc_row0 + wg_x() / S;
+    slice = wg_x() % S;
+    if (row >= a.rows || wg_x() / S >= kNucRows) return false;
     P = scalar_load(a.params + row);
     masked = a.mask != nullptr && (a.has_mask == nullptr || scalar_load_u8(a.has_mask + row) != 0);
     return row_mode(P, masked, a.vocab) == kModeNucleus;
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     lcs_params P;
     bool masked;
     if (!nuc_row(a, row, slice, P, masked)) return;
-    const uint32_t tid = threadIdx.x, S = a.slices;
+    const uint32_t tid = tid_x(), S = a.slices;
     const int lane = lane_id(), wv = (int)(tid / kWave);
     const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
     const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
@@ -573,7 +573,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     lcs_params P;
     bool masked;
     if (!nuc_row(a, row, slice, P, masked)) return;
-    const uint32_t tid = threadIdx.x, S = a.slices;
+    const uint32_t tid = tid_x(), S = a.slices;
     const uint32_t wrow = row - a.nuc_row0;
     NucRow* nr = a.nrow + wrow;
     if (scalar_load(&nr->flags) & kNucFallback) return;   // resolved by the exact path
@@ -822,7 +822,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
         return;
     }
     const SampleArgs a = uniform_args(sm.l.args);
-    const uint32_t tid = threadIdx.x;
+    const uint32_t tid = tid_x();
     const int lane = lane_id(), wv = (int)(tid / kWave);
     const lcs_params P = scalar_load(a.params + row);
     const uint32_t wrow = row - a.nuc_row0;
@@ -1174,7 +1174,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     lcs_params P;
     bool masked;
     if (!nuc_row(a, row, slice, P, masked)) return;
-    const uint32_t tid = threadIdx.x, S = a.slices;
+    const uint32_t tid = tid_x(), S = a.slices;
     const int lane = lane_id(), wv = (int)(tid / kWave);
     const uint32_t wrow = row - a.nuc_row0;
     NucRow* nr = a.nrow + wrow;

@@ -32,7 +32,7 @@ namespace lcs {
 template <int G>
 __global__ __launch_bounds__(kGenThreads) void general_kernel(SampleArgs a) {
     __shared__ ExactSmem<kGenThreads, kGenBins, kGenCap, kGenHistCap> sm;
-    const uint32_t row = blockIdx.x;
+    const uint32_t row = wg_x();
     if (row >= a.rows) return;
     const lcs_params P = a.params[row];
     const bool masked = a.mask != nullptr && (a.has_mask == nullptr || a.has_mask[row] != 0);
@@ -49,12 +49,12 @@ __device__ uint64_t g_prof[16384 * 32];
 #define PROF_MARK(k)                                                              \
     do {                                                                          \
         __syncthreads();                                                          \
-        if (threadIdx.x == 0 && blockIdx.x < 16384) g_prof[blockIdx.x * 32 + (k)] = wall_clock64(); \
+        if (tid_x() == 0 && wg_x() < 16384) g_prof[wg_x() * 32 + (k)] = wall_clock64(); \
     } while (0)
 // wave-level mark (no barrier), for the single-wave publish and finalize
 #define PROF_WMARK(k)                                                             \
     do {                                                                          \
-        if ((threadIdx.x & 63) == 0 && blockIdx.x < 16384) g_prof[blockIdx.x * 32 + (k)] = wall_clock64(); \
+        if ((tid_x() & 63) == 0 && wg_x() < 16384) g_prof[wg_x() * 32 + (k)] = wall_clock64(); \
     } while (0)
 #else
 #define PROF_MARK(k) \
@@ -170,8 +170,8 @@ __device__ __forceinline__ bool fin_logprobs(const SampleArgs& a, const uint64_t
     const double s_raw = mine ? bits_d(h1) : 0.0;
     const uint32_t nts = mine ? (uint32_t)(h4 >> 32) : 0u;
     const float M = wave_max(m_raw);
-    const double z = wave_sum(mine && m_raw != NEG ? s_raw * exp((double)m_raw - (double)M) : 0.0);
-    const double log_z = log(z) + (double)M;
+    const double z = wave_sum(mine && m_raw != NEG ? s_raw * exp_f64((double)m_raw - (double)M) : 0.0);
+    const double log_z = log_f64(z) + (double)M;
     if (lane == 0) sm.l.log_z = log_z;
     if (ntop == 0) return false;
     if (ballot(mine && (flags & rec::kFlagCandOverflow))) return true;
@@ -216,7 +216,7 @@ __device__ __forceinline__ void fin_norm(const SampleArgs& a, const uint64_t* re
     const double berr = mine ? bits_d(h6) : 0.0;
     const float maxl = wave_max(m_pen);
     const double d_s = mine ? ((double)m_pen - (double)maxl) * (double)inv_t : 0.0;
-    const double es = mine && m_pen != NEG ? exp(d_s) : 0.0;
+    const double es = mine && m_pen != NEG ? exp_f64(d_s) : 0.0;
     const double Sf = wave_sum(es * bulk);
     // the reference rounds (p - maxl) * inv_t in float: relative 2^-23 of the
     // slice-to-row part |d_s| as well as of each term's own offset
@@ -351,7 +351,7 @@ __device__ __forceinline__ bool fin_window(const SampleArgs& a, const uint64_t* 
         if (e < L0) {
             sm.u.f.sorted[rk[c]] = k[c];
             sm.u.f.sortedraw[rk[c]] = sm.u.f.entraw[e];
-            sm.u.f.sw[rk[c]] = exp((double)tempered(rank_val(k[c]), maxl, inv_t));
+            sm.u.f.sw[rk[c]] = exp_f64((double)tempered(rank_val(k[c]), maxl, inv_t));
         }
     }
     if (lane == 0) { sm.l.fin_L0 = L0; sm.l.fin_maxl = maxl; }
@@ -364,7 +364,7 @@ __device__ __forceinline__ bool fin_window(const SampleArgs& a, const uint64_t* 
 __device__ __forceinline__ void fin_fetch_topk(const uint64_t* recs, uint32_t S, uint32_t K, SliceSmem& sm) {
     constexpr uint32_t NF = 2 * kWave;                  // fetching threads
     constexpr uint32_t SL = kTopKMerge / NF;            // slots per thread
-    const uint32_t t = threadIdx.x - 2 * kWave;
+    const uint32_t t = tid_x() - 2 * kWave;
     uint64_t kk[SL];
     uint32_t rr[SL];
 #pragma unroll
@@ -415,7 +415,7 @@ __device__ __forceinline__ bool fin_topk_lengths(uint32_t S, uint32_t K, SliceSm
 //      over 16 lists at a time in lockstep (loads always in bounds). Rank keys
 //      are unique, so ranks below Ke are distinct.
 __device__ __forceinline__ void fin_merge_topk(uint32_t S, uint32_t K, SliceSmem& sm, float inv_t) {
-    const uint32_t tid = threadIdx.x;
+    const uint32_t tid = tid_x();
     const int lane = lane_id();
     static_assert(kTopKMerge <= 4 * kSliceThreads && kTopKMax <= 64 && kMaxSlices <= kWave, "merge shape");
     if (tid < kWave) {
@@ -511,7 +511,7 @@ __device__ __forceinline__ void fin_merge_topk(uint32_t S, uint32_t K, SliceSmem
     PROF_WMARK(17);
     if (tid >= kWave) return;
     const float maxl = rank_val(sm.u.f.sorted[0]);
-    const double w = (uint32_t)lane < Ke ? exp((double)tempered(rank_val(sm.u.f.sorted[lane]), maxl, inv_t)) : 0.0;
+    const double w = (uint32_t)lane < Ke ? exp_f64((double)tempered(rank_val(sm.u.f.sorted[lane]), maxl, inv_t)) : 0.0;
     if ((uint32_t)lane < Ke) sm.u.f.sw[lane] = w;
     const double Sf = wave_sum(w);
     if (lane == 0) {
@@ -525,10 +525,10 @@ __device__ __forceinline__ void fin_merge_topk(uint32_t S, uint32_t K, SliceSmem
 // Top-p, then min-p (sampling.cpp order), then the draw, 64 ranked row-window
 // entries at a time over the weights in sw. Returns true when a top-p / min-p
 // decision lies within the normaliser's error bound.
-__device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, SliceSmem& sm, uint32_t path) {
+__device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, SliceSmem& sm, uint32_t path,
+                                           const lcs_params& P, double u) {
     const int lane = lane_id();
     PROF_WMARK(12);
-    const lcs_params P = a.params[row];
     const uint32_t L0 = sm.l.fin_L0;
     const float maxl = sm.l.fin_maxl;
     const double Sf = sm.l.fin_S, rel = sm.l.fin_rel;
@@ -537,7 +537,6 @@ __device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, Sl
     const double tp = (double)P.top_p;
     const double inv_S = 1.0 / Sf;
     const double mp = (double)P.min_p;
-    const double u = a.u[row];
     // one inclusive scan of the weights per 64 entries serves the top-p sums
     // (cum = W / S), the kept mass and the draw
     double Wc = 0.0, kept_sum = 0.0;
@@ -628,12 +627,14 @@ __device__ __forceinline__ bool fin_row(uint32_t row, uint32_t mode, const lcs_p
                                         const uint64_t* recs) {
     SliceSmem& sm = g_slice;
     const SampleArgs a = uniform_args(sm.l.args);
-    const uint32_t tid = threadIdx.x;
+    const uint32_t tid = tid_x();
     const int lane = lane_id(), wv = (int)(tid / kWave);
     const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
     const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
     const bool stoch = mode == kModeWindow, topk = mode == kModeTopK;
     const float inv_t = fdiv(1.0f, P.temperature);
+    // the row's uniform, requested with the slice records
+    const double u = (stoch || topk) && wv == 0 ? a.u[row] : 0.0;
     bool fb = false;
     if (topk) {
         if (wv == 0) {
@@ -661,7 +662,7 @@ __device__ __forceinline__ bool fin_row(uint32_t row, uint32_t mode, const lcs_p
     __syncthreads();
     if (sm.l.fin_fb) return true;
     if (wv == 0 && (stoch || topk)) {
-        fb = fin_decide(a, row, sm, topk ? LCS_PATH_TOPK : LCS_PATH_WINDOW);
+        fb = fin_decide(a, row, sm, topk ? LCS_PATH_TOPK : LCS_PATH_WINDOW, P, u);
         if (fb && lane == 0) sm.l.fin_fb = 1u;
     }
     __syncthreads();
@@ -693,10 +694,10 @@ void slice_kernel(SampleArgs a) {
     constexpr int NG = kSliceElems / G;   // 16-byte groups per thread
     constexpr int HC = 8;                 // history ids per thread per chunk
     SliceSmem& sm = g_slice;
-    const uint32_t tid = threadIdx.x;
+    const uint32_t tid = tid_x();
     const int lane = lane_id(), wv = (int)(tid / kWave);
     const uint32_t S = a.slices;
-    const uint32_t row = blockIdx.x / S, slice = blockIdx.x % S;
+    const uint32_t row = wg_x() / S, slice = wg_x() % S;
     if (row >= a.rows) return;
     if ((a.flags & LCS_WRITE_PENALIZED) != 0) return;
     PROF_MARK(0);
@@ -1007,7 +1008,8 @@ void slice_kernel(SampleArgs a) {
             bs += c[0];
         }
         // window test in float, rounded down from the exact threshold (a superset)
-        const double delta = (double)P.temperature * (-log((double)P.min_p) + 1e-3);
+        const double delta = (double)P.temperature *
+                             (-(double)__builtin_amdgcn_logf(P.min_p) * 0.6931471805599453 * (1.0 + 1e-6) + 1e-3);
         if (tid == 0) sm.l.win_delta = delta;   // for this workgroup's finalize, if last
         const double thr = (double)ms - delta;
         float thr_f = (float)thr;

@@ -28,7 +28,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     __shared__ double redd[NT / kWave];
     __shared__ uint32_t last;
     const uint32_t rows = a.n_seq * a.rows_per_seq;
-    const uint32_t row = blockIdx.x;
+    const uint32_t row = wg_x();
     if (row >= rows) return;
     const uint32_t V = a.vocab;
     const uint32_t esz = a.dtype == LCS_BF16 ? 2u : 4u;
@@ -45,12 +45,12 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
         uint4 r[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const uint32_t gi = g0 + u * NT + threadIdx.x;
+            const uint32_t gi = g0 + u * NT + tid_x();
             r[u] = load16(rowp, gi < ng ? gi : 0u);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const uint32_t gi = g0 + u * NT + threadIdx.x;
+            const uint32_t gi = g0 + u * NT + tid_x();
             if (gi >= ng) continue;
             float v[G];
             decode<G>(r[u], v);
@@ -93,7 +93,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     block_argmax<NT>(bm, idx, redf, redu);
     const double sc = om == NEG ? 0.0 : os * exp((double)om - (double)bm);
     const double z = block_sum<NT>(sc, redd);
-    if (threadIdx.x == 0) {
+    if (tid_x() == 0) {
         const double log_z = log(z) + (double)bm;
         const int32_t d = a.draft[row];
         float lp = 0.0f;
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
         st_dev(reinterpret_cast<uint32_t*>(a.argmax_ids + row), idx < V ? idx : 0u);
     }
     if (!arrive_last(a.counters + row / a.rows_per_seq, a.rows_per_seq, &last)) return;
-    if (threadIdx.x == 0) {
+    if (tid_x() == 0) {
         const uint32_t seq = row / a.rows_per_seq;
         const uint32_t base = seq * a.rows_per_seq;
         uint32_t acc = 0;
