@@ -697,7 +697,13 @@ void slice_kernel(SampleArgs a) {
     const uint32_t tid = tid_x();
     const int lane = lane_id(), wv = (int)(tid / kWave);
     const uint32_t S = a.slices;
-    const uint32_t row = wg_x() / S, slice = wg_x() % S;
+    // Workgroups are dealt to the 8 XCDs round-robin; when the grid divides
+    // evenly, a row's slices are placed on one XCD so that its L2 serves the
+    // row's history ids to all of them.
+    uint32_t blk = wg_x();
+    const uint32_t nblk = a.rows * S;   // the launch's grid
+    if ((nblk & 7u) == 0u) blk = (blk & 7u) * (nblk >> 3) + (blk >> 3);
+    const uint32_t row = blk / S, slice = blk % S;
     if (row >= a.rows) return;
     if ((a.flags & LCS_WRITE_PENALIZED) != 0) return;
     PROF_MARK(0);
