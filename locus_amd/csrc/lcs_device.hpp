@@ -307,6 +307,18 @@ __device__ __forceinline__ uint32_t wave_kth_largest4(const uint32_t (&k)[4], ui
     }
     return T;
 }
+// As wave_kth_largest4, over keys below 2^16 (16 steps).
+__device__ __forceinline__ uint32_t wave_kth_largest4_16(const uint32_t (&k)[4], uint32_t n) {
+    uint32_t T = 0;
+    for (int b = 15; b >= 0; --b) {
+        const uint32_t Tb = T | (1u << b);
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) cnt += (uint32_t)__builtin_popcountll(__ballot(k[c] >= Tb));
+        if (cnt >= n) T = Tb;
+    }
+    return T;
+}
 // The n-th largest of the wave's 64 keys (1 <= n <= 64), as above.
 __device__ __forceinline__ uint32_t wave_kth_largest1(uint32_t k, uint32_t n) {
     uint32_t T = 0;

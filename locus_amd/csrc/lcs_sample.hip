@@ -84,7 +84,6 @@ struct SliceLocal {
     uint32_t nall[kSliceWaves];
     double sraw[kSliceWaves];
     double bulk[kSliceWaves];
-    double bterm[kSliceWaves];
     uint32_t ncand, nwin, last;
     // finalize hand-off between its waves
     double log_z, fin_S, fin_rel;
@@ -683,6 +682,19 @@ __device__ __forceinline__ bool fin_row(uint32_t row, uint32_t mode, const lcs_p
     return false;
 }
 
+// A bound of sum c|t| over a slice's n bulk terms c = 2^t, from their sum S
+// (taken from above): terms with t < 0 (c < 1) add -c log2 c, at most
+// S log2(n / S) for S <= n / e and n log2(e) / e beyond (the entropy bound);
+// terms with t > 0 (values within rounding of the slice max) have
+// 0 < t <= 2^-24 |ms kk| (the rounding of -ms kk), and number at most S / c.
+__device__ __forceinline__ double ent_bound(double S, uint32_t n, float mk) {
+    if (!(S > 0.0)) return 0.0;
+    const double dn = (double)n;
+    const double h = S <= dn * 0.36787944117144233 ? S * log_f64(dn / S) * 1.4426950408889634
+                                                   : dn * 0.5307378454223266;   // n log2(e) / e
+    return h + S * (double)mk * 0x1.4p-24;
+}
+
 // One workgroup per (row, slice of <= 8192 logits); 32 logits per thread in
 // registers. Penalised logits reach the slice through an LDS table of
 // override bits written once per distinct history id. Every slice publishes a
@@ -806,10 +818,17 @@ void slice_kernel(SampleArgs a) {
     }
     auto eid = [&](int q) { return lo + ((q / G) * NT + tid) * G + (uint32_t)(q % G); };
 
-    // ---- raw lane maxima, shared for the slice's statistics ----
+    // ---- raw lane maxima, shared for the slice's statistics; the maxima of
+    // the lane's 16-byte groups let threshold scans test a group at a time ----
     float lm = NEG;
+    float gm[NG];
 #pragma unroll
-    for (int q = 0; q < kSliceElems; ++q) lm = fmaxf(lm, v[q]);
+    for (int j = 0; j < NG; ++j) {
+        gm[j] = v[j * G];
+#pragma unroll
+        for (int k = 1; k < G; ++k) gm[j] = fmaxf(gm[j], v[j * G + k]);
+        lm = fmaxf(lm, gm[j]);
+    }
     sm.l.lmax[tid] = lm;
     // counts, then the owners' raw logits (in flight while the raw statistics run)
     uint32_t oA = 0, oB = 0;
@@ -835,9 +854,10 @@ void slice_kernel(SampleArgs a) {
         }
     }
     __syncthreads();
-    // the raw slice max from the 256 lane maxima; one wave also finds the
-    // ntop-th largest of them, a lower bound of the slice's top-n, while the
-    // others start the raw sums
+    // the raw slice max from the 256 lane maxima; one wave also finds a lower
+    // bound t of the slice's top-n while the others start the raw sums: the
+    // ntop-th largest lane max, its sort key cut to 16 bits (elements >= t
+    // include every element of the top-n)
     float Ms;
     {
         float m4[kSliceWaves];
@@ -848,8 +868,9 @@ void slice_kernel(SampleArgs a) {
             __builtin_amdgcn_s_setprio(2);   // a serial chain among busy waves
             uint32_t k4[kSliceWaves];
 #pragma unroll
-            for (int c = 0; c < kSliceWaves; ++c) k4[c] = fkey(m4[c]);
-            const float t = key_to_f(wave_kth_largest4(k4, ntop));
+            for (int c = 0; c < kSliceWaves; ++c) k4[c] = fkey(m4[c]) >> 16;
+            const uint32_t kneg = 0x007fffffu;   // fkey(-inf)
+            const float t = key_to_f(max(wave_kth_largest4_16(k4, ntop) << 16, kneg));
             if (lane == 0) sm.l.t_s = t;
             __builtin_amdgcn_s_setprio(0);
         }
@@ -903,12 +924,14 @@ void slice_kernel(SampleArgs a) {
     if (ntop) {
         const float t = sm.l.t_s;
         if (ballot(lm >= t)) {
-            if (lm >= t) {
 #pragma unroll
-                for (int q = 0; q < kSliceElems; ++q) {
-                    if (v[q] >= t) {
+            for (int j = 0; j < NG; ++j) {
+                if (gm[j] >= t) {
+#pragma unroll
+                    for (int k = 0; k < G; ++k) {
+                        const int q = j * G + k;
                         const uint32_t e = eid(q);
-                        if (e < hi) {
+                        if (v[q] >= t && e < hi) {
                             const uint32_t s = atomicAdd(&sm.l.ncand, 1u);
                             if (s < kCandCap) sm.l.ck[s] = rank_key(v[q], e);
                         }
@@ -934,7 +957,8 @@ void slice_kernel(SampleArgs a) {
             }
         }
     }
-    float lpm = NEG;   // lane max of the penalised values (sampled rows)
+    float lpm = NEG;   // lane max of the penalised values (sampled rows); gm
+                       // then holds the group maxima of the penalised values
     if (mode == kModeGreedy) {
         // first index of the max, over all ids and over the allowed ids;
         // the raw logit of each winner rides along for its logprob
@@ -972,11 +996,16 @@ void slice_kernel(SampleArgs a) {
         if (lane == 0) {
             sm.l.mpen[wv] = bv; sm.l.ipen[wv] = bi; sm.l.rpen[wv] = br;
             sm.l.mmsk[wv] = mv; sm.l.imsk[wv] = mi; sm.l.rmsk[wv] = mr; sm.l.nall[wv] = na;
-            sm.l.bulk[wv] = 0.0; sm.l.bterm[wv] = 0.0;
+            sm.l.bulk[wv] = 0.0;
         }
     } else {
 #pragma unroll
-        for (int q = 0; q < kSliceElems; ++q) lpm = fmaxf(lpm, v[q]);
+        for (int j = 0; j < NG; ++j) {
+            gm[j] = v[j * G];
+#pragma unroll
+            for (int k = 1; k < G; ++k) gm[j] = fmaxf(gm[j], v[j * G + k]);
+            lpm = fmaxf(lpm, gm[j]);
+        }
         const float pm = wave_max(lpm);
         if (lane == 0) { sm.l.mpen[wv] = pm; sm.l.ipen[wv] = kNoIdx; sm.l.nall[wv] = 0; }
         wave_sync();
@@ -994,19 +1023,15 @@ void slice_kernel(SampleArgs a) {
         const float kk = fmul(inv_t, kLog2E);
         // bulk term c = 2^t, t = RN(p kk + bb) = (p - ms) kk + e + rounding, with
         // bb = RN(-ms kk) and e = ms kk + bb common to all terms (taken out in
-        // f64 below); sum of c|t| bounds the rounding of t here and in the
-        // reference's tempered offsets (t clamped so that -inf logits add 0)
+        // f64 below); the publish bounds the sum of c|t|, which bounds the
+        // rounding of t here and in the reference's tempered offsets
         const float bb = -ms * kk;
-        float bs = 0.0f, bt = 0.0f;
+        float bs = 0.0f;
 #pragma unroll
         for (int j = 0; j < NG; ++j) {
             float c[G];
 #pragma unroll
-            for (int k = 0; k < G; ++k) {
-                const float t = fmaxf(fmaf(v[j * G + k], kk, bb), -1e30f);
-                c[k] = fast_exp2(t);
-                bt = fmaf(c[k], -t, bt);
-            }
+            for (int k = 0; k < G; ++k) c[k] = fast_exp2(fmaf(v[j * G + k], kk, bb));
 #pragma unroll
             for (int w = G / 2; w >= 1; w /= 2)
 #pragma unroll
@@ -1021,12 +1046,16 @@ void slice_kernel(SampleArgs a) {
         float thr_f = (float)thr;
         if ((double)thr_f > thr) thr_f = next_down(thr_f);
         if (ballot(lpm >= thr_f)) {
-            if (lpm >= thr_f) {
 #pragma unroll
-                for (int q = 0; q < kSliceElems; ++q) {
-                    if (v[q] >= thr_f) {
-                        const uint32_t s = atomicAdd(&sm.l.nwin, 1u);
-                        if (s < kWinLds) sm.l.wk[s] = rank_key(v[q], eid(q));
+            for (int j = 0; j < NG; ++j) {
+                if (gm[j] >= thr_f) {
+#pragma unroll
+                    for (int k = 0; k < G; ++k) {
+                        const int q = j * G + k;
+                        if (v[q] >= thr_f) {
+                            const uint32_t s = atomicAdd(&sm.l.nwin, 1u);
+                            if (s < kWinLds) sm.l.wk[s] = rank_key(v[q], eid(q));
+                        }
                     }
                 }
             }
@@ -1034,8 +1063,7 @@ void slice_kernel(SampleArgs a) {
         const double eb = ((double)ms * (double)kk + (double)bb) * 0.6931471805599453;
         const double fe = 1.0 - eb + 0.5 * eb * eb;   // 2^-e, |e| tiny
         const double bsum = (double)wave_sum_f(bs) * fe;
-        const double btsum = (double)wave_sum_f(bt) * fe;
-        if (lane == 0) { sm.l.bulk[wv] = bsum; sm.l.bterm[wv] = btsum; }
+        if (lane == 0) sm.l.bulk[wv] = bsum;
     } else if (topk) {
         // the slice's top-k by penalised value (sampling.cpp:87-97): elements
         // >= the k-th largest penalised lane maximum of the slice
@@ -1046,12 +1074,14 @@ void slice_kernel(SampleArgs a) {
         for (int c = 0; c < kSliceWaves; ++c) k4[c] = fkey(sm.l.lmax[lane + c * kWave]);
         const float t = key_to_f(wave_kth_largest4(k4, P.top_k));
         if (ballot(lpm >= t)) {
-            if (lpm >= t) {
 #pragma unroll
-                for (int q = 0; q < kSliceElems; ++q) {
-                    if (v[q] >= t) {
+            for (int j = 0; j < NG; ++j) {
+                if (gm[j] >= t) {
+#pragma unroll
+                    for (int k = 0; k < G; ++k) {
+                        const int q = j * G + k;
                         const uint32_t e = eid(q);
-                        if (e < hi) {
+                        if (v[q] >= t && e < hi) {
                             const uint32_t s = atomicAdd(&sm.l.nwin, 1u);
                             if (s < kWinLds) sm.l.wk[s] = rank_key(v[q], e);
                         }
@@ -1059,7 +1089,7 @@ void slice_kernel(SampleArgs a) {
                 }
             }
         }
-        if (lane == 0) { sm.l.bulk[wv] = 0.0; sm.l.bterm[wv] = 0.0; }
+        if (lane == 0) sm.l.bulk[wv] = 0.0;
     }
     PROF_MARK(4);
     __syncthreads();
@@ -1085,7 +1115,8 @@ void slice_kernel(SampleArgs a) {
             bk = wave_sum(lw ? sm.l.bulk[wl] : 0.0);
             // f32 terms: exp2 and the per-lane and cross-lane f32 sums within
             // 2^-19 of the bulk; the offsets' roundings within 2^-22 c|t|
-            be = wave_sum(lw ? sm.l.bterm[wl] : 0.0) * 0x1p-22 + bk * 0x1p-19 + (double)len * 0x1p-120;
+            be = ent_bound(bk * (1.0 + 0x1p-18), len, fabsf(ma) * fmul(fdiv(1.0f, P.temperature), kLog2E)) * 0x1p-22 +
+                 bk * 0x1p-19 + (double)len * 0x1p-120;
         } else {
             const uint32_t ia0 = ia, im0 = im;
             wave_argmax(ma, ia);
