@@ -49,12 +49,12 @@ __device__ uint64_t g_prof[16384 * 32];
 #define PROF_MARK(k)                                                              \
     do {                                                                          \
         __syncthreads();                                                          \
-        if (tid_x() == 0 && wg_x() < 16384) g_prof[wg_x() * 32 + (k)] = wall_clock64(); \
+        if (tid_x() == 0 && wg_x() < 16384) g_prof[wg_x() * 32 + (k)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
 // wave-level mark (no barrier), for the single-wave publish and finalize
 #define PROF_WMARK(k)                                                             \
     do {                                                                          \
-        if ((tid_x() & 63) == 0 && wg_x() < 16384) g_prof[wg_x() * 32 + (k)] = wall_clock64(); \
+        if ((tid_x() & 63) == 0 && wg_x() < 16384) g_prof[wg_x() * 32 + (k)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
 #else
 #define PROF_MARK(k) \
@@ -140,7 +140,7 @@ __device__ __forceinline__ float next_down(float x) {
 // and after one barrier wave 0 walks top-p / min-p / the draw. The finalize
 // is a separate function so that its live values do not crowd the slices'
 // main phase; its LDS is the file-scope g_slice.
-constexpr uint32_t kSpecWin = 16;   // window entries fetched with each slice header
+constexpr uint32_t kSpecWin = 4;    // window entries fetched with each slice header
 
 __device__ __forceinline__ float next_up(float x) {
     const uint32_t b = __float_as_uint(x);
@@ -214,6 +214,7 @@ __device__ __forceinline__ void fin_norm(const SampleArgs& a, const uint64_t* re
     const double bulk = mine ? bits_d(h5) : 0.0;
     const double berr = mine ? bits_d(h6) : 0.0;
     const float maxl = wave_max(m_pen);
+    PROF_WMARK(9);
     const double d_s = mine ? ((double)m_pen - (double)maxl) * (double)inv_t : 0.0;
     const double es = mine && m_pen != NEG ? exp_f64(d_s) : 0.0;
     const double Sf = wave_sum(es * bulk);
@@ -289,6 +290,7 @@ __device__ __forceinline__ bool fin_window(const SampleArgs& a, const uint64_t* 
     // (delta as this workgroup's slice phase computed it)
     const double delta = sm.l.win_delta;
     const float maxl = wave_max(m_pen);
+    PROF_WMARK(8);
     const double thr = (double)maxl - delta;
     float thr_up = (float)thr;
     if ((double)thr_up < thr) thr_up = next_up(thr_up);
