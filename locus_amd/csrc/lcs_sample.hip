@@ -141,6 +141,7 @@ __device__ __forceinline__ float next_down(float x) {
 // is a separate function so that its live values do not crowd the slices'
 // main phase; its LDS is the file-scope g_slice.
 constexpr uint32_t kSpecWin = 4;    // window entries fetched with each slice header
+constexpr uint32_t kMaxSlicesFast = 16;   // rows the finalize's one-pass window fetch covers
 
 __device__ __forceinline__ float next_up(float x) {
     const uint32_t b = __float_as_uint(x);
@@ -262,6 +263,28 @@ __device__ __forceinline__ void fin_greedy(const SampleArgs& a, const uint64_t* 
     }
 }
 
+// The row window's L0 entries (sm.u.f.ent / entraw) ranked into sorted /
+// sortedraw, with their weights in sw.
+__device__ __forceinline__ void fin_window_rank(SliceSmem& sm, uint32_t L0, float maxl, float inv_t) {
+    const int lane = lane_id();
+    wave_sync();
+    PROF_WMARK(10);
+    uint64_t k[4];
+    uint32_t rk[4];
+    lds_rank4(sm.u.f.ent, L0, k, rk);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
+        if (e < L0) {
+            sm.u.f.sorted[rk[c]] = k[c];
+            sm.u.f.sortedraw[rk[c]] = sm.u.f.entraw[e];
+            sm.u.f.sw[rk[c]] = exp_f64((double)tempered(rank_val(k[c]), maxl, inv_t));
+        }
+    }
+    if (lane == 0) { sm.l.fin_L0 = L0; sm.l.fin_maxl = maxl; }
+    PROF_WMARK(11);
+}
+
 // Sampled rows: every entry with p >= maxl - delta, gathered from the slices'
 // rank-ordered lists, ranked into sorted / sortedraw with its weight
 // exp((double)((p - maxl) * inv_t)) in sw. Returns true when the row needs
@@ -275,6 +298,7 @@ __device__ __forceinline__ bool fin_window(const SampleArgs& a, const uint64_t* 
     const uint64_t* my = recs + (mine ? lane : 0) * rec::kWords64;
     const float NEG = -__builtin_huge_valf();
     const uint64_t h0 = ld_dev_u64(my + 0), h2 = ld_dev_u64(my + 2);
+    wave_sync();   // (after a fast pass that wrote the LDS entries)
     uint64_t wk[kSpecWin];
     uint32_t wr[kSpecWin];
 #pragma unroll
@@ -341,23 +365,80 @@ __device__ __forceinline__ bool fin_window(const SampleArgs& a, const uint64_t* 
     }
     // a truncated slice whose every kept entry qualifies may hold more
     if (ballot(mine && (flags & rec::kFlagWinTrunc) && qtot == n_win)) return true;
-    wave_sync();
-    PROF_WMARK(10);
-    uint64_t k[4];
-    uint32_t rk[4];
-    lds_rank4(sm.u.f.ent, L0, k, rk);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
-        if (e < L0) {
-            sm.u.f.sorted[rk[c]] = k[c];
-            sm.u.f.sortedraw[rk[c]] = sm.u.f.entraw[e];
-            sm.u.f.sw[rk[c]] = exp_f64((double)tempered(rank_val(k[c]), maxl, inv_t));
-        }
-    }
-    if (lane == 0) { sm.l.fin_L0 = L0; sm.l.fin_maxl = maxl; }
-    PROF_WMARK(11);
+    fin_window_rank(sm, L0, maxl, inv_t);
     return false;
+}
+
+// Sampled rows, the common case: the first kSpecWinT entries of every slice
+// in one pass, lane l holding entry l % 16 of slice 4 g + l / 16 in its
+// group g (16 records' lines per load, 4 lines per load instruction);
+// qualifying entries are compacted by ballot. Returns 0 when done, 1 when the
+// row needs the exact path, 2 when a slice holds more qualifying entries than
+// were fetched (fin_window then fetches the row again).
+constexpr uint32_t kSpecWinT = 16;
+__device__ __forceinline__ uint32_t fin_window_fast(const SampleArgs& a, const uint64_t* recs, SliceSmem& sm,
+                                                    float inv_t) {
+    constexpr int NGR = (int)(kMaxSlicesFast / 4);
+    const int lane = lane_id();
+    const uint32_t S = a.slices;
+    const uint32_t j = (uint32_t)lane & 15u;
+    const float NEG = -__builtin_huge_valf();
+    uint64_t h0[NGR], h2[NGR], wk[NGR], wr[NGR];
+#pragma unroll
+    for (int g = 0; g < NGR; ++g) {
+        const uint32_t sl = (uint32_t)g * 4u + (uint32_t)lane / 16u;
+        const uint64_t* r = recs + (sl < S ? sl : 0u) * rec::kWords64;
+        h0[g] = ld_dev_u64(r + 0);
+        h2[g] = ld_dev_u64(r + 2);
+        wk[g] = ld_dev_u64(r + rec::kWin + j);
+        wr[g] = ld_dev_u64(r + rec::kWinRaw + j);
+    }
+    PROF_WMARK(7);
+    float mp = NEG;
+#pragma unroll
+    for (int g = 0; g < NGR; ++g) {
+        const uint32_t sl = (uint32_t)g * 4u + (uint32_t)lane / 16u;
+        if (sl < S) mp = fmaxf(mp, __uint_as_float((uint32_t)h2[g]));
+    }
+    const double delta = sm.l.win_delta;
+    const float maxl = wave_max(mp);
+    PROF_WMARK(8);
+    const double thr = (double)maxl - delta;
+    float thr_up = (float)thr;
+    if ((double)thr_up < thr) thr_up = next_up(thr_up);
+    const uint64_t below = ((uint64_t)1 << lane) - 1u;
+    uint32_t L0 = 0;
+    bool lost = false, more = false, trunc = false;
+#pragma unroll
+    for (int g = 0; g < NGR; ++g) {
+        const uint32_t sl = (uint32_t)g * 4u + (uint32_t)lane / 16u;
+        const bool in = sl < S;
+        const uint32_t n_win = in ? (uint32_t)(h0[g] >> 32) & 0xffffu : 0u;
+        const uint32_t flags = in ? (uint32_t)(h0[g] >> 48) : 0u;
+        const float m_pen = in ? __uint_as_float((uint32_t)h2[g]) : NEG;
+        // a slice that could hold row-window entries must not have lost any
+        lost = lost || ((flags & rec::kFlagWinLost) && m_pen >= thr_up);
+        // entries are in ascending rank order, so the qualifying ones lead
+        const bool qual = j < n_win && rank_val(wk[g]) >= thr_up;
+        // every fetched entry qualifies and the slice holds more
+        more = more || (j == kSpecWinT - 1u && qual && n_win > kSpecWinT);
+        // a truncated slice whose every kept entry qualifies may hold more
+        trunc = trunc || ((flags & rec::kFlagWinTrunc) && n_win >= 1u && j == n_win - 1u && qual);
+        const uint64_t m = ballot(qual);
+        if (qual) {
+            const uint32_t pos = L0 + (uint32_t)__builtin_popcountll(m & below);
+            if (pos < kRowWin) {
+                sm.u.f.ent[pos] = wk[g];
+                sm.u.f.entraw[pos] = __uint_as_float((uint32_t)wr[g]);
+            }
+        }
+        L0 += (uint32_t)__builtin_popcountll(m);
+    }
+    if (ballot(lost) || L0 > kRowWin) return 1u;
+    if (ballot(more)) return 2u;
+    if (ballot(trunc)) return 1u;
+    fin_window_rank(sm, L0, maxl, inv_t);
+    return 0u;
 }
 
 // Top-k rows: waves 2-3 copy the slices' rank-ordered top-k lists into LDS
@@ -652,7 +733,10 @@ __device__ __forceinline__ bool fin_row(uint32_t row, uint32_t mode, const lcs_p
         PROF_WMARK(15);
         fin_merge_topk(a.slices, P.top_k, sm, inv_t);
     } else if (wv == 0) {
-        if (stoch) fb = fin_window(a, recs, P, sm, inv_t);
+        if (stoch) {
+            const uint32_t r = a.slices <= kMaxSlicesFast ? fin_window_fast(a, recs, sm, inv_t) : 2u;
+            fb = r == 1u || (r == 2u && fin_window(a, recs, P, sm, inv_t));
+        }
         else fin_greedy(a, recs, row, masked, sm);
     } else if (wv == 1) {
         if (want_lp) fb = fin_logprobs(a, recs, row, ntop, sm);
