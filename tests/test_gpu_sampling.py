@@ -436,3 +436,37 @@ def test_random_batches(sampler):
         compare(w32, g, O.sample_batch(w32, threads=16, has_mask=has), f"random-{seed}")
         seen.update(np.unique(g["diag"]["path"]).tolist())
     assert {1, 2, 4, 5, 6} <= seen, seen
+
+
+def test_window_rows_with_many_entries_per_slice(sampler):
+    """Min-p window rows whose row window is planted in chosen slices: up to
+    16 qualifying entries per slice (the finalize's one-pass fetch), 17 to 64
+    in a slice (the per-slice fetch, header with 4 entries then more), a
+    slice past its 64-entry record (exact path) and a row window past 256
+    entries (exact path), including the short last slice."""
+    base = W.make("c2", rows=12, set_index=29)
+    V, S = base.vocab, (base.vocab + 8191) // 8192
+    rng = np.random.default_rng(2029)
+    logits = (rng.standard_normal((base.rows, V)) - 20.0).astype(np.float32)
+    plant = [  # (slice, entries) per row
+        [(0, 3), (7, 2)], [(0, 10)], [(0, 16)], [(0, 17)], [(2, 40), (9, 20)], [(S - 1, 30)],
+        [(0, 64)], [(0, 70)], [(s, 19) for s in range(S)], [(s, 12) for s in range(S)] + [(3, 8)],
+        [(4, 5), (5, 5), (6, 5)], [(1, 33), (14, 1)],
+    ]
+    for r, spots in enumerate(plant):
+        for s, n in spots:
+            lo, hi = s * 8192, min(V, (s + 1) * 8192)
+            idx = rng.choice(np.arange(lo, hi), size=n, replace=False)
+            logits[r, idx] = rng.uniform(9.0, 10.0, size=n).astype(np.float32)
+    p = base.params.copy()
+    p["temperature"], p["min_p"], p["top_p"], p["top_k"] = 1.0, 0.05, 0.9, 0
+    for r in range(0, base.rows, 2):
+        p["repeat_penalty"][r], p["frequency_penalty"][r], p["presence_penalty"][r] = 1.0, 0.0, 0.0
+    w = W.Workload("window-spots", base.rows, V, "f32", logits, p, base.seeds, base.u,
+                   base.hist_off, base.hist_ids, None, 5, True)
+    g = run(sampler, w)
+    compare(w, g, O.sample_batch(w, threads=8), "window-spots", expect_paths={2, 3, 4})
+    paths = g["diag"]["path"]
+    window_rows = [0, 1, 2, 3, 4, 5, 6, 9, 10, 11]
+    assert np.isin(paths[window_rows], [2, 3]).all(), paths.tolist()
+    assert (paths[[7, 8]] == 4).all(), paths.tolist()
