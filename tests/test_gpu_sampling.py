@@ -470,3 +470,30 @@ def test_window_rows_with_many_entries_per_slice(sampler):
     window_rows = [0, 1, 2, 3, 4, 5, 6, 9, 10, 11]
     assert np.isin(paths[window_rows], [2, 3]).all(), paths.tolist()
     assert (paths[[7, 8]] == 4).all(), paths.tolist()
+
+
+def test_top_n_with_clustered_maxima(sampler):
+    """Top-n logprobs where many logits near the top share the upper 16 bits
+    of their sort keys (the slice's candidate bound is cut to 16 bits): 40
+    and 100 such values in one slice, 200 in one slice (past the slice's
+    candidate capacity: exact path), spread over slices, and top-20."""
+    base = W.make("c2", rows=8, set_index=31)
+    V = base.vocab
+    rng = np.random.default_rng(2031)
+    logits = (rng.standard_normal((base.rows, V)) * 3.0).astype(np.float32)
+    f32 = lambda x: np.asarray(x, dtype=np.float32)
+    spots = [(0, 40), (3, 100), (5, 200), (None, 60), (15, 40), (0, 7), (8, 128), (None, 300)]
+    for r, (s, n) in enumerate(spots):
+        # distinct floats in [20, 20.07): one 16-bit key prefix spans 2^16 ulps
+        vals = f32(20.0) + f32(np.arange(n) * 2 ** -16 * 3 + rng.integers(0, 2, n) * 2 ** -20)
+        if s is None:
+            idx = rng.choice(V, size=n, replace=False)
+        else:
+            lo, hi = s * 8192, min(V, (s + 1) * 8192)
+            idx = rng.choice(np.arange(lo, hi), size=n, replace=False)
+        logits[r, idx] = vals
+    for n_top in (5, 20):
+        w = W.Workload(f"clustered-top{n_top}", base.rows, V, "f32", logits, base.params, base.seeds, base.u,
+                       base.hist_off, base.hist_ids, None, n_top, True)
+        g = run(sampler, w)
+        compare(w, g, O.sample_batch(w, threads=8), w.name, expect_paths={2, 3, 4})
