@@ -912,6 +912,14 @@ __device__ __forceinline__ void stash_args(SampleArgs* dst) {
 #pragma unroll
     for (uint32_t i = 0; i < sizeof(SampleArgs) / 4; ++i) d[i] = src[i];
 }
+// As above, from the kernel's SampleArgs parameter wherever it lies in the
+// kernel arguments.
+__device__ __forceinline__ void stash_args(SampleArgs* dst, const SampleArgs& src) {
+    const uint32_t* s = reinterpret_cast<const uint32_t*>(&src);
+    uint32_t* d = reinterpret_cast<uint32_t*>(dst);
+#pragma unroll
+    for (uint32_t i = 0; i < sizeof(SampleArgs) / 4; ++i) d[i] = s[i];
+}
 // The kernel arguments thread 0 staged in LDS, read back as wave-uniform values.
 __device__ __forceinline__ SampleArgs uniform_args(const SampleArgs& s) {
     constexpr uint32_t N = sizeof(SampleArgs) / 4;

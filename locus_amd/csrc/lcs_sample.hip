@@ -785,32 +785,36 @@ __device__ __forceinline__ double ent_bound(double S, uint32_t n, float mk) {
 // registers. Penalised logits reach the slice through an LDS table of
 // override bits written once per distinct history id. Every slice publishes a
 // record; the row's last arrival finalizes it.
+// The leading scalar arguments repeat fields of `a`: the build preloads them
+// into SGPRs at wave launch, so the slice's logit loads issue with no scalar
+// round trip to the kernel arguments.
 template <int G>
 __global__ __launch_bounds__(kSliceThreads) __attribute__((amdgpu_waves_per_eu(4)))
-void slice_kernel(SampleArgs a) {
+void slice_kernel(const void* logits, uint64_t row_stride, uint32_t rows, uint32_t slices, uint32_t slice_len,
+                  uint32_t vocab, uint32_t flags, uint32_t all_sliced, SampleArgs a) {
     constexpr int NT = kSliceThreads;
     constexpr int NG = kSliceElems / G;   // 16-byte groups per thread
     constexpr int HC = 8;                 // history ids per thread per chunk
     SliceSmem& sm = g_slice;
     const uint32_t tid = tid_x();
     const int lane = lane_id(), wv = (int)(tid / kWave);
-    const uint32_t S = a.slices;
+    const uint32_t S = slices;
     // Workgroups are dealt to the 8 XCDs round-robin; when the grid divides
     // evenly, a row's slices are placed on one XCD so that its L2 serves the
     // row's history ids to all of them.
     uint32_t blk = wg_x();
-    const uint32_t nblk = a.rows * S;   // the launch's grid
+    const uint32_t nblk = rows * S;   // the launch's grid
     if ((nblk & 7u) == 0u) blk = (blk & 7u) * (nblk >> 3) + (blk >> 3);
     const uint32_t row = blk / S, slice = blk % S;
-    if (row >= a.rows) return;
-    if ((a.flags & LCS_WRITE_PENALIZED) != 0) return;
+    if (row >= rows) return;
+    if ((flags & LCS_WRITE_PENALIZED) != 0) return;
     PROF_MARK(0);
-    const uint32_t V = a.vocab;
+    const uint32_t V = vocab;
     constexpr uint32_t DT = G == 8 ? LCS_BF16 : LCS_F32;   // the launch picks G from the dtype
     constexpr uint32_t esz = G == 8 ? 2u : 4u;
-    const void* rowp = static_cast<const char*>(a.logits) + (uint64_t)row * a.row_stride * esz;
-    const uint32_t lo = slice * a.slice_len;
-    const uint32_t hi = min(V, lo + a.slice_len);
+    const void* rowp = static_cast<const char*>(logits) + (uint64_t)row * row_stride * esz;
+    const uint32_t lo = slice * slice_len;
+    const uint32_t hi = min(V, lo + slice_len);
     const uint32_t len = hi - lo;
     // the slice's logits, one 16-byte load per group (groups past the slice
     // load the slice's first group and are masked below); issued before
@@ -824,7 +828,7 @@ void slice_kernel(SampleArgs a) {
             raw[j] = load16(rowp, (e0 < hi ? e0 : lo) / G);
         }
     };
-    const bool early = a.all_sliced != 0u;
+    const bool early = all_sliced != 0u;
     if (early) load_logits();
     // the row's parameters and the small per-row words come through the
     // scalar cache, so that waiting for them never waits for logits
@@ -1277,7 +1281,7 @@ void slice_kernel(SampleArgs a) {
         const bool last = prev == S - 1;
         if (last) {
             st_dev(a.counters + row, 0u);
-            stash_args(&sm.l.args);   // for the finalize (fin_row)
+            stash_args(&sm.l.args, a);   // for the finalize (fin_row)
         }
         sm.l.last = last ? 1u : 0u;
         sm.l.fin_fb = 0u;
@@ -1301,9 +1305,11 @@ extern "C" int lcs_prof_read(uint64_t* out, uint32_t n) {
 hipError_t launch_slice(const SampleArgs& a, hipStream_t st) {
     const dim3 grid(a.rows * a.slices), block(kSliceThreads);
     if (a.dtype == LCS_BF16) {
-        hipLaunchKernelGGL(slice_kernel<8>, grid, block, 0, st, a);
+        hipLaunchKernelGGL(slice_kernel<8>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices,
+                           a.slice_len, a.vocab, a.flags, a.all_sliced, a);
     } else {
-        hipLaunchKernelGGL(slice_kernel<4>, grid, block, 0, st, a);
+        hipLaunchKernelGGL(slice_kernel<4>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices,
+                           a.slice_len, a.vocab, a.flags, a.all_sliced, a);
     }
     return hipGetLastError();
 }
