@@ -30,9 +30,11 @@ HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contra
              "-fno-honor-nans", "-mno-amdgpu-ieee",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I" + INCLUDE]
 HIP_SOURCES = ["lcs_api.hip", "lcs_sample.hip", "lcs_nucleus.hip", "lcs_verify.hip"]
-# slice_kernel's leading scalar arguments (8) arrive preloaded in SGPRs; the
-# code object keeps a prologue that loads them where the firmware does not
-HIP_EXTRA = {"lcs_sample.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"]}
+# the leading scalar arguments (8) of slice_kernel and the nucleus kernels
+# arrive preloaded in SGPRs; the code object keeps a prologue that loads them
+# where the firmware does not
+HIP_EXTRA = {"lcs_sample.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
+             "lcs_nucleus.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"]}
 SAMPLER_SO = os.path.join(HERE, "liblocus_sampler.so")
 HOST_SO = os.path.join(HERE, "liblocus_host.so")
 HOST_SOURCES = ["grammar.cpp", "speculative.cpp", "sampler_registry.cpp", "host_capi.cpp", "sampling.cpp",

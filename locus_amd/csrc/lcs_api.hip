@@ -246,6 +246,8 @@ int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
     // every row known to run sliced: the slice kernel may start its logit
     // loads before it has the row's parameters
     a.all_sliced = (b->params_host && !any_general && !any_nucleus) ? 1u : 0u;
+    // likewise for the nucleus kernels when every row takes that path
+    a.all_nucleus = (b->params_host && !any_general && !any_slice) ? 1u : 0u;
     a.nrow = c->nrow;
     a.nh_cnt = c->nh_cnt;
     a.nh_mass = c->nh_mass;

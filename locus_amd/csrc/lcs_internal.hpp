@@ -124,6 +124,7 @@ struct SampleArgs {
     uint32_t slices;         // workgroups per row on the sliced path
     uint32_t slice_len;      // elements per slice (multiple of 8)
     uint32_t all_sliced;     // 1: the host saw every row take a sliced mode
+    uint32_t all_nucleus;    // 1: the host saw every row take the nucleus mode
     uint32_t nuc_row0;       // first row of this nucleus launch
     // nucleus path workspace, for rows nuc_row0 .. nuc_row0 + kNucRows - 1
     NucRow* nrow;            // kNucRows

@@ -115,18 +115,20 @@ struct SliceIn {
     float v[kSliceElems];
 
     // logits first, then the history window ids and the mask words
+    // (pre: this slice's logits, already requested by load_raw, else null)
     __device__ __forceinline__ void start(const SampleArgs& a, uint32_t row, uint32_t slice,
-                                          const lcs_params& P, bool masked) {
+                                          const lcs_params& P, bool masked, const uint4* pre = nullptr) {
         const uint32_t tid = tid_x();
         V = a.vocab;
         rowp = static_cast<const char*>(a.logits) + (uint64_t)row * a.row_stride * (G == 8 ? 2u : 4u);
         lo = slice * a.slice_len;
         hi = min(V, lo + a.slice_len);
         len = hi - lo;
+        if (pre) {
 #pragma unroll
-        for (int j = 0; j < NG; ++j) {
-            const uint32_t e0 = lo + (j * NT + tid) * G;
-            raw[j] = load16(rowp, (e0 < hi ? e0 : lo) / G);
+            for (int j = 0; j < NG; ++j) raw[j] = pre[j];
+        } else {
+            load_raw(raw, rowp, lo, hi);
         }
         mrow = masked ? a.mask + (uint64_t)row * a.mask_words : nullptr;
         const bool pen = penalties_active(P) && a.hist_off != nullptr;
@@ -157,6 +159,15 @@ struct SliceIn {
             }
         }
         mbits = 0xffffffffu;
+    }
+    // one 16-byte load per group of the slice [l0, h0) (groups past it load
+    // the slice's first group and are masked later)
+    static __device__ __forceinline__ void load_raw(uint4 (&dst)[NG], const void* rp, uint32_t l0, uint32_t h0) {
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            const uint32_t e0 = l0 + (j * NT + tid_x()) * G;
+            dst[j] = load16(rp, (e0 < h0 ? e0 : l0) / G);
+        }
     }
     // the thread's 32 mask bits (bit q for element q), where the row is masked
     __device__ __forceinline__ void load_mask() {
@@ -321,6 +332,24 @@ __device__ __forceinline__ bool nuc_row(const SampleArgs& a, uint32_t& row, uint
     return row_mode(P, masked, a.vocab) == kModeNucleus;
 }
 
+// Kernel arguments the nucleus kernels take ahead of SampleArgs: the build
+// preloads them into SGPRs at wave launch, so that when the host saw every
+// row take the nucleus mode, a workgroup's logit loads issue before it has
+// read anything (its row's parameters included).
+#define NUC_LEAD                                                                                   \
+    const void *logits, uint64_t row_stride, uint32_t rows, uint32_t slices, uint32_t slice_len, \
+        uint32_t vocab, uint32_t nuc_row0, uint32_t all_nucleus
+template <int G>
+__device__ __forceinline__ bool nuc_early(NUC_LEAD, uint4 (&pre)[SliceIn<G>::NG]) {
+    if (all_nucleus == 0u) return false;
+    const uint32_t row = nuc_row0 + wg_x() / slices;
+    if (row >= rows || wg_x() / slices >= kNucRows) return false;
+    const void* rp = static_cast<const char*>(logits) + (uint64_t)row * row_stride * (G == 8 ? 2u : 4u);
+    const uint32_t l0 = (wg_x() % slices) * slice_len;
+    SliceIn<G>::load_raw(pre, rp, l0, min(vocab, l0 + slice_len));
+    return true;
+}
+
 // ========================================================== A: nuc_stats ==
 // Record words (u64) of pass A, per slice:
 namespace nrec {
@@ -333,19 +362,24 @@ constexpr uint32_t kTop = kHdr;               // kTopMax rank keys, ascending
 }  // namespace nrec
 
 template <int G>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nuc_stats(SampleArgs a) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nuc_stats(NUC_LEAD, SampleArgs a) {
     NucSmem& sm = g_nuc;
+    uint4 pre[SliceIn<G>::NG];
+    const bool early = nuc_early<G>(logits, row_stride, rows, slices, slice_len, vocab, nuc_row0, all_nucleus, pre);
     uint32_t row, slice;
     lcs_params P;
     bool masked;
-    if (!nuc_row(a, row, slice, P, masked)) return;
+    if (!nuc_row(a, row, slice, P, masked)) {
+        wait_all_memory();   // (loads issued only when the host's parameter copy disagreed)
+        return;
+    }
     const uint32_t tid = tid_x(), S = a.slices;
     const int lane = lane_id(), wv = (int)(tid / kWave);
     const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
     const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
     const float NEG = -__builtin_huge_valf();
     SliceIn<G> in;
-    in.start(a, row, slice, P, masked);
+    in.start(a, row, slice, P, masked, early ? pre : nullptr);
     in.load_mask();   // (its loads arrive with the logits')
     if (tid == 0) sm.l.ncand = 0;
     if (in.hany) {
@@ -567,12 +601,17 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
 
 // =========================================================== B: nuc_hist ==
 template <int G>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nuc_hist(SampleArgs a) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nuc_hist(NUC_LEAD, SampleArgs a) {
     NucSmem& sm = g_nuc;
+    uint4 pre[SliceIn<G>::NG];
+    const bool early = nuc_early<G>(logits, row_stride, rows, slices, slice_len, vocab, nuc_row0, all_nucleus, pre);
     uint32_t row, slice;
     lcs_params P;
     bool masked;
-    if (!nuc_row(a, row, slice, P, masked)) return;
+    if (!nuc_row(a, row, slice, P, masked)) {
+        wait_all_memory();   // (loads issued only when the host's parameter copy disagreed)
+        return;
+    }
     const uint32_t tid = tid_x(), S = a.slices;
     const uint32_t wrow = row - a.nuc_row0;
     NucRow* nr = a.nrow + wrow;
@@ -581,7 +620,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     const float sx = scalar_load(&nr->sx);
     const bool use_mask = scalar_load(&nr->use_mask) != 0u;
     SliceIn<G> in;
-    in.start(a, row, slice, P, masked);
+    in.start(a, row, slice, P, masked, early ? pre : nullptr);
     if (use_mask) in.load_mask();   // (its loads arrive with the logits')
     in.penalise(sm, P);   // (ends on a barrier when it used the LDS)
     for (uint32_t b = tid; b < kNucBins; b += NT) { sm.u.h.cnt[b] = 0u; sm.u.h.mass[b] = 0.0; }
@@ -1168,26 +1207,34 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
 
 
 template <int G>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nuc_select(SampleArgs a) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nuc_select(NUC_LEAD, SampleArgs a) {
     NucSmem& sm = g_nuc;
+    uint4 pre[SliceIn<G>::NG];
+    const bool early = nuc_early<G>(logits, row_stride, rows, slices, slice_len, vocab, nuc_row0, all_nucleus, pre);
     uint32_t row, slice;
     lcs_params P;
     bool masked;
-    if (!nuc_row(a, row, slice, P, masked)) return;
+    if (!nuc_row(a, row, slice, P, masked)) {
+        wait_all_memory();   // (loads issued only when the host's parameter copy disagreed)
+        return;
+    }
     const uint32_t tid = tid_x(), S = a.slices;
     const int lane = lane_id(), wv = (int)(tid / kWave);
     const uint32_t wrow = row - a.nuc_row0;
     NucRow* nr = a.nrow + wrow;
     const uint32_t flags = scalar_load(&nr->flags);
     const bool exact = (flags & kNucFallback) != 0u;
-    if (exact && slice != 0) return;   // slice 0 resolves the row by the exact path
+    if (exact && slice != 0) {   // slice 0 resolves the row by the exact path
+        wait_all_memory();
+        return;
+    }
     bool run_fin = exact;
     if (!exact) {
     const float maxl = scalar_load(&nr->maxl);
     const float sx = scalar_load(&nr->sx);
     const bool use_mask = scalar_load(&nr->use_mask) != 0u;
     SliceIn<G> in;
-    in.start(a, row, slice, P, masked);
+    in.start(a, row, slice, P, masked, early ? pre : nullptr);
     if (use_mask) in.load_mask();   // (its loads arrive with the logits')
     in.penalise(sm, P);
     // the planned bins as a bitmap in LDS
@@ -1266,7 +1313,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     run_fin = nuc_arrive(a.counters + row, S, sm);
     }
     if (!run_fin) return;
-    if (tid == 0) stash_args(&sm.l.args);
+    if (tid == 0) stash_args(&sm.l.args, a);
     __syncthreads();
     nuc_select_fin<G>(row, exact);
 }
@@ -1279,13 +1326,19 @@ hipError_t launch_nucleus(const SampleArgs& a0, hipStream_t st) {
         const uint32_t nrows = min(kNucRows, a0.rows - r0);
         const dim3 grid(nrows * a.slices), block(NT);
         if (a.dtype == LCS_BF16) {
-            hipLaunchKernelGGL(nuc_stats<8>, grid, block, 0, st, a);
-            hipLaunchKernelGGL(nuc_hist<8>, grid, block, 0, st, a);
-            hipLaunchKernelGGL(nuc_select<8>, grid, block, 0, st, a);
+            hipLaunchKernelGGL(nuc_stats<8>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
+                               a.vocab, a.nuc_row0, a.all_nucleus, a);
+            hipLaunchKernelGGL(nuc_hist<8>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
+                               a.vocab, a.nuc_row0, a.all_nucleus, a);
+            hipLaunchKernelGGL(nuc_select<8>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
+                               a.vocab, a.nuc_row0, a.all_nucleus, a);
         } else {
-            hipLaunchKernelGGL(nuc_stats<4>, grid, block, 0, st, a);
-            hipLaunchKernelGGL(nuc_hist<4>, grid, block, 0, st, a);
-            hipLaunchKernelGGL(nuc_select<4>, grid, block, 0, st, a);
+            hipLaunchKernelGGL(nuc_stats<4>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
+                               a.vocab, a.nuc_row0, a.all_nucleus, a);
+            hipLaunchKernelGGL(nuc_hist<4>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
+                               a.vocab, a.nuc_row0, a.all_nucleus, a);
+            hipLaunchKernelGGL(nuc_select<4>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
+                               a.vocab, a.nuc_row0, a.all_nucleus, a);
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
