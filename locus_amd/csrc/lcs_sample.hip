@@ -1156,13 +1156,15 @@ void slice_kernel(const void* logits, uint64_t row_stride, uint32_t rows, uint32
         if (lane == 0) sm.l.bulk[wv] = bsum;
     } else if (topk) {
         // the slice's top-k by penalised value (sampling.cpp:87-97): elements
-        // >= the k-th largest penalised lane maximum of the slice
+        // >= t (the publish ranks them and keeps the first k)
         sm.l.lmax[tid] = lpm;
         __syncthreads();
+        // a lower bound of the slice's k-th largest penalised value: the k-th
+        // largest penalised lane max, its sort key cut to 16 bits
         uint32_t k4[kSliceWaves];
 #pragma unroll
-        for (int c = 0; c < kSliceWaves; ++c) k4[c] = fkey(sm.l.lmax[lane + c * kWave]);
-        const float t = key_to_f(wave_kth_largest4(k4, P.top_k));
+        for (int c = 0; c < kSliceWaves; ++c) k4[c] = fkey(sm.l.lmax[lane + c * kWave]) >> 16;
+        const float t = key_to_f(max(wave_kth_largest4_16(k4, P.top_k) << 16, 0x007fffffu));
         if (ballot(lpm >= t)) {
 #pragma unroll
             for (int j = 0; j < NG; ++j) {
