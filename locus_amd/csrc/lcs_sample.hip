@@ -953,14 +953,20 @@ void slice_kernel(const void* logits, uint64_t row_stride, uint32_t rows, uint32
         float m4[kSliceWaves];
 #pragma unroll
         for (int c = 0; c < kSliceWaves; ++c) m4[c] = sm.l.lmax[lane + c * kWave];
-        Ms = wave_max(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])));
+        const float m1 = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+        Ms = wave_max(m1);
         if (ntop && wv == kSliceWaves - 1) {
             __builtin_amdgcn_s_setprio(2);   // a serial chain among busy waves
-            uint32_t k4[kSliceWaves];
-#pragma unroll
-            for (int c = 0; c < kSliceWaves; ++c) k4[c] = fkey(m4[c]) >> 16;
+            // (over the lane's largest of its four lane maxima: the ntop-th
+            // largest of those 64 bounds the ntop-th largest of all 256)
+            const uint32_t k1 = fkey(m1) >> 16;
+            uint32_t T = 0;
+            for (int bit = 15; bit >= 0; --bit) {
+                const uint32_t Tb = T | (1u << bit);
+                if ((uint32_t)__builtin_popcountll(ballot(k1 >= Tb)) >= ntop) T = Tb;
+            }
             const uint32_t kneg = 0x007fffffu;   // fkey(-inf)
-            const float t = key_to_f(max(wave_kth_largest4_16(k4, ntop) << 16, kneg));
+            const float t = key_to_f(max(T << 16, kneg));
             if (lane == 0) sm.l.t_s = t;
             __builtin_amdgcn_s_setprio(0);
         }
