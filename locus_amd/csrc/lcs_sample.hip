@@ -959,11 +959,16 @@ void slice_kernel(const void* logits, uint64_t row_stride, uint32_t rows, uint32
             __builtin_amdgcn_s_setprio(2);   // a serial chain among busy waves
             // (over the lane's largest of its four lane maxima: the ntop-th
             // largest of those 64 bounds the ntop-th largest of all 256)
+            // two bits per step: the counts at the three larger digits
             const uint32_t k1 = fkey(m1) >> 16;
             uint32_t T = 0;
-            for (int bit = 15; bit >= 0; --bit) {
-                const uint32_t Tb = T | (1u << bit);
-                if ((uint32_t)__builtin_popcountll(ballot(k1 >= Tb)) >= ntop) T = Tb;
+#pragma unroll
+            for (int sh = 14; sh >= 0; sh -= 2) {
+                const uint32_t T1 = T | (1u << sh), T2 = T | (2u << sh), T3 = T | (3u << sh);
+                const uint32_t c1 = (uint32_t)__builtin_popcountll(ballot(k1 >= T1));
+                const uint32_t c2 = (uint32_t)__builtin_popcountll(ballot(k1 >= T2));
+                const uint32_t c3 = (uint32_t)__builtin_popcountll(ballot(k1 >= T3));
+                T = c3 >= ntop ? T3 : c2 >= ntop ? T2 : c1 >= ntop ? T1 : T;
             }
             const uint32_t kneg = 0x007fffffu;   // fkey(-inf)
             const float t = key_to_f(max(T << 16, kneg));
