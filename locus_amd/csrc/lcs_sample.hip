@@ -376,23 +376,35 @@ __device__ __forceinline__ bool fin_window(const SampleArgs& a, const uint64_t* 
 // row needs the exact path, 2 when a slice holds more qualifying entries than
 // were fetched (fin_window then fetches the row again).
 constexpr uint32_t kSpecWinT = 16;
-__device__ __forceinline__ uint32_t fin_window_fast(const SampleArgs& a, const uint64_t* recs, SliceSmem& sm,
+constexpr int kWinGroups = (int)(kMaxSlicesFast / 4);
+// The one-pass fetch, issued as the finalize begins.
+struct WinFetch {
+    uint64_t h0[kWinGroups], h2[kWinGroups], wk[kWinGroups], wr[kWinGroups];
+};
+__device__ __forceinline__ void fin_window_fetch(const uint64_t* recs, uint32_t S, WinFetch& f) {
+    const int lane = lane_id();
+    const uint32_t j = (uint32_t)lane & 15u;
+#pragma unroll
+    for (int g = 0; g < kWinGroups; ++g) {
+        const uint32_t sl = (uint32_t)g * 4u + (uint32_t)lane / 16u;
+        const uint64_t* r = recs + (sl < S ? sl : 0u) * rec::kWords64;
+        f.h0[g] = ld_dev_u64(r + 0);
+        f.h2[g] = ld_dev_u64(r + 2);
+        f.wk[g] = ld_dev_u64(r + rec::kWin + j);
+        f.wr[g] = ld_dev_u64(r + rec::kWinRaw + j);
+    }
+}
+__device__ __forceinline__ uint32_t fin_window_fast(const SampleArgs& a, const WinFetch& f, SliceSmem& sm,
                                                     float inv_t) {
-    constexpr int NGR = (int)(kMaxSlicesFast / 4);
+    constexpr int NGR = kWinGroups;
     const int lane = lane_id();
     const uint32_t S = a.slices;
     const uint32_t j = (uint32_t)lane & 15u;
     const float NEG = -__builtin_huge_valf();
-    uint64_t h0[NGR], h2[NGR], wk[NGR], wr[NGR];
-#pragma unroll
-    for (int g = 0; g < NGR; ++g) {
-        const uint32_t sl = (uint32_t)g * 4u + (uint32_t)lane / 16u;
-        const uint64_t* r = recs + (sl < S ? sl : 0u) * rec::kWords64;
-        h0[g] = ld_dev_u64(r + 0);
-        h2[g] = ld_dev_u64(r + 2);
-        wk[g] = ld_dev_u64(r + rec::kWin + j);
-        wr[g] = ld_dev_u64(r + rec::kWinRaw + j);
-    }
+    const uint64_t(&h0)[NGR] = f.h0;
+    const uint64_t(&h2)[NGR] = f.h2;
+    const uint64_t(&wk)[NGR] = f.wk;
+    const uint64_t(&wr)[NGR] = f.wr;
     PROF_WMARK(7);
     float mp = NEG;
 #pragma unroll
@@ -706,11 +718,15 @@ __device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, Sl
 // needs the exact single-workgroup path.
 template <int G>
 __device__ __forceinline__ bool fin_row(uint32_t row, uint32_t mode, const lcs_params& P, bool masked,
-                                        const uint64_t* recs) {
+                                        const uint64_t* recs, uint32_t S) {
     SliceSmem& sm = g_slice;
-    const SampleArgs a = uniform_args(sm.l.args);
     const uint32_t tid = tid_x();
     const int lane = lane_id(), wv = (int)(tid / kWave);
+    // sampled rows: wave 0's window fetch goes out before anything else
+    const bool fast = mode == kModeWindow && wv == 0 && S <= kMaxSlicesFast;
+    WinFetch wf;
+    if (fast) fin_window_fetch(recs, S, wf);
+    const SampleArgs a = uniform_args(sm.l.args);
     const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
     const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
     const bool stoch = mode == kModeWindow, topk = mode == kModeTopK;
@@ -734,7 +750,7 @@ __device__ __forceinline__ bool fin_row(uint32_t row, uint32_t mode, const lcs_p
         fin_merge_topk(a.slices, P.top_k, sm, inv_t);
     } else if (wv == 0) {
         if (stoch) {
-            const uint32_t r = a.slices <= kMaxSlicesFast ? fin_window_fast(a, recs, sm, inv_t) : 2u;
+            const uint32_t r = fast ? fin_window_fast(a, wf, sm, inv_t) : 2u;
             fb = r == 1u || (r == 2u && fin_window(a, recs, P, sm, inv_t));
         }
         else fin_greedy(a, recs, row, masked, sm);
@@ -1303,7 +1319,7 @@ void slice_kernel(const void* logits, uint64_t row_stride, uint32_t rows, uint32
     PROF_MARK(5);
     if (!sm.l.last) return;
     // =============== last-arriving workgroup finishes the row ===============
-    const bool fb = fin_row<G>(row, mode, P, masked, reinterpret_cast<const uint64_t*>(a.recs) + (uint64_t)row * S * rec::kWords64);
+    const bool fb = fin_row<G>(row, mode, P, masked, reinterpret_cast<const uint64_t*>(a.recs) + (uint64_t)row * S * rec::kWords64, S);
     PROF_MARK(6);
     if (fb) exact_row<kSliceThreads, kFbBins, kFbCap, kFbHistCap, G>(sm.l.args, row, sm.u.ex);
 }
