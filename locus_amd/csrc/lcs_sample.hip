@@ -762,14 +762,9 @@ __device__ __forceinline__ bool fin_row(uint32_t row, uint32_t mode, const lcs_p
     if (fb && lane == 0) sm.l.fin_fb = 1u;
     __syncthreads();
     if (sm.l.fin_fb) return true;
-    if (wv == 0 && (stoch || topk)) {
-        fb = fin_decide(a, row, sm, topk ? LCS_PATH_TOPK : LCS_PATH_WINDOW, P, u);
-        if (fb && lane == 0) sm.l.fin_fb = 1u;
-    }
-    __syncthreads();
-    if (sm.l.fin_fb) return true;
-    if (tid == 0 && want_lp) {
-        // logprob of the chosen token, or of the caller's lp_ids token
+    // logprob of the chosen token, or of the caller's lp_ids token (thread 0,
+    // once the row's choice and log-normaliser are in)
+    auto write_lp = [&]() {
         constexpr uint32_t DT = G == 8 ? LCS_BF16 : LCS_F32;
         const void* rowp = static_cast<const char*>(a.logits) + (uint64_t)row * a.row_stride * (G == 8 ? 2u : 4u);
         float raw = sm.l.chosen_raw;
@@ -780,8 +775,18 @@ __device__ __forceinline__ bool fin_row(uint32_t row, uint32_t mode, const lcs_p
             raw = inr ? load_elem(rowp, DT, (uint32_t)lid) : 0.0f;
         }
         a.chosen_lp[row] = inr ? (float)((double)raw - sm.l.log_z) : 0.0f;
+    };
+    if (!(stoch || topk)) {
+        if (tid == 0 && want_lp) write_lp();
+        return false;
     }
-    return false;
+    if (wv == 0) {
+        fb = fin_decide(a, row, sm, topk ? LCS_PATH_TOPK : LCS_PATH_WINDOW, P, u);
+        if (fb && lane == 0) sm.l.fin_fb = 1u;
+        if (!fb && tid == 0 && want_lp) write_lp();
+    }
+    __syncthreads();
+    return sm.l.fin_fb != 0u;
 }
 
 // A bound of sum c|t| over a slice's n bulk terms c = 2^t, from their sum S
