@@ -81,18 +81,6 @@ __device__ __forceinline__ float penalize_fast(float l, uint32_t count, const lc
     const float sub = fadd(fmul(p.frequency_penalty, static_cast<float>(count)), p.presence_penalty);
     return fsub(l, sub);
 }
-// penalize_fast() without branches, for callers that handle a tiny positive
-// quotient (where the f64 product may round differently from the divide)
-// themselves: returns false for such an l. rp1: repeat_penalty == 1.
-__device__ __forceinline__ float penalize_nb(float l, uint32_t count, const lcs_params& p, double inv_rp, bool rp1,
-                                             bool& ok) {
-    const double y = (double)l * inv_rp;
-    const float q = l > 0.0f ? (float)y : fmul(l, p.repeat_penalty);
-    ok = rp1 || !(l > 0.0f) || y >= 0x1p-125;
-    const float m = rp1 ? l : q;
-    const float sub = fadd(fmul(p.frequency_penalty, static_cast<float>(count)), p.presence_penalty);
-    return fsub(m, sub);
-}
 __device__ __forceinline__ bool penalties_active(const lcs_params& p) {
     return !(p.repeat_penalty == 1.0f && p.frequency_penalty == 0.0f &&
              p.presence_penalty == 0.0f);
@@ -319,15 +307,6 @@ __device__ __forceinline__ uint32_t wave_kth_largest4_16(const uint32_t (&k)[4],
     }
     return T;
 }
-// The n-th largest of the wave's 64 keys (1 <= n <= 64), as above.
-__device__ __forceinline__ uint32_t wave_kth_largest1(uint32_t k, uint32_t n) {
-    uint32_t T = 0;
-    for (int b = 31; b >= 0; --b) {
-        const uint32_t Tb = T | (1u << b);
-        if ((uint32_t)__builtin_popcountll(__ballot(k >= Tb)) >= n) T = Tb;
-    }
-    return T;
-}
 __device__ __forceinline__ int lane_id() { return (int)(tid_x() & 63u); }
 // Orders LDS traffic between lanes of one wave (no cross-wave barrier).
 __device__ __forceinline__ void wave_sync() {
@@ -528,16 +507,6 @@ __device__ __forceinline__ uint32_t scalar_load_u8(const uint8_t* p) {
 }
 
 // ------------------------------------------------------- vector loads ----
-// Raw buffer loads: a scalar resource over [base, base + bytes) and one
-// 32-bit lane offset; a load that does not fit in the range reads as 0
-// instead of faulting.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    const auto x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
-    return make_uint4(x[0], x[1], x[2], x[3]);
-}
 // 16-byte group loads: 4 f32 or 8 bf16 elements.
 __device__ __forceinline__ uint4 load16(const void* base, uint64_t group) {
     return reinterpret_cast<const uint4*>(base)[group];
