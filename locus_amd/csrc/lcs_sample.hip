@@ -66,6 +66,7 @@ __device__ uint64_t g_prof[16384 * 32];
 #endif
 
 constexpr int kSliceWaves = kSliceThreads / kWave;
+static_assert(kSliceWaves == 4, "the publish sums four waves' partials");
 constexpr uint32_t kCandCap = 128;   // top-n candidates one slice can hold
 constexpr uint32_t kWinLds = 256;    // window entries one slice can rank
 constexpr uint32_t kRowWin = 4 * kWave;  // row-window entries the finalize can rank
@@ -797,8 +798,14 @@ __device__ __forceinline__ bool fin_row(uint32_t row, uint32_t mode, const lcs_p
 __device__ __forceinline__ double ent_bound(double S, uint32_t n, float mk) {
     if (!(S > 0.0)) return 0.0;
     const double dn = (double)n;
-    const double h = S <= dn * 0.36787944117144233 ? S * log_f64(dn / S) * 1.4426950408889634
-                                                   : dn * 0.5307378454223266;   // n log2(e) / e
+    double h = dn * 0.5307378454223266;   // n log2(e) / e
+    if (S <= dn * 0.36787944117144233) {
+        // log2(n / S) >= log2(e) in f32: the hardware reciprocal and log2
+        // (each within an ulp or two) taken upward by a relative and an
+        // absolute 2^-19
+        const float lg = __builtin_amdgcn_logf((float)dn * __builtin_amdgcn_rcpf((float)S));
+        h = S * ((double)lg * (1.0 + 0x1p-19) + 0x1p-19);
+    }
     return h + S * (double)mk * 0x1.4p-24;
 }
 
@@ -1224,7 +1231,9 @@ void slice_kernel(const void* logits, uint64_t row_stride, uint32_t rows, uint32
         const bool lw = lane < kSliceWaves;
         const int wl = lw ? lane : 0;
         const float mrs = Ms;
-        const double ses = wave_sum(lw && want_lp ? sm.l.sraw[wl] : 0.0);
+        // the four waves' partials, summed in wave order by every lane
+        auto sum4 = [&](const double (&x)[kSliceWaves]) { return ((x[0] + x[1]) + x[2]) + x[3]; };
+        const double ses = want_lp ? sum4(sm.l.sraw) : 0.0;
         float ma = lw ? sm.l.mpen[wl] : NEG;
         uint32_t ia = lw ? sm.l.ipen[wl] : kNoIdx;
         float ra = lw ? sm.l.rpen[wl] : 0.0f;
@@ -1234,9 +1243,9 @@ void slice_kernel(const void* logits, uint64_t row_stride, uint32_t rows, uint32
         uint32_t na = 0;
         double bk = 0.0, be = 0.0;
         if (stoch) {
-            ma = wave_max(ma);
+            ma = fmaxf(fmaxf(sm.l.mpen[0], sm.l.mpen[1]), fmaxf(sm.l.mpen[2], sm.l.mpen[3]));
             ia = kNoIdx;
-            bk = wave_sum(lw ? sm.l.bulk[wl] : 0.0);
+            bk = sum4(sm.l.bulk);
             // f32 terms: exp2 and the per-lane and cross-lane f32 sums within
             // 2^-19 of the bulk; the offsets' roundings within 2^-22 c|t|
             be = ent_bound(bk * (1.0 + 0x1p-18), len, fabsf(ma) * fmul(fdiv(1.0f, P.temperature), kLog2E)) * 0x1p-22 +
