@@ -83,7 +83,8 @@ struct SliceLocal {
     uint32_t imsk[kSliceWaves];
     float rmsk[kSliceWaves];
     uint32_t nall[kSliceWaves];
-    double sraw[kSliceWaves];
+    double sraw[kSliceWaves];    // raw sums against each wave's max
+    float mraw[kSliceWaves];     // the waves' raw maxima
     double bulk[kSliceWaves];
     uint32_t ncand, nwin, last;
     // finalize hand-off between its waves
@@ -948,6 +949,32 @@ void slice_kernel(const void* logits, uint64_t row_stride, uint32_t rows, uint32
         lm = fmaxf(lm, gm[j]);
     }
     sm.l.lmax[tid] = lm;
+    // ---- raw sum of exp against the wave's max Mw (before the counts, which
+    // wait for the history ids; the publish rescales the four partials to the
+    // slice max): terms 2^fma(v, L, b) with b = RN(-Mw L) share the exponent
+    // error e_b = Mw L + b, taken out in f64 ----
+    {
+        const float Mw = wave_max(lm);
+        double sw = 0.0;
+        if (want_lp && Mw != NEG) {
+            const float b = -Mw * kLog2E;
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NG; ++j) {
+                float c[G];
+#pragma unroll
+                for (int k = 0; k < G; ++k) c[k] = fast_exp2(fmaf(v[j * G + k], kLog2E, b));
+#pragma unroll
+                for (int w = G / 2; w >= 1; w /= 2)
+#pragma unroll
+                    for (int k = 0; k < w; ++k) c[k] += c[k + w];
+                s += c[0];
+            }
+            const double eb = ((double)Mw * (double)kLog2E + (double)b) * 0.6931471805599453;
+            sw = (double)wave_sum_f(s) * (1.0 - eb + 0.5 * eb * eb);   // 2^-e_b, |e_b| tiny
+        }
+        if (lane == 0) { sm.l.sraw[wv] = sw; sm.l.mraw[wv] = Mw; }
+    }
     // counts, then the owners' raw logits (in flight while the raw statistics run)
     uint32_t oA = 0, oB = 0;
     float rA[HC], rB[HC];
@@ -1006,27 +1033,6 @@ void slice_kernel(const void* logits, uint64_t row_stride, uint32_t rows, uint32
     }
     PROF_MARK(1);
 
-    // ---- raw sum of exp against the slice max: terms 2^fma(v, L, b) with b =
-    // RN(-Ms L) share the exponent error e_b = Ms L + b, taken out in f64 ----
-    double sw = 0.0;
-    if (want_lp && Ms != NEG) {
-        const float b = -Ms * kLog2E;
-        float s = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NG; ++j) {
-            float c[G];
-#pragma unroll
-            for (int k = 0; k < G; ++k) c[k] = fast_exp2(fmaf(v[j * G + k], kLog2E, b));
-#pragma unroll
-            for (int w = G / 2; w >= 1; w /= 2)
-#pragma unroll
-                for (int k = 0; k < w; ++k) c[k] += c[k + w];
-            s += c[0];
-        }
-        const double eb = ((double)Ms * (double)kLog2E + (double)b) * 0.6931471805599453;
-        sw = (double)wave_sum_f(s) * (1.0 - eb + 0.5 * eb * eb);   // 2^-e_b, |e_b| tiny
-    }
-    if (lane == 0) sm.l.sraw[wv] = sw;
     PROF_MARK(2);
 
     // ---- penalties, part 2: each owner writes its id's word, penalised ^ raw
@@ -1233,7 +1239,12 @@ void slice_kernel(const void* logits, uint64_t row_stride, uint32_t rows, uint32
         const float mrs = Ms;
         // the four waves' partials, summed in wave order by every lane
         auto sum4 = [&](const double (&x)[kSliceWaves]) { return ((x[0] + x[1]) + x[2]) + x[3]; };
-        const double ses = want_lp ? sum4(sm.l.sraw) : 0.0;
+        // raw sum against the slice max: each wave's partial rescaled by
+        // exp(Mw - Ms) in f64 (lane w), summed in wave order
+        const float mw = lw ? sm.l.mraw[wl] : NEG;
+        const double tw = lw && want_lp && mw != NEG ? sm.l.sraw[wl] * exp_f64((double)mw - (double)Ms) : 0.0;
+        const double ses = ((bits_d(readlane_u64(d_bits(tw), 0)) + bits_d(readlane_u64(d_bits(tw), 1))) +
+                            bits_d(readlane_u64(d_bits(tw), 2))) + bits_d(readlane_u64(d_bits(tw), 3));
         float ma = lw ? sm.l.mpen[wl] : NEG;
         uint32_t ia = lw ? sm.l.ipen[wl] : kNoIdx;
         float ra = lw ? sm.l.rpen[wl] : 0.0f;
