@@ -71,7 +71,10 @@ typedef struct lcs_batch {
     const int32_t* hist_ids;   /* token history (the request's generated ids) */
     const double* u;           /* rows: uniform in [0,1) per stochastic row, the
                                   generate_canonical<double,53> draw of the row's
-                                  mt19937_64 (libstdc++ random.tcc:3348-3380) */
+                                  mt19937_64 (libstdc++ random.tcc:3348-3380).
+                                  May be NULL only when params_host is given and
+                                  no row has temperature > 0; otherwise a NULL u
+                                  returns LCS_ERR_INVALID_ARG before any launch */
     const uint32_t* mask;      /* rows x mask_words allow-bits (bit t&31 of word
                                   t>>5, LSB first), or NULL for no constraint */
     const uint8_t* has_mask;   /* rows, nonzero = row constrained; NULL = all rows

@@ -24,7 +24,6 @@ struct lcs_ctx {
     uint32_t max_slices = 0;
     uint32_t* recs = nullptr;
     uint32_t* counters = nullptr;
-    uint32_t* vcounters = nullptr;
     uint32_t* d_ids = nullptr;
     float* d_raw = nullptr;
     float* d_pen = nullptr;
@@ -121,7 +120,6 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t 
     hipError_t e = hipSuccess;
     if ((e = hipMalloc(&c->recs, rec_bytes)) != hipSuccess ||
         (e = hipMalloc(&c->counters, (size_t)max_rows * 4)) != hipSuccess ||
-        (e = hipMalloc(&c->vcounters, (size_t)max_rows * 4)) != hipSuccess ||
         (e = hipMalloc(&c->d_ids, d_elems * 4)) != hipSuccess ||
         (e = hipMalloc(&c->d_raw, d_elems * 4)) != hipSuccess ||
         (e = hipMalloc(&c->d_pen, d_elems * 4)) != hipSuccess ||
@@ -131,7 +129,6 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t 
         (e = hipMalloc(&c->nh_mass, nh_elems * 8)) != hipSuccess ||
         (e = hipMalloc(&c->nlist, nuc_rows * lcs::kNucList * 8)) != hipSuccess ||
         (e = hipMemset(c->counters, 0, (size_t)max_rows * 4)) != hipSuccess ||
-        (e = hipMemset(c->vcounters, 0, (size_t)max_rows * 4)) != hipSuccess ||
         (e = hipMemset(c->status, 0, 4)) != hipSuccess ||
         (e = hipDeviceSynchronize()) != hipSuccess) {
         g_create_error = std::string("lcs_create: ") + hipGetErrorString(e);
@@ -147,7 +144,6 @@ void lcs_destroy(lcs_ctx* c) {
     (void)hipDeviceSynchronize();
     (void)hipFree(c->recs);
     (void)hipFree(c->counters);
-    (void)hipFree(c->vcounters);
     (void)hipFree(c->d_ids);
     (void)hipFree(c->d_raw);
     (void)hipFree(c->nrow);
@@ -187,7 +183,11 @@ int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
     if ((b->flags & LCS_WRITE_PENALIZED) && b->dtype != LCS_F32) {
         return fail(c, LCS_ERR_INVALID_ARG, "LCS_WRITE_PENALIZED needs f32 logits");
     }
-    if (!b->u && b->params_host) {
+    // Stochastic rows read u[row] on the device. With a host copy of the
+    // params only those rows need it; without one the row modes are unknown
+    // here, so u is required outright (nothing is launched otherwise).
+    if (!b->u) {
+        if (!b->params_host) return fail(c, LCS_ERR_INVALID_ARG, "u is required when params_host is NULL");
         for (uint32_t r = 0; r < b->rows; ++r) {
             if (b->params_host[r].temperature > 0.0f) return fail(c, LCS_ERR_INVALID_ARG, "u missing for a stochastic row");
         }
@@ -287,7 +287,6 @@ int lcs_verify(lcs_ctx* c, const lcs_verify_batch* b, const lcs_verify_out* o, v
     a.argmax_ids = o->argmax_ids;
     a.draft_lp = o->draft_lp;
     a.accept_len = o->accept_len;
-    a.counters = c->vcounters;
     DeviceGuard g(c->device);
     const hipError_t e = lcs::launch_verify(a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(c, e, "verify kernel launch");

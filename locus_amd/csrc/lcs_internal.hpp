@@ -141,7 +141,6 @@ struct VerifyArgs {
     int32_t* argmax_ids;
     float* draft_lp;
     uint32_t* accept_len;
-    uint32_t* counters;      // n_seq
 };
 
 // status bits

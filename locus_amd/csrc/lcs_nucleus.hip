@@ -311,8 +311,7 @@ __device__ __forceinline__ bool nuc_arrive(uint32_t* counter, uint32_t S, NucSme
     wait_all_memory();
     __syncthreads();
     if (tid_x() == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = prev == S - 1;
+        const bool last = arrive_rmw(counter, S);
         if (last) st_dev(counter, 0u);
         sm.l.last = last ? 1u : 0u;
     }

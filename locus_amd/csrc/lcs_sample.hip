@@ -1330,9 +1330,7 @@ void slice_kernel(const void* logits, uint64_t row_stride, uint32_t rows, uint32
     PROF_WMARK(19);
     __syncthreads();
     if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(a.counters + row, 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = prev == S - 1;
+        const bool last = arrive_rmw(a.counters + row, S);
         if (last) {
             st_dev(a.counters + row, 0u);
             stash_args(&sm.l.args, a);   // for the finalize (fin_row)

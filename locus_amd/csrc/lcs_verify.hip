@@ -2,11 +2,15 @@
 //
 // Per row: greedy argmax with the first-index tie rule (llama.cpp:1237-1245)
 // and the natural-distribution log-probability of the row's draft token
-// (logprobs_from with chosen = draft, n_top = 0: sampling.cpp:241-261). Per
-// sequence: the acceptance length of engine.cpp:366-383 - the number of
-// leading rows whose argmax equals the draft they predict. One workgroup per
-// row streams the row once; the sequence's last-arriving row workgroup
-// computes the acceptance length from the rows' published argmaxes.
+// (logprobs_from with chosen = draft, n_top = 0: sampling.cpp:150-170). Per
+// sequence: the acceptance length of engine.cpp:357-383 - the number of
+// leading rows whose argmax equals the draft they predict.
+//
+// Two launches on the caller's stream: verify_kernel streams each row once
+// (one workgroup per row) and writes the row's argmax and draft logprob;
+// accept_kernel then reads each sequence's argmaxes and writes its acceptance
+// length. The kernel boundary orders the first launch's stores before the
+// second's loads, so no workgroup waits on or signals another.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -26,7 +30,6 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     __shared__ float redf[NT / kWave];
     __shared__ uint32_t redu[NT / kWave];
     __shared__ double redd[NT / kWave];
-    __shared__ uint32_t last;
     const uint32_t rows = a.n_seq * a.rows_per_seq;
     const uint32_t row = wg_x();
     if (row >= rows) return;
@@ -99,20 +102,19 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
         float lp = 0.0f;
         if (d >= 0 && (uint32_t)d < V) lp = (float)((double)load_elem(rowp, a.dtype, (uint32_t)d) - log_z);
         a.draft_lp[row] = lp;
-        st_dev(reinterpret_cast<uint32_t*>(a.argmax_ids + row), idx < V ? idx : 0u);
+        a.argmax_ids[row] = (int32_t)(idx < V ? idx : 0u);
     }
-    if (!arrive_last(a.counters + row / a.rows_per_seq, a.rows_per_seq, &last)) return;
-    if (tid_x() == 0) {
-        const uint32_t seq = row / a.rows_per_seq;
-        const uint32_t base = seq * a.rows_per_seq;
-        uint32_t acc = 0;
-        while (acc < a.rows_per_seq &&
-               (int32_t)ld_dev(reinterpret_cast<const uint32_t*>(a.argmax_ids + base + acc)) ==
-                   a.draft[base + acc]) {
-            ++acc;
-        }
-        a.accept_len[seq] = acc;
-    }
+}
+
+// Acceptance length per sequence (engine.cpp:366-383): leading rows whose
+// argmax equals their draft. One thread per sequence.
+__global__ __launch_bounds__(256) void accept_kernel(VerifyArgs a) {
+    const uint32_t seq = wg_x() * 256u + tid_x();
+    if (seq >= a.n_seq) return;
+    const uint32_t base = seq * a.rows_per_seq;
+    uint32_t acc = 0;
+    while (acc < a.rows_per_seq && a.argmax_ids[base + acc] == a.draft[base + acc]) ++acc;
+    a.accept_len[seq] = acc;
 }
 
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t st) {
@@ -122,6 +124,9 @@ hipError_t launch_verify(const VerifyArgs& a, hipStream_t st) {
     } else {
         hipLaunchKernelGGL(verify_kernel<4>, grid, block, 0, st, a);
     }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(accept_kernel, dim3((a.n_seq + 255u) / 256u), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

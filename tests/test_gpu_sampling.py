@@ -143,6 +143,30 @@ def test_deterministic_and_host_params_optional(sampler):
     assert np.array_equal(a["top_lp"], b["top_lp"])
 
 
+def test_missing_u_is_rejected_before_any_launch(sampler):
+    # without params_host the row modes are unknown on the host, so u is
+    # required; with params_host it is required only by stochastic rows
+    from locus_amd.sampler import LCS_ERR_INVALID_ARG, SamplerError
+    w = W.make("c2", rows=4, set_index=3)
+    d = sampler.upload(w)
+    d.pop("u")
+    out = sampler.alloc_out(w.rows, w.n_top, w.want_logprobs)
+    for host_params in (False, True):
+        with pytest.raises(SamplerError, match=f"lcs error {LCS_ERR_INVALID_ARG}"):
+            sampler.sample_dev(d, out, use_host_params=host_params)
+    sampler.torch.cuda.synchronize()
+    assert (out["ids"].cpu().numpy() == -7).all(), "a kernel ran"
+    # greedy rows need no u when the host sees their params
+    g = W.make("c1g")
+    assert (g.params["temperature"] <= 0).all()
+    dg = sampler.upload(g)
+    dg.pop("u", None)
+    og = sampler.alloc_out(g.rows, g.n_top, g.want_logprobs)
+    sampler.sample_dev(dg, og)
+    sampler.torch.cuda.synchronize()
+    assert og["ids"].cpu().numpy()[0] == O.sample_batch(g).ids[0]
+
+
 def test_mixed_modes_in_one_batch(sampler):
     # one batch mixing greedy, min-p window, top-k and top-p-only rows
     base = W.make("c2", rows=8, set_index=7)
