@@ -31,9 +31,16 @@ MALL_BYTES = 256 << 20
 
 # the kernels that do a workload's work (the roofline's subject): a name
 # pattern (SQL LIKE) matching them, and the stem of their profile summaries
-KERNEL = {"c1g": ("slice_kernel", "slice_kernel"), "c1s": ("slice_kernel", "slice_kernel"),
-          "c2": ("slice_kernel", "slice_kernel"), "c3": ("nuc_", "nucleus"),
-          "c4": ("nuc_", "nucleus"), "c5": ("verify_kernel", "verify_kernel")}
+# ("a|b" matches either)
+KERNEL = {"c1g": ("slice_stats|row_fin", "sliced"), "c1s": ("slice_stats|row_fin", "sliced"),
+          "c2": ("slice_stats|row_fin", "sliced"), "c3": ("nuc_", "nucleus"),
+          "c4": ("nuc_", "nucleus"), "c5": ("verify_kernel|accept_kernel", "verify")}
+
+
+def _like(column, kernel):
+    """SQL condition and parameters for a name pattern "a|b" (either)."""
+    parts = kernel.split("|")
+    return "(" + " or ".join(f"{column} like ?" for _ in parts) + ")", tuple(f"%{k}%" for k in parts)
 
 CONFIG_TEXT = {
     "c1g": "B=1 V=128256 f32 greedy",
@@ -190,8 +197,9 @@ def summarize_trace(path, kernel):
         out.append(f"{n:>7} {tot:>12.3f} {avg:>10.3f} {pct:>6.2f}  {name}")
     # one dispatch of each matching kernel per call: the call's kernel time is
     # the sum of their averages
+    cond, par = _like("name", kernel)
     ks = c.execute("select name, count(*), avg(duration), min(duration), max(duration) from kernels "
-                   "where name like ? group by name", (f"%{kernel}%",)).fetchall()
+                   f"where {cond} group by name", par).fetchall()
     for name, n, avg, mn, mx in ks:
         out.append(f"kernel_avg_us[{name}]: {avg / 1e3:.3f}  (n={n}, min {mn / 1e3:.3f}, max {mx / 1e3:.3f})")
     out.append(f"call_kernel_avg_us[{kernel}]: {sum(k[2] for k in ks) / 1e3:.3f}  ({len(ks)} kernel(s) per call)")
@@ -202,9 +210,10 @@ def _pmc_avg(path, kernel, counter):
     """Per-call reading of `counter`: the sum over the kernels matching
     `kernel` of each one's average per dispatch."""
     c, _ = _db(path)
+    cond, par = _like("kernel_name", kernel)
     rs = c.execute("select kernel_name, count(*), avg(value) from counters_collection "
-                   "where kernel_name like ? and counter_name = ? group by kernel_name",
-                   (f"%{kernel}%", counter)).fetchall()
+                   f"where {cond} and counter_name = ? group by kernel_name",
+                   par + (counter,)).fetchall()
     if not rs:
         raise SystemExit(f"{counter} for {kernel} not found in {path}")
     return min(r[1] for r in rs), float(sum(r[2] for r in rs))
@@ -214,9 +223,10 @@ def summarize_counters(path, kernel):
     """Per-kernel average per dispatch of every counter in a `rocprofv3 --pmc`
     database, for the kernels matching `kernel`."""
     c, f = _db(path)
+    cond, par = _like("kernel_name", kernel)
     rs = c.execute("select kernel_name, counter_name, count(*), avg(value) from counters_collection "
-                   "where kernel_name like ? group by kernel_name, counter_name "
-                   "order by kernel_name, counter_name", (f"%{kernel}%",)).fetchall()
+                   f"where {cond} group by kernel_name, counter_name "
+                   "order by kernel_name, counter_name", par).fetchall()
     out = [f"# source: {os.path.basename(f)} (counters_collection; average per dispatch)"]
     for kname, cname, n, avg in rs:
         out.append(f"{cname:<24} {avg:>16.1f}  (n={n})  {kname}")
@@ -273,7 +283,7 @@ def main():
                     help="print per-kernel averages of every counter of a rocprofv3 --pmc output")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "16")),
                     help="threads of the all-cores CPU baseline (0: skip it)")
-    ap.add_argument("--kernel", default="slice_kernel")
+    ap.add_argument("--kernel", default="slice_stats|row_fin")
     ap.add_argument("--copy-bytes", type=int, default=256 << 20)
     args = ap.parse_args()
     if args.summarize_trace:
@@ -296,8 +306,8 @@ def main():
     ceiling = copy_ceiling()
     rows = w.rows
     alg = w.algorithmic_bytes()
-    # the timed region's average call duration (one kernel per call, three
-    # for the nucleus path: their sum is the call)
+    # the timed region's average call duration (two kernels per call on the
+    # sliced and verify paths, three on the nucleus path: their sum is the call)
     achieved = alg / (ms_step * 1e-3) / 1e9
     kernel, stem = KERNEL[args.workload]
     traffic = committed_traffic(stem, args.workload)

@@ -29,11 +29,11 @@ HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
              "-fno-honor-nans", "-mno-amdgpu-ieee",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I" + INCLUDE]
-HIP_SOURCES = ["lcs_api.hip", "lcs_sample.hip", "lcs_nucleus.hip", "lcs_verify.hip"]
-# the leading scalar arguments (8) of slice_kernel and the nucleus kernels
+HIP_SOURCES = ["lcs_api.hip", "lcs_sample.hip", "lcs_slice.hip", "lcs_nucleus.hip", "lcs_verify.hip"]
+# the leading scalar arguments (8) of slice_stats and the nucleus kernels
 # arrive preloaded in SGPRs; the code object keeps a prologue that loads them
 # where the firmware does not
-HIP_EXTRA = {"lcs_sample.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
+HIP_EXTRA = {"lcs_slice.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
              "lcs_nucleus.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"]}
 SAMPLER_SO = os.path.join(HERE, "liblocus_sampler.so")
 HOST_SO = os.path.join(HERE, "liblocus_host.so")

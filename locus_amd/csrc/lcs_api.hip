@@ -23,6 +23,7 @@ struct lcs_ctx {
     uint32_t max_rows = 0, max_vocab = 0, max_hist = 0, max_top = 0;
     uint32_t max_slices = 0;
     uint32_t* recs = nullptr;
+    uint64_t* srecs = nullptr;
     uint32_t* counters = nullptr;
     uint32_t* d_ids = nullptr;
     float* d_raw = nullptr;
@@ -65,11 +66,13 @@ bool is_gfx950(int dev) {
     return std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
 }
 
-uint32_t slices_for(uint32_t vocab) {
-    return (vocab + lcs::kSliceMax - 1) / lcs::kSliceMax;
+// Slices of a row: the nucleus passes cut rows into <= kSliceMax logits, the
+// sliced path into <= kSsMax; lengths are balanced and a multiple of 8.
+uint32_t slices_for(uint32_t vocab, uint32_t max_len) {
+    return (vocab + max_len - 1) / max_len;
 }
-uint32_t slice_len_for(uint32_t vocab) {
-    const uint32_t s = slices_for(vocab);
+uint32_t slice_len_for(uint32_t vocab, uint32_t max_len) {
+    const uint32_t s = slices_for(vocab, max_len);
     const uint32_t per = (vocab + s - 1) / s;
     return (per + 7u) & ~7u;
 }
@@ -112,13 +115,15 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t 
     c->max_vocab = max_vocab;
     c->max_hist = max_hist > 0 ? max_hist : 1;
     c->max_top = max_top;
-    c->max_slices = slices_for(max_vocab);
+    c->max_slices = slices_for(max_vocab, lcs::kSliceMax);
     const size_t rec_bytes = (size_t)max_rows * c->max_slices * lcs::rec::kWords * 4;
+    const size_t srec_bytes = (size_t)max_rows * lcs::kSsMaxSlices * lcs::rec::kWords64 * 8;
     const size_t d_elems = (size_t)max_rows * c->max_hist;
     const size_t nuc_rows = max_rows < lcs::kNucRows ? max_rows : lcs::kNucRows;
     const size_t nh_elems = nuc_rows * lcs::kMaxSlices * lcs::kNucBins;
     hipError_t e = hipSuccess;
     if ((e = hipMalloc(&c->recs, rec_bytes)) != hipSuccess ||
+        (e = hipMalloc(&c->srecs, srec_bytes)) != hipSuccess ||
         (e = hipMalloc(&c->counters, (size_t)max_rows * 4)) != hipSuccess ||
         (e = hipMalloc(&c->d_ids, d_elems * 4)) != hipSuccess ||
         (e = hipMalloc(&c->d_raw, d_elems * 4)) != hipSuccess ||
@@ -143,6 +148,7 @@ void lcs_destroy(lcs_ctx* c) {
     DeviceGuard g(c->device);
     (void)hipDeviceSynchronize();
     (void)hipFree(c->recs);
+    (void)hipFree(c->srecs);
     (void)hipFree(c->counters);
     (void)hipFree(c->d_ids);
     (void)hipFree(c->d_raw);
@@ -241,8 +247,11 @@ int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
     a.d_pen = c->d_pen;
     a.max_hist = c->max_hist;
     a.status = c->status;
-    a.slices = slices_for(b->vocab);
-    a.slice_len = slice_len_for(b->vocab);
+    a.slices = slices_for(b->vocab, lcs::kSliceMax);
+    a.slice_len = slice_len_for(b->vocab, lcs::kSliceMax);
+    a.srecs = c->srecs;
+    a.ss_slices = slices_for(b->vocab, lcs::kSsMax);
+    a.ss_len = slice_len_for(b->vocab, lcs::kSsMax);
     // every row known to run sliced: the slice kernel may start its logit
     // loads before it has the row's parameters
     a.all_sliced = (b->params_host && !any_general && !any_nucleus) ? 1u : 0u;

@@ -932,10 +932,16 @@ __device__ __forceinline__ SampleArgs uniform_args(const SampleArgs& s) {
     __builtin_memcpy(&r, w, sizeof(r));
     return r;
 }
-__device__ __forceinline__ void stage_args(SampleArgs* dst) {
-    static_assert(sizeof(SampleArgs) % 4 == 0 && sizeof(SampleArgs) / 4 <= 64, "args size");
-    const uint32_t* src = (const uint32_t*)__builtin_amdgcn_kernarg_segment_ptr();
-    if (tid_x() < sizeof(SampleArgs) / 4) reinterpret_cast<uint32_t*>(dst)[tid_x()] = src[tid_x()];
+// Parallel copy of the kernel's SampleArgs parameter into LDS (two dwords per
+// lane of the first wave), then a barrier: `src` is the kernel parameter
+// itself, read where it lies in the kernel arguments.
+__device__ __forceinline__ void stage_args(SampleArgs* dst, const SampleArgs& src) {
+    constexpr uint32_t N = sizeof(SampleArgs) / 4;
+    static_assert(sizeof(SampleArgs) % 4 == 0 && N <= 2 * kWave, "args size");
+    const uint32_t* s = reinterpret_cast<const uint32_t*>(&src);
+    const uint32_t t = tid_x();
+    if (t < N) reinterpret_cast<uint32_t*>(dst)[t] = s[t];
+    if (t + kWave < N && t < kWave) reinterpret_cast<uint32_t*>(dst)[t + kWave] = s[t + kWave];
     __syncthreads();
 }
 

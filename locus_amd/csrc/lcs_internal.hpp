@@ -7,7 +7,7 @@
 
 namespace lcs {
 
-// ---- sliced (multi-workgroup) path ----
+// ---- nucleus slices (multi-workgroup passes) ----
 constexpr int kSliceThreads = 256;      // threads per slice workgroup
 constexpr int kSliceElems = 32;         // logits held in registers per thread
 constexpr uint32_t kSliceMax = kSliceThreads * kSliceElems;  // 8192 per slice
@@ -17,8 +17,19 @@ constexpr uint32_t kTopMax = 20;        // logprob alternatives per row
 constexpr uint32_t kWinCap = 64;        // min-p window entries per slice
 constexpr uint32_t kFastHistMax = 4096; // penalty window handled by the sliced path
 
-// Slice record (64-bit words), written with device-scope stores by each
-// slice workgroup and read by the row's last-arriving workgroup.
+// ---- sliced path (greedy, min-p window and top-k rows): slice_stats maps
+// each (row, slice of <= 8192 logits) to a record, row_fin reduces a row's
+// records (lcs_slice.hip) ----
+constexpr int kSsThreads = 256;         // threads per slice workgroup
+constexpr int kSsElems = 32;            // logits per thread (8 f32 / 4 bf16 16-byte groups)
+constexpr uint32_t kSsMax = kSsThreads * kSsElems;          // 8192 per slice
+constexpr uint32_t kSsMaxSlices = kMaxVocab / kSsMax;       // 32
+constexpr uint32_t kSsTopKMerge = 2048;  // slices x top_k entries row_fin merges
+constexpr int kFinThreads = 256;         // row_fin workgroup
+
+// Slice record (64-bit words): the nucleus passes write and read it within a
+// kernel (device-scope stores, agent-scope release / acquire arrival);
+// slice_stats writes it with plain stores for the next kernel, row_fin.
 namespace rec {
 constexpr uint32_t kHdr = 8;         // header words:
 // 0: f32 raw max | u16 window entries << 32 | u16 flags << 48
@@ -60,8 +71,8 @@ __host__ __device__ inline uint32_t row_mode(const lcs_params& p, bool masked, u
                        p.presence_penalty == 0.0f);
     const bool pen_ok = !pen || p.repeat_last_n <= kFastHistMax;
     const bool topk = p.top_k > 0 && p.top_k < vocab;
-    const uint32_t slices = (vocab + kSliceMax - 1) / kSliceMax;
-    if (topk && !masked && pen_ok && p.top_k <= kTopKMax && p.top_k * slices <= kTopKMerge) {
+    const uint32_t slices = (vocab + kSsMax - 1) / kSsMax;
+    if (topk && !masked && pen_ok && p.top_k <= kTopKMax && p.top_k * slices <= kSsTopKMerge) {
         return kModeTopK;
     }
     if (p.min_p > 0.0f && !masked && !topk && pen_ok) return kModeWindow;
@@ -97,7 +108,7 @@ struct NucRow {
     NucRange r[kNucRanges];
 };
 
-struct SampleArgs {
+struct SampleArgs {   // (at most 128 dwords: kernels stage it in LDS, two dwords per lane)
     const void* logits;
     uint64_t row_stride;
     uint32_t rows, vocab, dtype, flags, n_top, mask_words;
@@ -114,15 +125,18 @@ struct SampleArgs {
     float* top_lp;
     lcs_row_diag* diag;
     // workspace
-    uint32_t* recs;          // rows x slices x rec::kWords
+    uint32_t* recs;          // nucleus: rows x slices x rec::kWords
     uint32_t* counters;      // rows
+    uint64_t* srecs;         // sliced path: rows x kSsMaxSlices x rec::kWords64
+    uint32_t ss_slices;      // sliced path: slices per row (<= kSsMaxSlices)
+    uint32_t ss_len;         // sliced path: elements per slice (multiple of 8, <= kSsMax)
     uint32_t* d_ids;         // rows x max_hist (distinct penalised ids)
     float* d_raw;
     float* d_pen;
     uint32_t max_hist;
     uint32_t* status;        // device error word (sticky bits)
-    uint32_t slices;         // workgroups per row on the sliced path
-    uint32_t slice_len;      // elements per slice (multiple of 8)
+    uint32_t slices;         // nucleus: workgroups per row
+    uint32_t slice_len;      // nucleus: elements per slice (multiple of 8)
     uint32_t all_sliced;     // 1: the host saw every row take a sliced mode
     uint32_t all_nucleus;    // 1: the host saw every row take the nucleus mode
     uint32_t nuc_row0;       // first row of this nucleus launch

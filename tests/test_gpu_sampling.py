@@ -387,11 +387,12 @@ def _all_paths_workload(V, seed, dtype="f32"):
     return wb, w32, has
 
 
-@pytest.mark.parametrize("V,dtype", [(8192, "f32"), (8193, "f32"), (16385, "bf16"), (262144, "f32"),
-                                     (262144, "bf16")])
+@pytest.mark.parametrize("V,dtype", [(4096, "f32"), (4097, "bf16"), (8192, "f32"), (8193, "f32"),
+                                     (16385, "bf16"), (262144, "f32"), (262144, "bf16")])
 def test_every_path_at_slice_boundaries_and_max_vocab(sampler, V, dtype):
-    """Every row path at vocabularies that end a slice exactly, leave a
-    one-logit last slice, and fill all 32 slices (the maximum vocabulary)."""
+    """Every row path at vocabularies that end a slice exactly (8192-logit
+    slices of the sliced path and of the nucleus passes), one past it, half a
+    slice, and the maximum vocabulary (32 slices)."""
     wg, w32, has = _all_paths_workload(V, 20261300 + V, dtype)
     say("paths", V, dtype)
     g = run(sampler, wg, has_mask=sampler.torch.from_numpy(has).cuda())
@@ -462,24 +463,33 @@ def test_random_batches(sampler):
     assert {1, 2, 4, 5, 6} <= seen, seen
 
 
+def slice_geometry(V):
+    """The sliced path's cut of a row: S slices of L logits (the last one
+    shorter), L a multiple of 8 and at most 8192 (lcs_api.hip)."""
+    S = -(-V // 8192)
+    L = (-(-V // S) + 7) // 8 * 8
+    return S, L
+
+
 def test_window_rows_with_many_entries_per_slice(sampler):
-    """Min-p window rows whose row window is planted in chosen slices: up to
-    16 qualifying entries per slice (the finalize's one-pass fetch), 17 to 64
-    in a slice (the per-slice fetch, header with 4 entries then more), a
-    slice past its 64-entry record (exact path) and a row window past 256
-    entries (exact path), including the short last slice."""
+    """Min-p window rows whose row window is planted in chosen slices: up to 4
+    qualifying entries per slice (row_fin's first fetch round), more (further
+    rounds, up to a slice's 64-entry record), a slice past its record (exact
+    path) and a row window past 256 entries (exact path), including the short
+    last slice."""
     base = W.make("c2", rows=12, set_index=29)
-    V, S = base.vocab, (base.vocab + 8191) // 8192
+    V = base.vocab
+    S, L = slice_geometry(V)
     rng = np.random.default_rng(2029)
     logits = (rng.standard_normal((base.rows, V)) - 20.0).astype(np.float32)
     plant = [  # (slice, entries) per row
         [(0, 3), (7, 2)], [(0, 10)], [(0, 16)], [(0, 17)], [(2, 40), (9, 20)], [(S - 1, 30)],
-        [(0, 64)], [(0, 70)], [(s, 19) for s in range(S)], [(s, 12) for s in range(S)] + [(3, 8)],
+        [(0, 64)], [(0, 70)], [(s, 17) for s in range(S)], [(s, 6) for s in range(S)] + [(3, 8)],
         [(4, 5), (5, 5), (6, 5)], [(1, 33), (14, 1)],
     ]
     for r, spots in enumerate(plant):
         for s, n in spots:
-            lo, hi = s * 8192, min(V, (s + 1) * 8192)
+            lo, hi = s * L, min(V, (s + 1) * L)
             idx = rng.choice(np.arange(lo, hi), size=n, replace=False)
             logits[r, idx] = rng.uniform(9.0, 10.0, size=n).astype(np.float32)
     p = base.params.copy()
@@ -503,6 +513,7 @@ def test_top_n_with_clustered_maxima(sampler):
     candidate capacity: exact path), spread over slices, and top-20."""
     base = W.make("c2", rows=8, set_index=31)
     V = base.vocab
+    S, L = slice_geometry(V)
     rng = np.random.default_rng(2031)
     logits = (rng.standard_normal((base.rows, V)) * 3.0).astype(np.float32)
     f32 = lambda x: np.asarray(x, dtype=np.float32)
@@ -513,7 +524,7 @@ def test_top_n_with_clustered_maxima(sampler):
         if s is None:
             idx = rng.choice(V, size=n, replace=False)
         else:
-            lo, hi = s * 8192, min(V, (s + 1) * 8192)
+            lo, hi = s * L, min(V, (s + 1) * L)
             idx = rng.choice(np.arange(lo, hi), size=n, replace=False)
         logits[r, idx] = vals
     for n_top in (5, 20):
