@@ -202,6 +202,7 @@ int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
     // kernels re-derive each row's mode on the device). Without a host copy
     // of the params both are launched.
     bool any_slice = true, any_general = true, any_nucleus = true;
+    uint32_t ss_modes = 0;   // the sliced modes seen (0: unknown)
     if (b->params_host) {
         any_slice = any_general = any_nucleus = false;
         for (uint32_t r = 0; r < b->rows; ++r) {
@@ -212,6 +213,7 @@ int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
                 if (!masked && b->mask && !b->has_mask) continue;  // every row masked
                 const uint32_t m = lcs::row_mode(p, masked, b->vocab);
                 any_slice = any_slice || (m != lcs::kModeGeneral && m != lcs::kModeNucleus);
+                if (m != lcs::kModeGeneral && m != lcs::kModeNucleus) ss_modes |= m;
                 any_general = any_general || m == lcs::kModeGeneral;
                 any_nucleus = any_nucleus || m == lcs::kModeNucleus;
             }
@@ -255,6 +257,7 @@ int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
     // every row known to run sliced: the slice kernel may start its logit
     // loads before it has the row's parameters
     a.all_sliced = (b->params_host && !any_general && !any_nucleus) ? 1u : 0u;
+    a.ss_modes = ss_modes;
     // likewise for the nucleus kernels when every row takes that path
     a.all_nucleus = (b->params_host && !any_general && !any_slice) ? 1u : 0u;
     a.nrow = c->nrow;

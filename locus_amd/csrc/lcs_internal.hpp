@@ -48,6 +48,8 @@ constexpr uint32_t kWords = 2 * kWords64;          // in uint32 units (workspace
 constexpr uint32_t kFlagWinTrunc = 1u;             // more window entries than kWinCap (top kWinCap kept)
 constexpr uint32_t kFlagCandOverflow = 2u;         // more top-n candidates than the slice holds
 constexpr uint32_t kFlagWinLost = 4u;              // more window entries than the slice could rank
+constexpr uint32_t kFlagPenOverflow = 8u;          // more penalised groups than the slice could take
+constexpr uint32_t kFlagExact = 16u;               // the row is resolved on the exact path
 }  // namespace rec
 
 // ---- single-workgroup exact path ----
@@ -138,6 +140,7 @@ struct SampleArgs {   // (at most 128 dwords: kernels stage it in LDS, two dword
     uint32_t slices;         // nucleus: workgroups per row
     uint32_t slice_len;      // nucleus: elements per slice (multiple of 8)
     uint32_t all_sliced;     // 1: the host saw every row take a sliced mode
+    uint32_t ss_modes;       // sliced modes the host saw (0: unknown)
     uint32_t all_nucleus;    // 1: the host saw every row take the nucleus mode
     uint32_t nuc_row0;       // first row of this nucleus launch
     // nucleus path workspace, for rows nuc_row0 .. nuc_row0 + kNucRows - 1

@@ -99,59 +99,76 @@ __device__ __forceinline__ double ent_bound(double S, uint32_t n, float mk) {
 }
 
 // ============================================================ slice_stats ==
-constexpr int kPenWave = kSsWaves - 1;         // the wave that counts the history ids
+constexpr uint32_t kXElems = 2048;   // logits of penalised groups a slice takes as exceptions
+                                     // (a quarter per wave)
+constexpr uint32_t kXParts = 2 * kSsWaves;   // partials: one per wave over its unpenalised groups,
+                                             // one per wave over the exceptions it resolved
 
 struct SsSmem {
-    uint32_t tab[kSsMax];      // per slice position: history count, then penalised ^ raw bits
-    float lmax[kSsThreads];    // raw lane maxima (top-n bound)
-    float lmaxp[kSsThreads];   // penalised lane maxima (top-k bound)
-    float mraw[kSsWaves];      // the waves' raw maxima and raw sums against them
+    uint32_t cnt[kSsMax / 2];   // history counts, 16 bits per slice position
+    uint32_t gbit[kSsThreads];  // bit j of word t: group j * kSsThreads + t holds a counted position
+    float xv[kXElems];          // exception groups' raw logits
+    uint16_t xg[kXElems / 4];   // their group index in the slice
+    float lmax[kSsThreads];     // raw lane maxima (top-n bound)
+    float lmaxp[kSsThreads];    // lane maxima over unpenalised groups (top-k bound)
+    float mraw[kSsWaves];       // the waves' raw maxima and raw sums against them
     float sraw[kSsWaves];
-    float mpen[kSsWaves];      // the waves' penalised maxima (greedy: first index, raw logit there)
-    uint32_t ipen[kSsWaves];
-    float rpen[kSsWaves];
-    float mmsk[kSsWaves];      // the same over allowed ids (masked greedy rows)
-    uint32_t imsk[kSsWaves];
-    float rmsk[kSsWaves];
-    uint32_t nall[kSsWaves];
-    float bulk[kSsWaves];      // window rows: the bulk against the wave's penalised max
-    float t_s;                 // top-n bound
+    uint32_t nall[kSsWaves];    // masked rows: allowed ids
+    float pmax[kXParts];        // penalised max (greedy: its first index and raw logit)
+    uint32_t pidx[kXParts];
+    float praw[kXParts];
+    float mmax[kXParts];        // the same over allowed ids (masked greedy rows)
+    uint32_t midx[kXParts];
+    float mrw[kXParts];
+    float bref[kXParts];        // window rows: the bulk against the reference bref
+    float bulk[kXParts];
+    float t_s;                  // top-n bound
+    uint32_t nxw[kSsWaves];     // penalised groups per wave
     uint32_t ncand, nwin;
-    uint64_t ck[kCandCap];     // top-n candidates (rank keys)
-    uint64_t wk[kWinLds];      // window / top-k entries (rank keys)
+    uint64_t ck[kCandCap];      // top-n candidates (rank keys)
+    uint64_t wk[kWinLds];       // window / top-k entries (rank keys) and their raw logits
+    float wr[kWinLds];
 };
 
 // One workgroup per (row, slice), four waves holding the slice's logits (32
-// per thread). The leading scalar arguments repeat fields of `a` that the
+// per thread, in 16-byte groups: group j of thread t is slice group
+// j * 256 + t). The leading scalar arguments repeat fields of `a` that the
 // prologue needs: the build preloads them into SGPRs at wave launch, so the
 // logit loads issue with no scalar round trip.
 //
-//   waves 0-2:  logit loads; raw lane / wave maxima, the raw sum against the
-//               wave max                                                 | B1
-//   wave 3:     first clears the penalty table and loads the history window
-//               (its loads go out ahead of its own logits: a wave's loads
-//               return in order), then its logits; counts the in-slice ids
-//               into the table; then as waves 0-2                         | B1
-//   B1 -> B2:   penalties applied by the thread holding each counted
-//               position (sampling.cpp:34-39, once per distinct id, with its
-//               count), the word penalised ^ raw left in the table; the
-//               penalised lane and wave maxima, the bulk against the wave
-//               max; the slice's top-n bound (wave 3)
-//   B2 -> B3:   top-n candidates (raw values), window entries against the
-//               slice max (or top-k entries)
-//   B3 ->:      the record: header (waves 0 and 2), top-n (wave 1),
-//               entries (wave 2)
-template <int G>
+// Arithmetic per logit is what bounds this kernel once the logits have
+// arrived (a wave64 VALU instruction holds its SIMD for four cycles, and 16
+// waves share a CU), so each logit costs a group max step, one exp per sum
+// and nothing else. Penalties (sampling.cpp:16-41) touch only the groups
+// that hold a history id: those groups leave the waves' reductions and are
+// resolved as exceptions, a group per lane.
+//
+//   B0          the count tables cleared (rows with penalties)
+//   -> B1       raw group / lane / wave maxima; the raw sum (logprobs) and
+//               the tempered group sums (window rows) against the wave's raw
+//               max; history ids counted into the tables
+//   -> B2       reductions over the unpenalised groups; each wave copies
+//               its penalised groups to its part of the exception list and
+//               resolves them (counts, penalties, their maxima and sums); the
+//               slice's top-n bound
+//   -> B3       top-n candidates (raw), window entries against the slice max
+//               (or top-k entries against a lower bound of the k-th largest)
+//   ->          the record: header (waves 0 and 2), top-n (wave 1), entries
+//               (wave 2)
+template <int G, uint32_t MS>
 __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, uint64_t row_stride, uint32_t rows,
                                                         uint32_t slices, uint32_t slice_len, uint32_t vocab,
                                                         uint32_t flags, uint32_t all_sliced, SampleArgs a) {
     constexpr int NT = kSsThreads;
-    constexpr int NG = kSsElems / G;      // 16-byte groups per thread
+    constexpr int NG = kSsElems / G;      // groups per thread
     constexpr int NE = kSsElems;
+    constexpr uint32_t XQ = kXElems / G / kSsWaves;   // exception groups a wave holds
+    constexpr int XR = (int)(XQ / kWave);             // exception groups per lane
+    static_assert(XQ % kWave == 0 && XQ * kSsWaves <= kXElems / 4, "exception list sizes");
     __shared__ SsSmem sm;
     const uint32_t tid = tid_x();
-    const int lane = lane_id(), wv = (int)(tid / kWave);
-    const bool penw = wv == kPenWave;
+    const int lane = lane_id();
+    const int wv = __builtin_amdgcn_readfirstlane((int)(tid / kWave));   // (an SGPR: wave-uniform branches)
     const uint32_t S = slices;
     // Workgroups are dealt to the 8 XCDs round-robin; when the grid divides
     // evenly, a row's slices are placed on one XCD so that its L2 serves the
@@ -168,29 +185,32 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
     const uint32_t lo = slice * slice_len;
     const uint32_t hi = min(V, lo + slice_len);
     const uint32_t len = hi - lo;
-    const uint32_t dt = tid;
-    // the slice's logits, one 16-byte load per group (groups past the slice
-    // load the slice's first group and are masked below); waves 0-2 issue
-    // them first when the host saw every row take this path, else once the
-    // row's mode is known; wave 3 after its history ids
+    // the slice's logits, one 16-byte buffer load per group: the row, up to
+    // its last 16-byte group (rows are whole 16-byte groups: the stride is a
+    // multiple of one), is the buffer, and the hardware range check returns
+    // 0 past it; each group row's offset is a scalar, the lane's 16 bytes the
+    // one vector offset; positions past the slice are masked below. Issued
+    // first when the host saw every row take this path, else once the row's
+    // mode is known.
     uint4 raw[NG];
+    const uint32_t esz = G == 8 ? 2u : 4u;
+    const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(rowp), 0,
+                                                                         (int)((V * esz + 15u) & ~15u), 0x00020000);
     auto load_logits = [&]() {
 #pragma unroll
-        for (int j = 0; j < NG; ++j) {
-            const uint32_t e0 = lo + (j * NT + dt) * G;
-            raw[j] = load16(rowp, (e0 < hi ? e0 : lo) / G);
-        }
+        for (int j = 0; j < NG; ++j)
+            raw[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   lrs, tid * 16u, (lo + (uint32_t)j * NT * G) * esz, 0));
     };
     const bool early = all_sliced != 0u;
-    if (early && !penw) load_logits();
+    if (early) load_logits();
     // per-row words come through the scalar cache, so that waiting for them
     // never waits for the logits; the history offsets are loaded whether or
     // not the row has penalties, so that they arrive with its parameters
-    uint32_t hoff = 0, hend = 0, htot = 0;
+    uint32_t hoff = 0, hend = 0;
     if (a.hist_off != nullptr) {
         hoff = scalar_load(a.hist_off + row);
         hend = scalar_load(a.hist_off + row + 1);
-        htot = scalar_load(a.hist_off + rows);
     }
     const lcs_params P = scalar_load(a.params + row);
     const bool masked = a.mask != nullptr && (a.has_mask == nullptr || scalar_load_u8(a.has_mask + row) != 0);
@@ -204,70 +224,83 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
     const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
     uint64_t* myrec = a.srecs + ((uint64_t)row * kSsMaxSlices + slice) * rec::kWords64;
     const float NEG = -__builtin_huge_valf();
-    const bool stoch = mode == kModeWindow;
-    const bool topk = mode == kModeTopK;
+    if ((mode & MS) == 0u) {
+        // a sliced row this instantiation leaves out (the host's parameter
+        // copy disagreed): row_fin resolves it on the exact path
+        if (tid == 0) myrec[0] = (uint64_t)rec::kFlagExact << 48;
+        wait_all_memory();
+        return;
+    }
+    const bool greedy = (MS & kModeGreedy) != 0u && mode == kModeGreedy;
+    const bool stoch = (MS & kModeWindow) != 0u && mode == kModeWindow;
+    const bool topk = (MS & kModeTopK) != 0u && mode == kModeTopK;
     const bool pen = penalties_active(P) && a.hist_off != nullptr && P.repeat_last_n > 0;
-    if (tid == 0) { sm.ncand = 0; sm.nwin = 0; }
-    // the history window [hs, hs + nwin_h): 16-byte buffer loads over the
-    // whole id array (aligned to the array; the hardware range check returns
-    // 0 past its end), group g at array index w0 + 4 g
+    const float inv_t = stoch ? fdiv(1.0f, P.temperature) : 1.0f;
+    const float kk = fmul(inv_t, kLog2E);   // tempered offsets in log2 units
+    if (!early) load_logits();
+
+    // the history window [hs, hend): 16-byte buffer loads from the aligned
+    // word w0 <= hs, wave w taking groups (c * 4 + w) * 64 + lane; the words
+    // before hs are dropped from the first group, and the buffer ends at
+    // hend, so the words past it (up to the last row of 64 groups) read as 0:
+    // id 0, counted at position 0 of slice 0 and taken out again (zpad)
     const uint32_t hn = hend - hoff;
-    const uint32_t nwin_h = pen ? (hn > P.repeat_last_n ? P.repeat_last_n : hn) : 0u;
+    const uint32_t nwin_h = pen ? min(hn, P.repeat_last_n) : 0u;
     const uint32_t hs = hend - nwin_h;
     const uint32_t w0 = hs & ~3u;
-    const uint32_t nq = (hend - w0 + 3) / 4;   // groups, <= (kFastHistMax + 6) / 4
-    const bool hany = nwin_h > 0;
-    constexpr int HC = 9;                      // groups per lane per chunk (2304 ids a chunk)
-    constexpr uint32_t kChunk = HC * kWave;
+    const uint32_t nq = (hend - w0 + 3) / 4;   // groups of the window, <= (kFastHistMax + 6) / 4
+    const bool hany = nwin_h > 0;              // (uniform over the workgroup)
+    const uint32_t zpad = lo == 0u && hany ? 4u * kWave * ((nq + kWave - 1) / kWave) - (hend - w0) : 0u;
+    constexpr int HC = 3;                      // groups per lane per pass (3072 ids a pass)
+    constexpr uint32_t kPass = HC * kSsWaves * kWave;
     int4 hq[HC];
     const __amdgpu_buffer_rsrc_t hrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int32_t*>(a.hist_ids), 0, (int)min((uint64_t)htot * 4u, (uint64_t)0x7ffffffc), 0x00020000);
+        const_cast<int32_t*>(a.hist_ids + w0), 0, (int)((hend - w0) * 4u), 0x00020000);
+    auto hgroup = [&](uint32_t base, int c) { return base + ((uint32_t)c * kSsWaves + (uint32_t)wv) * kWave + (uint32_t)lane; };
     auto hload = [&](uint32_t base) {
 #pragma unroll
-        for (int g = 0; g < HC; ++g) {
-            if (base + (uint32_t)g * kWave < nq) {
-                const uint32_t gi = min(base + (uint32_t)g * kWave + (uint32_t)lane, nq - 1u);
-                hq[g] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(hrs, (w0 + 4u * gi) * 4u, 0, 0));
-            }
+        for (int c = 0; c < HC; ++c) {
+            if (hgroup(base, c) - (uint32_t)lane < nq)   // (wave-uniform)
+                hq[c] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(hrs, hgroup(base, c) * 16u, 0, 0));
         }
     };
     auto hcount = [&](uint32_t base) {
-        // branch-free: an id outside the slice or the window adds 0 to a slot
-        // of its own lane; this wave's LDS operations stay in order
-        const uint32_t gl = hs - w0, gh = hend - w0;   // window words
+        // ids outside the slice are skipped
+        const uint32_t gl = hs - w0;   // words of the first group before the window
 #pragma unroll
-        for (int g = 0; g < HC; ++g) {
-            if (base + (uint32_t)g * kWave < nq) {
-                const int32_t h4[4] = {hq[g].x, hq[g].y, hq[g].z, hq[g].w};
-                const uint32_t gi = base + (uint32_t)g * kWave + (uint32_t)lane;
+        for (int c = 0; c < HC; ++c) {
+            const uint32_t gi = hgroup(base, c);
+            if (gi - (uint32_t)lane < nq) {
+                int32_t h4[4] = {hq[c].x, hq[c].y, hq[c].z, hq[c].w};
+                if (gi == 0u) {
+#pragma unroll
+                    for (int m = 0; m < 3; ++m) h4[m] = (uint32_t)m < gl ? -1 : h4[m];
+                }
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
                     const uint32_t d = (uint32_t)h4[m] - lo;   // d < len: in the slice (hence < V)
-                    const bool in = gi < nq && d < len && 4u * gi + (uint32_t)m - gl < gh - gl;
-                    atomicAdd(&sm.tab[in ? d : (uint32_t)lane], in ? 1u : 0u);
+                    if (d < len) {
+                        atomicAdd(&sm.cnt[d >> 1], 1u << ((d & 1u) << 4));
+                        atomicOr(&sm.gbit[(d / G) % NT], 1u << (d / (G * NT)));
+                    }
                 }
             }
         }
     };
-    if (penw) {
-        if (hany) hload(0);
-        load_logits();
-        if (hany) {
-#pragma unroll 8
-            for (int i = 0; i < (int)(kSsMax / 4 / kWave); ++i)
-                reinterpret_cast<uint4*>(sm.tab)[i * kWave + lane] = make_uint4(0, 0, 0, 0);
-            hcount(0);
-            for (uint32_t b = kChunk; b < nq; b += kChunk) {   // windows past 2300 ids
-                hload(b);
-                hcount(b);
-            }
-        }
-    } else if (!early) {
-        load_logits();
+    if (hany) {
+        hload(0);
+        // clear the tables (16 count words and one group word a thread)
+#pragma unroll
+        for (int i = 0; i < (int)(kSsMax / 2 / 4 / NT); ++i)
+            reinterpret_cast<uint4*>(sm.cnt)[i * NT + tid] = make_uint4(0, 0, 0, 0);
+        sm.gbit[tid] = 0u;
+        __syncthreads();   // B0
     }
+    if (tid == 0) { sm.ncand = 0; sm.nwin = 0; }
 
     float v[NE];
-    float gr[NG], gm[NG];   // raw and penalised group maxima
+    float gr[NG];   // raw group maxima
+    float cb[NG];   // window rows: tempered group sums against the wave's raw max
     float lm = NEG;
     {
         // values; positions past the slice read as -inf
@@ -279,16 +312,12 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
             for (int k = 0; k < G; ++k) v[j * G + k] = t[k];
             // wave-uniform: does this group row run past the slice for any lane?
             if (lo + (j * NT + (uint32_t)wv * kWave + kWave) * G > hi) {
-                const uint32_t e0 = lo + (j * NT + dt) * G;
+                const uint32_t e0 = lo + (j * NT + tid) * G;
 #pragma unroll
                 for (int k = 0; k < G; ++k) v[j * G + k] = e0 + k < hi ? v[j * G + k] : NEG;
             }
         }
         PROF_W0(wg_x(), 1);
-        // raw lane maxima and each group's max (threshold scans test a group
-        // at a time); the raw sum of exp against the wave's max Mw: terms
-        // 2^fma(v, L, b) with b = RN(-Mw L) share the exponent error
-        // e_b = Mw L + b (exact in an fma), taken out below
 #pragma unroll
         for (int j = 0; j < NG; ++j) {
             gr[j] = v[j * G];
@@ -296,34 +325,302 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
             for (int k = 1; k < G; ++k) gr[j] = fmaxf(gr[j], v[j * G + k]);
             lm = fmaxf(lm, gr[j]);
         }
-        sm.lmax[dt] = lm;
+        sm.lmax[tid] = lm;
+        // sums of exponentials against the wave's raw max Mw: terms
+        // 2^fma(v, K, b) with b = RN(-Mw K) share the exponent error
+        // e_b = Mw K + b (exact in an fma), taken out of the sums
         const float Mw = wave_max(lm);
-        float sw = 0.0f;
-        if (want_lp && Mw != NEG) {
-            const float b = -Mw * kLog2E;
-            float s = 0.0f;
+        float sr = 0.0f;
+        const float br = -Mw * kLog2E, bb = -Mw * kk;
+#pragma unroll
+        for (int j = 0; j < NG; ++j) cb[j] = 0.0f;
+        if (Mw != NEG) {   // (a wave past the slice's end holds no term)
 #pragma unroll
             for (int j = 0; j < NG; ++j) {
-                float c[G];
+                if (want_lp) {
+                    float c[G];
 #pragma unroll
-                for (int k = 0; k < G; ++k) c[k] = fast_exp2(fmaf(v[j * G + k], kLog2E, b));
+                    for (int k = 0; k < G; ++k) c[k] = fast_exp2(fmaf(v[j * G + k], kLog2E, br));
 #pragma unroll
-                for (int w = G / 2; w >= 1; w /= 2)
+                    for (int w = G / 2; w >= 1; w /= 2)
 #pragma unroll
-                    for (int k = 0; k < w; ++k) c[k] += c[k + w];
-                s += c[0];
+                        for (int k = 0; k < w; ++k) c[k] += c[k + w];
+                    sr += c[0];
+                }
+                if (stoch) {
+                    float c[G];
+#pragma unroll
+                    for (int k = 0; k < G; ++k) c[k] = fast_exp2(fmaf(v[j * G + k], kk, bb));
+#pragma unroll
+                    for (int w = G / 2; w >= 1; w /= 2)
+#pragma unroll
+                        for (int k = 0; k < w; ++k) c[k] += c[k + w];
+                    cb[j] = c[0];
+                }
             }
-            sw = wave_sum_f(s) * fast_exp2(-fmaf(Mw, kLog2E, b));
         }
-        if (lane == 0) { sm.sraw[wv] = sw; sm.mraw[wv] = Mw; }
+        if (want_lp) {
+            const float sw = Mw != NEG ? wave_sum_f(sr) * fast_exp2(-fmaf(Mw, kLog2E, br)) : 0.0f;
+            if (lane == 0) { sm.sraw[wv] = sw; sm.mraw[wv] = Mw; }
+        } else if (lane == 0) {
+            sm.mraw[wv] = Mw;
+        }
         PROF_W0(wg_x(), 2);
+        if (hany) {
+            hcount(0);
+            for (uint32_t b = kPass; b < nq; b += kPass) {   // windows past 3000 ids
+                hload(b);
+                hcount(b);
+            }
+        }
+        // the wave's raw max travels to the penalised phase in bref (window rows)
+        if (stoch && lane == 0) sm.bref[wv] = Mw;
     }
     __syncthreads();   // B1: the counts, the raw lane maxima
     PROF_W0(wg_x(), 3);
-    auto eid = [&](int q) { return lo + ((q / G) * NT + dt) * G + (uint32_t)(q % G); };
-    auto pos = [&](int q) { return ((q / G) * NT + dt) * G + (uint32_t)(q % G); };   // slice position
-    float lpm = NEG;   // lane max of the penalised values; gm then holds their group maxima
-    if (ntop && penw) {
+
+    // ---- reductions over the unpenalised groups (for those, penalised =
+    // raw), and the penalised groups copied out as exceptions ----
+    const uint32_t hb = hany ? sm.gbit[tid] : 0u;   // bit j: group j holds a counted position
+    auto eid = [&](int q) { return lo + ((q / G) * NT + tid) * G + (uint32_t)(q % G); };
+    float gm[NG];   // group maxima over unpenalised groups (-inf for penalised ones)
+    float lpm = NEG;
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+        gm[j] = ((hb >> j) & 1u) ? NEG : gr[j];
+        lpm = fmaxf(lpm, gm[j]);
+    }
+    const float mwp = wave_max(lpm);
+    if (topk) sm.lmaxp[tid] = lpm;
+    if (greedy) {
+        // first index of the max (and of the max over allowed ids) among the
+        // unpenalised groups; the lanes holding the wave max look for it
+        uint32_t bi = kNoIdx;
+        if (lpm == mwp) {   // (all lanes when the values are -inf)
+#pragma unroll
+            for (int j = NG - 1; j >= 0; --j) {
+                if (!((hb >> j) & 1u) && gm[j] == mwp) {
+#pragma unroll
+                    for (int k = G - 1; k >= 0; --k)
+                        bi = (v[j * G + k] == mwp && eid(j * G + k) < hi) ? eid(j * G + k) : bi;
+                }
+            }
+        }
+        bi = wave_min_u(bi);
+        float mv = NEG, mr = 0.0f;
+        uint32_t mi = kNoIdx, na = 0;
+        if (mrow) {
+            float lmm = NEG;
+            uint32_t mw[NG];
+#pragma unroll
+            for (int j = 0; j < NG; ++j) {
+                const uint32_t e0 = lo + (j * NT + tid) * G;
+                const uint32_t ee = e0 < hi ? e0 : lo;
+                mw[j] = e0 < hi ? (mrow[ee >> 5] >> (ee & 31u)) & ((1u << G) - 1u) : 0u;
+                if (e0 + G > hi) {
+#pragma unroll
+                    for (int k = 0; k < G; ++k) mw[j] &= e0 + k < hi ? ~0u : ~(1u << k);
+                }
+                na += (uint32_t)__builtin_popcount(mw[j]);
+                if (!((hb >> j) & 1u)) {
+#pragma unroll
+                    for (int k = 0; k < G; ++k) lmm = ((mw[j] >> k) & 1u) ? fmaxf(lmm, v[j * G + k]) : lmm;
+                }
+            }
+            mv = wave_max(lmm);
+            if (lmm == mv) {
+#pragma unroll
+                for (int j = NG - 1; j >= 0; --j) {
+                    if (!((hb >> j) & 1u) && mw[j] != 0u) {
+#pragma unroll
+                        for (int k = G - 1; k >= 0; --k)
+                            mi = (((mw[j] >> k) & 1u) && v[j * G + k] == mv) ? eid(j * G + k) : mi;
+                    }
+                }
+            }
+            mi = wave_min_u(mi);
+            na = wave_sum_u(na);
+            mr = mv;
+        }
+        if (lane == 0) {
+            sm.pmax[wv] = mwp; sm.pidx[wv] = bi; sm.praw[wv] = mwp;
+            sm.mmax[wv] = mv; sm.midx[wv] = mi; sm.mrw[wv] = mr; sm.nall[wv] = na;
+        }
+    } else {
+        if (lane == 0) sm.pmax[wv] = mwp;
+        if (stoch) {
+            // the bulk over the unpenalised groups against the wave's raw max
+            // (or, when the penalised groups held the top and the rest lie
+            // far below it, recomputed against their own max)
+            const float Mw = sm.bref[wv];
+            float bs = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NG; ++j) bs += ((hb >> j) & 1u) ? 0.0f : cb[j];
+            float ref = Mw, bsum = 0.0f;
+            if (mwp != NEG) {
+                if ((Mw - mwp) * kk <= 64.0f) {
+                    const float bb = -Mw * kk;
+                    bsum = wave_sum_f(bs) * fast_exp2(-fmaf(Mw, kk, bb));
+                } else {
+                    ref = mwp;
+                    const float bb = -mwp * kk;
+                    bs = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < NG; ++j) {
+                        if (!((hb >> j) & 1u)) {
+#pragma unroll
+                            for (int k = 0; k < G; ++k) bs += fast_exp2(fmaf(v[j * G + k], kk, bb));
+                        }
+                    }
+                    bsum = wave_sum_f(bs) * fast_exp2(-fmaf(mwp, kk, bb));
+                }
+            }
+            if (lane == 0) { sm.bref[wv] = ref; sm.bulk[wv] = bsum; }
+        }
+    }
+    // penalised groups to this wave's part of the exception list, in (group
+    // row, lane) order: the list and so every sum over it is the same on
+    // every run
+    uint32_t nxa = 0;   // (wave-uniform)
+    if (hany) {
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            const bool h = ((hb >> j) & 1u) != 0u;
+            const uint64_t m = ballot(h);
+            if (h) {
+                const uint32_t s = nxa + (uint32_t)__builtin_amdgcn_mbcnt_hi(
+                                             (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                if (s < XQ) {
+                    const uint32_t sw = (uint32_t)wv * XQ + s;
+                    sm.xg[sw] = (uint16_t)(j * NT + tid);
+#pragma unroll
+                    for (int k = 0; k < G; k += 4)
+                        *reinterpret_cast<float4*>(&sm.xv[sw * G + k]) =
+                            make_float4(v[j * G + k], v[j * G + k + 1], v[j * G + k + 2], v[j * G + k + 3]);
+                }
+            }
+            nxa += (uint32_t)__builtin_popcountll(m);
+        }
+        if (lane == 0) sm.nxw[wv] = nxa;
+        wave_sync();   // (only this wave reads its part)
+    } else if (lane == 0) {
+        sm.nxw[wv] = 0u;
+    }
+    PROF_W0(wg_x(), 4);
+
+    // ---- exceptions: a group per lane, penalties as apply_penalties
+    // (sampling.cpp:34-39: once per distinct id, with its count) ----
+    const uint32_t nx = min(nxa, XQ);
+    float xp[XR][G];    // penalised logits of this lane's exceptions (-inf: none)
+    uint32_t xe[XR];    // their first id (none: past any slice)
+#pragma unroll
+    for (int r = 0; r < XR; ++r) {
+        xe[r] = 0xfffffff0u;
+#pragma unroll
+        for (int k = 0; k < G; ++k) xp[r][k] = NEG;
+    }
+    if (nx) {
+        const double inv_rp = 1.0 / (double)P.repeat_penalty;
+#pragma unroll
+        for (int r = 0; r < XR; ++r) {
+            const uint32_t s = (uint32_t)r * kWave + (uint32_t)lane;
+            if (s < nx) {
+                const uint32_t gx = sm.xg[(uint32_t)wv * XQ + s];
+                xe[r] = lo + gx * G;
+                uint32_t cw[G / 2];
+#pragma unroll
+                for (int k = 0; k < G / 2; ++k) cw[k] = sm.cnt[gx * (G / 2) + k];
+                if (gx == 0u) cw[0] -= zpad;   // (the padding's zeros, all at position 0)
+#pragma unroll
+                for (int k = 0; k < G; ++k) {
+                    const float x = sm.xv[((uint32_t)wv * XQ + s) * G + k];
+                    const uint32_t c = (cw[k / 2] >> ((k & 1) * 16)) & 0xffffu;
+                    xp[r][k] = c ? penalize_fast(x, c, P, inv_rp) : x;
+                }
+            }
+        }
+        // this wave's exception partial: max, first index, bulk
+        float xm = NEG;
+#pragma unroll
+        for (int r = 0; r < XR; ++r)
+#pragma unroll
+            for (int k = 0; k < G; ++k) xm = fmaxf(xm, xp[r][k]);
+        const float xmw = wave_max(xm);
+        const int xw = kSsWaves + wv;
+        if (greedy) {
+            // (the lowest id among this lane's exceptions at the max: the
+            // list holds groups in no particular order)
+            uint32_t bi = kNoIdx, mi = kNoIdx;
+            float br = 0.0f, mv = NEG, mrr = 0.0f;
+            if (xm == xmw) {
+#pragma unroll
+                for (int r = 0; r < XR; ++r)
+#pragma unroll
+                    for (int k = 0; k < G; ++k) {
+                        const uint32_t e = xe[r] + k;
+                        if (xp[r][k] == xmw && e < hi && e < bi) {
+                            bi = e;
+                            br = sm.xv[((uint32_t)wv * XQ + (uint32_t)r * kWave + (uint32_t)lane) * G + k];
+                        }
+                    }
+            }
+            const uint32_t bi0 = bi;
+            bi = wave_min_u(bi);
+            const uint64_t ob = ballot(bi0 == bi && bi != kNoIdx);
+            br = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(br), ob ? __builtin_ctzll(ob) : 0));
+            if (mrow) {
+                float xmm = NEG;
+                bool al[XR][G];
+#pragma unroll
+                for (int r = 0; r < XR; ++r)
+#pragma unroll
+                    for (int k = 0; k < G; ++k) {
+                        const uint32_t e = xe[r] + k;
+                        const uint32_t ec = e < hi ? e : lo;   // (an id of the row)
+                        al[r][k] = e < hi && ((mrow[ec >> 5] >> (ec & 31u)) & 1u);
+                        xmm = al[r][k] ? fmaxf(xmm, xp[r][k]) : xmm;
+                    }
+                mv = wave_max(xmm);
+                if (xmm == mv) {
+#pragma unroll
+                    for (int r = 0; r < XR; ++r)
+#pragma unroll
+                        for (int k = 0; k < G; ++k) {
+                            const uint32_t e = xe[r] + k;
+                            if (al[r][k] && xp[r][k] == mv && e < mi) {
+                                mi = e;
+                                mrr = sm.xv[((uint32_t)wv * XQ + (uint32_t)r * kWave + (uint32_t)lane) * G + k];
+                            }
+                        }
+                }
+                const uint32_t mi0 = mi;
+                mi = wave_min_u(mi);
+                const uint64_t om = ballot(mi0 == mi && mi != kNoIdx);
+                mrr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mrr), om ? __builtin_ctzll(om) : 0));
+            }
+            if (lane == 0) {
+                sm.pmax[xw] = xmw; sm.pidx[xw] = bi; sm.praw[xw] = br;
+                sm.mmax[xw] = mv; sm.midx[xw] = mi; sm.mrw[xw] = mrr;
+            }
+        } else {
+            float xs = 0.0f;
+            if (stoch && xmw != NEG) {
+                const float bb = -xmw * kk;
+#pragma unroll
+                for (int r = 0; r < XR; ++r)
+#pragma unroll
+                    for (int k = 0; k < G; ++k) xs += fast_exp2(fmaf(xp[r][k], kk, bb));
+                xs = wave_sum_f(xs) * fast_exp2(-fmaf(xmw, kk, bb));
+            }
+            if (lane == 0) { sm.pmax[xw] = xmw; sm.bref[xw] = xmw; sm.bulk[xw] = xs; }
+        }
+    } else if (lane == 0) {
+        const int xw = kSsWaves + wv;
+        sm.pmax[xw] = NEG; sm.pidx[xw] = kNoIdx; sm.praw[xw] = 0.0f;
+        sm.mmax[xw] = NEG; sm.midx[xw] = kNoIdx; sm.mrw[xw] = 0.0f;
+        sm.bref[xw] = NEG; sm.bulk[xw] = 0.0f;
+    }
+    if (ntop && wv == kSsWaves - 1) {
         // the slice's top-n bound: the ntop-th largest of the lanes' largest
         // of four lane maxima, its sort key cut to 16 bits (every element of
         // the slice's top-n is >= it)
@@ -344,192 +641,75 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
         const uint32_t kneg = 0x007fffffu;   // fkey(-inf)
         if (lane == 0) sm.t_s = key_to_f(max(T << 16, kneg));
     }
-    {
-        // penalties by the holder of each counted position (four counts a
-        // read; a group row no lane of the wave needs is skipped); the divide
-        // l / repeat_penalty as in penalize_fast, the exact divide only for
-        // its rare tiny quotients
-        if (hany) {
-            const double inv_rp = 1.0 / (double)P.repeat_penalty;
-            const bool rp_on = P.repeat_penalty != 1.0f;
-#pragma unroll
-            for (int j = 0; j < NG; ++j) {
-#pragma unroll
-                for (int h4 = 0; h4 < G / 4; ++h4) {
-                    const int q0 = j * G + h4 * 4;
-                    uint4* slot = reinterpret_cast<uint4*>(sm.tab) + pos(q0) / 4;
-                    const uint4 cnt = *slot;
-                    const bool any = (cnt.x | cnt.y | cnt.z | cnt.w) != 0u;
-                    if (ballot(any)) {
-                        const uint32_t c4[4] = {cnt.x, cnt.y, cnt.z, cnt.w};
-                        uint32_t x4[4];
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            const float r = v[q0 + k];
-                            float l = r;
-                            if (rp_on) {
-                                const double y = (double)r * inv_rp;
-                                l = r > 0.0f ? (float)y : fmul(r, P.repeat_penalty);
-                                const bool tiny = c4[k] != 0u && r > 0.0f && !(y >= 0x1p-125);
-                                if (ballot(tiny)) l = tiny ? fdiv(r, P.repeat_penalty) : l;
-                            }
-                            const float sub = fadd(fmul(P.frequency_penalty, (float)c4[k]), P.presence_penalty);
-                            const float p = c4[k] ? fsub(l, sub) : r;
-                            x4[k] = __float_as_uint(p) ^ __float_as_uint(r);
-                            v[q0 + k] = p;
-                        }
-                        if (any) *slot = make_uint4(x4[0], x4[1], x4[2], x4[3]);
-                    }
-                }
-            }
-        }
-        PROF_W0(wg_x(), 4);
-        if (mode == kModeGreedy) {
-            // first index of the max, over all ids and over the allowed ids;
-            // the raw logit of each winner rides along for its logprob
-            float bv = NEG, mv = NEG, br = 0.0f, mr = 0.0f;
-            uint32_t bi = kNoIdx, mi = kNoIdx, na = 0;
-            uint32_t mw[NG];
-            if (mrow) {
-#pragma unroll
-                for (int j = 0; j < NG; ++j) {
-                    const uint32_t e0 = lo + (j * NT + dt) * G;
-                    const uint32_t ee = e0 < hi ? e0 : lo;
-                    mw[j] = mrow[ee >> 5] >> (ee & 31u);
-                }
-            }
-#pragma unroll
-            for (int q = 0; q < NE; ++q) {
-                const uint32_t e = eid(q);
-                const bool ok = e < hi;
-                const float x = v[q];
-                if (ok && (x > bv || bi == kNoIdx)) { bv = x; bi = e; }
-                if (mrow) {
-                    const bool al = ok && ((mw[q / G] >> (q % G)) & 1u);
-                    na += al ? 1u : 0u;
-                    if (al && (x > mv || mi == kNoIdx)) { mv = x; mi = e; }
-                }
-            }
-            br = bv;
-            mr = mv;
-            if (want_lp && hany) {
-                if (bi < V) br = __uint_as_float(__float_as_uint(bv) ^ sm.tab[bi - lo]);
-                if (mi < V) mr = __uint_as_float(__float_as_uint(mv) ^ sm.tab[mi - lo]);
-            }
-            const uint32_t bi0 = bi, mi0 = mi;
-            wave_argmax(bv, bi);
-            const uint64_t ob = ballot(bi0 == bi && bi < V);
-            br = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(br), ob ? __builtin_ctzll(ob) : 0));
-            if (mrow) {
-                wave_argmax(mv, mi);
-                const uint64_t om = ballot(mi0 == mi && mi < V);
-                mr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mr), om ? __builtin_ctzll(om) : 0));
-                na = wave_sum_u(na);
-            }
-            if (lane == 0) {
-                sm.mpen[wv] = bv; sm.ipen[wv] = bi; sm.rpen[wv] = br;
-                sm.mmsk[wv] = mv; sm.imsk[wv] = mi; sm.rmsk[wv] = mr; sm.nall[wv] = na;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < NG; ++j) {
-                gm[j] = v[j * G];
-#pragma unroll
-                for (int k = 1; k < G; ++k) gm[j] = fmaxf(gm[j], v[j * G + k]);
-                lpm = fmaxf(lpm, gm[j]);
-            }
-            const float mwp = wave_max(lpm);
-            if (lane == 0) sm.mpen[wv] = mwp;
-            if (topk) sm.lmaxp[dt] = lpm;
-            if (stoch) {
-                // the normaliser's bulk against the wave's penalised max mw:
-                // term c = 2^t, t = RN(p kk + bb) = (p - mw) kk + e + rounding,
-                // with bb = RN(-mw kk) and e = mw kk + bb common to all terms
-                // (taken out below); the record's bound covers sum c|t|, which
-                // bounds the rounding of t here and in the reference's tempered
-                // offsets
-                const float inv_t = fdiv(1.0f, P.temperature);
-                const float kk = fmul(inv_t, kLog2E);
-                const float bb = mwp != NEG ? -mwp * kk : 0.0f;
-                float bs = 0.0f;
-                if (mwp != NEG) {   // (a wave past the slice's end holds no term)
-#pragma unroll
-                    for (int j = 0; j < NG; ++j) {
-                        float c[G];
-#pragma unroll
-                        for (int k = 0; k < G; ++k) c[k] = fast_exp2(fmaf(v[j * G + k], kk, bb));
-#pragma unroll
-                        for (int w = G / 2; w >= 1; w /= 2)
-#pragma unroll
-                            for (int k = 0; k < w; ++k) c[k] += c[k + w];
-                        bs += c[0];
-                    }
-                }
-                const float bsum = mwp != NEG ? wave_sum_f(bs) * fast_exp2(-fmaf(mwp, kk, bb)) : 0.0f;
-                if (lane == 0) sm.bulk[wv] = bsum;
-            }
-        }
-        PROF_W0(wg_x(), 5);
-    }
-    __syncthreads();   // B2: the top-n bound, the waves' penalised maxima
+    PROF_W0(wg_x(), 5);
+    __syncthreads();   // B2: the partials, the top-n bound
     PROF_W0(wg_x(), 6);
-    const double delta = stoch ? (double)P.temperature *
-                                     (-(double)__builtin_amdgcn_logf(P.min_p) * 0.6931471805599453 * (1.0 + 1e-6) + 1e-3)
-                               : 0.0;
-    float wthr = NEG;   // window rows: the slice's threshold ms - delta, rounded down
-    float ms = NEG;
-    if (stoch) {
-        ms = fmaxf(fmaxf(sm.mpen[0], sm.mpen[1]), fmaxf(sm.mpen[2], sm.mpen[3]));
-        const double thr = (double)ms - delta;
-        wthr = (float)thr;
-        if ((double)wthr > thr) wthr = next_down(wthr);
-    }
-    {
-        // top-n candidates: raw values (penalised ^ word) >= the bound, in
-        // the few lanes and groups that can hold one (their raw group max is
-        // at most their lane's raw max)
-        if (ntop) {
-            const float t = sm.t_s;
-            if (lm >= t) {
+
+    float ms = NEG;    // the slice's penalised max
 #pragma unroll
-                for (int j = 0; j < NG; ++j) {
-                    if (gr[j] >= t) {
+    for (int w = 0; w < (int)kXParts; ++w) ms = fmaxf(ms, sm.pmax[w]);
+    // top-n candidates: raw values >= the bound, in the few lanes and groups
+    // that can hold one (a group's raw max bounds its values)
+    if (ntop) {
+        const float t = sm.t_s;
+        if (lm >= t) {
 #pragma unroll
-                        for (int k = 0; k < G; ++k) {
-                            const int q = j * G + k;
-                            const uint32_t e = eid(q);
-                            const float x = hany ? __uint_as_float(__float_as_uint(v[q]) ^ sm.tab[pos(q)]) : v[q];
-                            if (x >= t && e < hi) {
-                                const uint32_t s = atomicAdd(&sm.ncand, 1u);
-                                if (s < kCandCap) sm.ck[s] = rank_key(x, e);
-                            }
+            for (int j = 0; j < NG; ++j) {
+                if (gr[j] >= t) {
+#pragma unroll
+                    for (int k = 0; k < G; ++k) {
+                        const int q = j * G + k;
+                        if (v[q] >= t && eid(q) < hi) {
+                            const uint32_t s = atomicAdd(&sm.ncand, 1u);
+                            if (s < kCandCap) sm.ck[s] = rank_key(v[q], eid(q));
                         }
                     }
                 }
             }
         }
-        // window entries p >= ms - delta, or the top-k entries: elements >=
-        // a lower bound of the slice's k-th largest (the k-th largest
-        // penalised lane max, its key cut to 16 bits); the publish ranks them
-        float t = wthr;
-        if (topk) {
+    }
+    if (stoch || topk) {
+        // window entries p >= ms - delta (min-p: p >= ms + T ln(min_p) up to
+        // the margin delta), or the top-k entries: elements >= a lower bound
+        // of the slice's k-th largest (the k-th largest lane max over the
+        // unpenalised groups, its key cut to 16 bits); the publish ranks them
+        float t;
+        if (stoch) {
+            const double delta = (double)P.temperature *
+                                 (-(double)__builtin_amdgcn_logf(P.min_p) * 0.6931471805599453 * (1.0 + 1e-6) + 1e-3);
+            const double thr = (double)ms - delta;
+            t = (float)thr;
+            if ((double)t > thr) t = next_down(t);
+        } else {
             uint32_t k4[kSsWaves];
 #pragma unroll
             for (int c = 0; c < kSsWaves; ++c) k4[c] = fkey(sm.lmaxp[lane + c * kWave]) >> 16;
             t = key_to_f(max(wave_kth_largest4_16(k4, P.top_k) << 16, 0x007fffffu));
         }
-        if ((stoch || topk) && lpm >= t) {
+        if (lpm >= t) {
 #pragma unroll
             for (int j = 0; j < NG; ++j) {
-                if (gm[j] >= t) {
+                if (!((hb >> j) & 1u) && gm[j] >= t) {   // (t may be -inf)
 #pragma unroll
                     for (int k = 0; k < G; ++k) {
                         const int q = j * G + k;
-                        const uint32_t e = eid(q);
-                        if (v[q] >= t && e < hi) {
+                        if (v[q] >= t && eid(q) < hi) {
                             const uint32_t s = atomicAdd(&sm.nwin, 1u);
-                            if (s < kWinLds) sm.wk[s] = rank_key(v[q], e);
+                            if (s < kWinLds) { sm.wk[s] = rank_key(v[q], eid(q)); sm.wr[s] = v[q]; }
                         }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < XR; ++r) {
+#pragma unroll
+            for (int k = 0; k < G; ++k) {
+                if (xp[r][k] >= t && xe[r] + k < hi) {
+                    const uint32_t s = atomicAdd(&sm.nwin, 1u);
+                    if (s < kWinLds) {
+                        sm.wk[s] = rank_key(xp[r][k], xe[r] + k);
+                        sm.wr[s] = sm.xv[((uint32_t)wv * XQ + (uint32_t)r * kWave + (uint32_t)lane) * G + k];
                     }
                 }
             }
@@ -543,64 +723,68 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
     // entries (wave 2), all plain stores for row_fin ----
     const bool wins = stoch || topk;
     if (wv == 0) {
-        const bool lw = lane < kSsWaves;
-        const int wl0 = lw ? lane : 0;
+        const bool lw = lane < (int)kXParts;
+        const int wl = lw ? lane : 0;
         // the slice's raw max and the raw sum against it: each wave's partial
         // rescaled by 2^((Mw - Ms) L) in f32 (relative 2^-22: ample for the
         // logprob tolerance), summed in wave order in f64
-        const float mwr = lw ? sm.mraw[wl0] : NEG;
+        const bool lr = lane < kSsWaves;
+        const float mwr = lr ? sm.mraw[lr ? lane : 0] : NEG;
         const float Ms = wave_max(mwr);
-        const float tw = lw && want_lp && mwr != NEG ? sm.sraw[wl0] * fast_exp2((mwr - Ms) * kLog2E) : 0.0f;
+        const float tw = lr && want_lp && mwr != NEG ? sm.sraw[lr ? lane : 0] * fast_exp2((mwr - Ms) * kLog2E) : 0.0f;
         double tq[kSsWaves];
 #pragma unroll
         for (int w = 0; w < kSsWaves; ++w) tq[w] = (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(tw), w));
         const double ses = ((tq[0] + tq[1]) + tq[2]) + tq[3];
-        float ma = lw ? sm.mpen[wl0] : NEG;
-        uint32_t ia = lw && mode == kModeGreedy ? sm.ipen[wl0] : kNoIdx;
-        float ra = lw && mode == kModeGreedy ? sm.rpen[wl0] : 0.0f;
-        float mm = lw && mode == kModeGreedy ? sm.mmsk[wl0] : NEG;
-        uint32_t im = lw && mode == kModeGreedy ? sm.imsk[wl0] : kNoIdx;
-        float rm = lw && mode == kModeGreedy ? sm.rmsk[wl0] : 0.0f;
-        uint32_t na = 0;
+        float ma = lw ? sm.pmax[wl] : NEG;
+        uint32_t ia = kNoIdx, im = kNoIdx, na = 0;
+        float ra = 0.0f, mm = NEG, rm = 0.0f;
         double bk = 0.0, be = 0.0;
         if (stoch) {
-            // bulk: each wave's partial rescaled to the slice max ms by
-            // 2^((mw - ms) kk) in f32, summed in f64; its bound: f32 exp2 and
+            // bulk: each partial rescaled to the slice max ms by
+            // 2^((ref - ms) kk) in f32, summed in f64; its bound: f32 exp2 and
             // the per-lane and cross-lane f32 sums within 2^-19 of the bulk,
             // the rescale's argument and exp2 within (|dw| + 1) 2^-22, and the
             // offsets' roundings within 2^-22 sum c|t| (the entropy bound over
             // the slice's terms relative to ms; the terms within rounding of
-            // their wave's max through the largest |max kk|)
-            const float inv_t = fdiv(1.0f, P.temperature);
-            const float kk = fmul(inv_t, kLog2E);
-            const float dw = lw && ma != NEG ? (ma - ms) * kk : 0.0f;
-            const float part = lw && ma != NEG ? sm.bulk[wl0] * fast_exp2(dw) : 0.0f;
+            // their reference through the largest |ref kk|)
+            const float ref = lw ? sm.bref[wl] : NEG;
+            const float part0 = lw ? sm.bulk[wl] : 0.0f;
+            const float dw = ref != NEG && part0 > 0.0f ? (ref - ms) * kk : 0.0f;
+            const float part = ref != NEG && part0 > 0.0f ? part0 * fast_exp2(dw) : 0.0f;
             const float errw = part * (fabsf(dw) + 1.0f) * 0x1p-22f;
-            double pw[kSsWaves], ew = 0.0;
+            double pw[kXParts], ew = 0.0;
             float mabs = fabsf(ms);
 #pragma unroll
-            for (int w = 0; w < kSsWaves; ++w) {
+            for (int w = 0; w < (int)kXParts; ++w) {
                 pw[w] = (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), w));
                 ew += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(errw), w));
-                const float mw_ = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ma), w));
-                mabs = mw_ != NEG ? fmaxf(mabs, fabsf(mw_)) : mabs;
+                const float rw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ref), w));
+                mabs = rw != NEG ? fmaxf(mabs, fabsf(rw)) : mabs;
             }
-            bk = ((pw[0] + pw[1]) + pw[2]) + pw[3];
+            bk = (((pw[0] + pw[1]) + (pw[2] + pw[3])) + ((pw[4] + pw[5]) + (pw[6] + pw[7])));
             be = ent_bound(bk * (1.0 + 0x1p-18), len, mabs * kk) * 0x1p-22 + bk * 0x1p-19 + ew +
                  (double)len * 0x1p-120;
             ma = ms;
-            ia = kNoIdx;
-        } else {
-            const uint32_t ia0 = ia, im0 = im;
+        } else if (greedy) {
+            ia = lw ? sm.pidx[wl] : kNoIdx;
+            ra = lw ? sm.praw[wl] : 0.0f;
+            const uint32_t ia0 = ia;
             wave_argmax(ma, ia);
             const uint64_t oa = ballot(lw && ia0 == ia && ia < V);
             ra = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ra), oa ? __builtin_ctzll(oa) : 0));
             if (mrow) {
+                mm = lw ? sm.mmax[wl] : NEG;
+                im = lw ? sm.midx[wl] : kNoIdx;
+                rm = lw ? sm.mrw[wl] : 0.0f;
+                const uint32_t im0 = im;
                 wave_argmax(mm, im);
                 const uint64_t om = ballot(lw && im0 == im && im < V);
                 rm = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), om ? __builtin_ctzll(om) : 0));
-                na = wave_sum_u(lw ? sm.nall[wl0] : 0u);
+                na = wave_sum_u(lr ? sm.nall[lane] : 0u);
             }
+        } else {
+            ma = ms;
         }
         const uint32_t nts = min(ntop, len);
         uint64_t hw = 0;
@@ -632,7 +816,7 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
     } else if (wv == 2) {
         // header word 0 (raw slice max, entry count, flags) and the window /
         // top-k entries: the first kWinCap by rank, ascending, each with its
-        // raw logit (the value itself unless penalised)
+        // raw logit
         const uint32_t nwr = wins ? sm.nwin : 0u;
         const uint32_t nwl = min(nwr, kWinLds);
         if (nwl) {
@@ -643,16 +827,16 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
             for (int c = 0; c < 4; ++c) {
                 const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
                 if (e < nwl && rk[c] < kWinCap) {
-                    const uint32_t id = rank_idx(k[c]);
-                    const uint32_t kr = __float_as_uint(rank_val(k[c])) ^ (hany ? sm.tab[id - lo] : 0u);
                     myrec[rec::kWin + rk[c]] = k[c];
-                    myrec[rec::kWinRaw + rk[c]] = (uint64_t)kr;
+                    myrec[rec::kWinRaw + rk[c]] = (uint64_t)__float_as_uint(sm.wr[e]);
                 }
             }
         }
         const uint32_t nts = min(ntop, len);
         const uint32_t fl = (nwr > kWinCap ? rec::kFlagWinTrunc : 0u) | (nwr > kWinLds ? rec::kFlagWinLost : 0u) |
-                            (nts && sm.ncand > kCandCap ? rec::kFlagCandOverflow : 0u);
+                            (nts && sm.ncand > kCandCap ? rec::kFlagCandOverflow : 0u) |
+                            (sm.nxw[0] > XQ || sm.nxw[1] > XQ || sm.nxw[2] > XQ || sm.nxw[3] > XQ
+                                 ? rec::kFlagPenOverflow : 0u);
         const float Ms = fmaxf(fmaxf(sm.mraw[0], sm.mraw[1]), fmaxf(sm.mraw[2], sm.mraw[3]));
         if (lane == 0)
             myrec[0] = (uint64_t)__float_as_uint(Ms) | ((uint64_t)min(nwr, kWinCap) << 32) | ((uint64_t)fl << 48);
@@ -684,17 +868,20 @@ struct FinSmem {
     uint32_t tk_ns[kSsMaxSlices];                    // top-k rows: entries of each slice's list,
     uint32_t tk_cs[kSsMaxSlices], tk_base[kSsMaxSlices];   // its candidates (keys <= U), their offset
     uint32_t tk_ke, tk_nc;
+    uint32_t tn_ns[kSsMaxSlices];                    // top-n list lengths (logprobs)
     SampleArgs args;   // the kernel arguments (exact_row reads them from here)
 };
 
 constexpr uint32_t kSpecWin = 4;    // window entries fetched per slice per round
 
-// Raw log-normaliser over the slices and the k-way merge of their top-n lists
-// (logprobs_from, sampling.cpp:150-190). Returns true when a slice's
-// candidate list overflowed.
-__device__ __forceinline__ bool fin_logprobs(const SampleArgs& a, const uint64_t (&hd)[rec::kHdr],
-                                             const uint64_t (&tk)[kTopMax], uint32_t S, uint32_t row, uint32_t ntop,
-                                             FinSmem& sm) {
+// Raw log-normaliser over the slices (logprobs_from, sampling.cpp:150-190),
+// and the slices' top-n lists staged in LDS for fin_topn_merge. The
+// normaliser goes through f32 exp2 / log2 against the row max, each slice's
+// term within a few ulp and the f64 sum of at most 32 of them: well inside
+// the logprob tolerance of the outputs (which are f32). Returns true when a
+// slice's candidate list overflowed.
+__device__ __forceinline__ bool fin_logz(const uint64_t (&hd)[rec::kHdr], const uint64_t (&tk)[kTopMax], uint32_t S,
+                                         uint32_t ntop, FinSmem& sm) {
     const int lane = lane_id();
     const bool mine = (uint32_t)lane < S;
     const float NEG = -__builtin_huge_valf();
@@ -704,8 +891,9 @@ __device__ __forceinline__ bool fin_logprobs(const SampleArgs& a, const uint64_t
     const double s_raw = mine ? bits_d(h1) : 0.0;
     const uint32_t nts = mine ? (uint32_t)(h4 >> 32) : 0u;
     const float M = wave_max(m_raw);
-    const double z = wave_sum(mine && m_raw != NEG ? s_raw * exp_f64((double)m_raw - (double)M) : 0.0);
-    const double log_z = log_f64(z) + (double)M;
+    const double term = mine && m_raw != NEG ? s_raw * (double)fast_exp2((m_raw - M) * kLog2E) : 0.0;
+    const double z = wave_sum(term);   // in [1, V]
+    const double log_z = (double)__builtin_amdgcn_logf((float)z) * 0.6931471805599453 + (double)M;
     if (lane == 0) sm.log_z = log_z;
     if (ntop == 0) return false;
     if (ballot(mine && (flags & rec::kFlagCandOverflow))) return true;
@@ -713,7 +901,18 @@ __device__ __forceinline__ bool fin_logprobs(const SampleArgs& a, const uint64_t
     for (int j = 0; j < (int)kTopMax; ++j) {
         if (mine && (uint32_t)j < ntop) sm.u.f.top[lane * kTopMax + j] = (uint32_t)j < nts ? tk[j] : ~0ull;
     }
-    wave_sync();
+    if (lane < (int)kSsMaxSlices) sm.tn_ns[lane] = nts;
+    return false;
+}
+
+// The k-way merge of the slices' top-n lists staged by fin_logz, and the
+// row's top-n outputs (logprobs_from, sampling.cpp:171-190).
+__device__ __forceinline__ void fin_topn_merge(const SampleArgs& a, uint32_t S, uint32_t row, uint32_t ntop,
+                                               FinSmem& sm) {
+    const int lane = lane_id();
+    const bool mine = (uint32_t)lane < S;
+    const uint32_t nts = mine ? sm.tn_ns[lane] : 0u;
+    const double log_z = sm.log_z;
     // merge on the value half of the rank keys; among equal values the lowest
     // lane holds the lowest index (slices are in index order)
     uint32_t p = 0;
@@ -733,7 +932,6 @@ __device__ __forceinline__ bool fin_logprobs(const SampleArgs& a, const uint64_t
         a.top_ids[(uint64_t)row * a.n_top + lane] = (int32_t)rank_idx(myk);
         a.top_lp[(uint64_t)row * a.n_top + lane] = (float)((double)rank_val(myk) - log_z);
     }
-    return false;
 }
 
 // The sampling normaliser: slice bulks rescaled to the row max, with the
@@ -1151,7 +1349,8 @@ __global__ __launch_bounds__(kFinThreads) void row_fin(const lcs_params* params,
     PROF_AT(kProfFin + row, 0 + tid_x() / 64);
     if (row >= rows || (flags & LCS_WRITE_PENALIZED) != 0) return;
     const uint32_t tid = tid_x();
-    const int lane = lane_id(), wv = (int)(tid / kWave);
+    const int lane = lane_id();
+    const int wv = __builtin_amdgcn_readfirstlane((int)(tid / kWave));   // (an SGPR: wave-uniform branches)
     const uint32_t S = slices;
     const uint64_t* recs = srecs + (uint64_t)row * kSsMaxSlices * rec::kWords64;
     const uint64_t* my = recs + ((uint32_t)lane < S ? lane : 0) * rec::kWords64;   // lane s: slice s
@@ -1176,8 +1375,15 @@ __global__ __launch_bounds__(kFinThreads) void row_fin(const lcs_params* params,
     const bool masked = a.mask != nullptr && (a.has_mask == nullptr || scalar_load_u8(a.has_mask + row) != 0);
     const uint32_t mode = row_mode(P, masked, vocab);
     if (mode != kModeGreedy && mode != kModeWindow && mode != kModeTopK) return;
-    // a slice that could not apply the penalties sends the row to the exact
-    // path (every wave holds the same headers, so the test is uniform)
+    // a slice that could not take all its penalised groups as exceptions, or
+    // that left the row out, sends the row to the exact path (every wave
+    // holds the same headers, so the test is uniform)
+    if (ballot((uint32_t)lane < S && ((uint32_t)(hd[0] >> 48) & (rec::kFlagPenOverflow | rec::kFlagExact)) != 0u)) {
+        stage_args(&sm.args, a);
+        exact_row<kFinThreads, kFbBins, kFbCap, kFbHistCap, G>(sm.args, row, sm.u.ex);
+        return;
+    }
+    PROF_AT(kProfFin + row, 20 + wv);
     const bool stoch = mode == kModeWindow, topk = mode == kModeTopK;
     const float inv_t = stoch || topk ? fdiv(1.0f, P.temperature) : 1.0f;
     const double u = (stoch || topk) && wv == 0 ? a.u[row] : 0.0;
@@ -1189,7 +1395,7 @@ __global__ __launch_bounds__(kFinThreads) void row_fin(const lcs_params* params,
         if (wv == 0) {
             fb = fin_topk_lengths(S, P.top_k, sm, hd[0]);
         } else if (wv == 1) {
-            if (want_lp) fb = fin_logprobs(a, hd, tk, S, row, ntop, sm);
+            if (want_lp) fb = fin_logz(hd, tk, S, ntop, sm);
         } else {
             fin_fetch_topk(recs, S, P.top_k, sm);
         }
@@ -1200,7 +1406,7 @@ __global__ __launch_bounds__(kFinThreads) void row_fin(const lcs_params* params,
         if (stoch) fb = fin_window(hd, wk, wr, my, S, P, sm, inv_t);
         else fin_greedy(a, hd, S, vocab, row, masked, sm);
     } else if (wv == 1) {
-        if (want_lp) fb = fin_logprobs(a, hd, tk, S, row, ntop, sm);
+        if (want_lp) fb = fin_logz(hd, tk, S, ntop, sm);
     } else if (wv == 2) {
         if (stoch) fin_norm(hd, S, sm, inv_t);
     }
@@ -1223,6 +1429,8 @@ __global__ __launch_bounds__(kFinThreads) void row_fin(const lcs_params* params,
             }
             a.chosen_lp[row] = inr ? (float)((double)raw - sm.log_z) : 0.0f;
         };
+        // the top-n outputs (wave 1) beside the decision (wave 0)
+        if (wv == 1 && ntop) fin_topn_merge(a, S, row, ntop, sm);
         if (!(stoch || topk)) {
             if (tid == 0 && want_lp) write_lp();
             return;
@@ -1246,14 +1454,28 @@ __global__ __launch_bounds__(kFinThreads) void row_fin(const lcs_params* params,
 }
 
 // Host launchers (the kernels stay private to this translation unit).
+template <int G, uint32_t MS>
+static void launch_stats(const SampleArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL((slice_stats<G, MS>), dim3(a.rows * a.ss_slices), dim3(kSsThreads), 0, st, a.logits,
+                       a.row_stride, a.rows, a.ss_slices, a.ss_len, a.vocab, a.flags, a.all_sliced, a);
+}
+template <int G>
+static void launch_stats_for(const SampleArgs& a, hipStream_t st) {
+    // an instantiation per single row mode (the host saw every sliced row
+    // take it) and one for any mix
+    switch (a.ss_modes) {
+        case kModeWindow: launch_stats<G, kModeWindow>(a, st); break;
+        case kModeGreedy: launch_stats<G, kModeGreedy>(a, st); break;
+        case kModeTopK: launch_stats<G, kModeTopK>(a, st); break;
+        default: launch_stats<G, kModeGreedy | kModeWindow | kModeTopK>(a, st); break;
+    }
+}
+
 hipError_t launch_slice(const SampleArgs& a, hipStream_t st) {
-    const dim3 grid(a.rows * a.ss_slices), block(kSsThreads);
     if (a.dtype == LCS_BF16) {
-        hipLaunchKernelGGL(slice_stats<8>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.ss_slices,
-                           a.ss_len, a.vocab, a.flags, a.all_sliced, a);
+        launch_stats_for<8>(a, st);
     } else {
-        hipLaunchKernelGGL(slice_stats<4>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.ss_slices,
-                           a.ss_len, a.vocab, a.flags, a.all_sliced, a);
+        launch_stats_for<4>(a, st);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
