@@ -101,14 +101,20 @@ __device__ __forceinline__ double ent_bound(double S, uint32_t n, float mk) {
 // ============================================================ slice_stats ==
 constexpr uint32_t kXElems = 2048;   // logits of penalised groups a slice takes as exceptions
                                      // (a quarter per wave)
+constexpr uint32_t kHistPass = 3 * kSsWaves * kWave * 4;   // history ids a pass over the window reads
 constexpr uint32_t kXParts = 2 * kSsWaves;   // partials: one per wave over its unpenalised groups,
                                              // one per wave over the exceptions it resolved
 
 struct SsSmem {
     uint32_t cnt[kSsMax / 2];   // history counts, 16 bits per slice position
     uint32_t gbit[kSsThreads];  // bit j of word t: group j * kSsThreads + t holds a counted position
-    float xv[kXElems];          // exception groups' raw logits
-    uint16_t xg[kXElems / 4];   // their group index in the slice
+    union {
+        struct {
+            float xv[kXElems];          // exception groups' raw logits
+            uint16_t xg[kXElems / 4];   // their group index in the slice
+        } x;
+        uint16_t hq[kSsWaves * kHistPass / kSsWaves];   // in-slice history positions, a part per wave
+    } u;
     float lmax[kSsThreads];     // raw lane maxima (top-n bound)
     float lmaxp[kSsThreads];    // lane maxima over unpenalised groups (top-k bound)
     float mraw[kSsWaves];       // the waves' raw maxima and raw sums against them
@@ -163,8 +169,8 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
     constexpr int NG = kSsElems / G;      // groups per thread
     constexpr int NE = kSsElems;
     constexpr uint32_t XQ = kXElems / G / kSsWaves;   // exception groups a wave holds
-    constexpr int XR = (int)(XQ / kWave);             // exception groups per lane
-    static_assert(XQ % kWave == 0 && XQ * kSsWaves <= kXElems / 4, "exception list sizes");
+    constexpr int XE = (int)(XQ * G / kWave);         // exception elements per lane
+    static_assert(XQ * G % kWave == 0 && XQ * kSsWaves <= kXElems / 4, "exception list sizes");
     __shared__ SsSmem sm;
     const uint32_t tid = tid_x();
     const int lane = lane_id();
@@ -253,6 +259,7 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
     const uint32_t zpad = lo == 0u && hany ? 4u * kWave * ((nq + kWave - 1) / kWave) - (hend - w0) : 0u;
     constexpr int HC = 3;                      // groups per lane per pass (3072 ids a pass)
     constexpr uint32_t kPass = HC * kSsWaves * kWave;
+    static_assert(kPass * 4 == kHistPass, "history pass size");
     int4 hq[HC];
     const __amdgpu_buffer_rsrc_t hrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int32_t*>(a.hist_ids + w0), 0, (int)((hend - w0) * 4u), 0x00020000);
@@ -265,8 +272,11 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
         }
     };
     auto hcount = [&](uint32_t base) {
-        // ids outside the slice are skipped
+        // the in-slice positions of this wave's ids are queued (ballot
+        // compaction), then counted a position per lane
         const uint32_t gl = hs - w0;   // words of the first group before the window
+        uint16_t* qw = sm.u.hq + (uint32_t)wv * (kHistPass / kSsWaves);
+        uint32_t nqw = 0;              // (wave-uniform)
 #pragma unroll
         for (int c = 0; c < HC; ++c) {
             const uint32_t gi = hgroup(base, c);
@@ -279,13 +289,25 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
                     const uint32_t d = (uint32_t)h4[m] - lo;   // d < len: in the slice (hence < V)
-                    if (d < len) {
-                        atomicAdd(&sm.cnt[d >> 1], 1u << ((d & 1u) << 4));
-                        atomicOr(&sm.gbit[(d / G) % NT], 1u << (d / (G * NT)));
-                    }
+                    const bool in = d < len;
+                    const uint64_t mm = ballot(in);
+                    if (in)
+                        qw[__builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mm, nqw))] =
+                            (uint16_t)d;
+                    nqw += (uint32_t)__builtin_popcountll(mm);
                 }
             }
         }
+        wave_sync();
+        for (uint32_t e0 = 0; e0 < nqw; e0 += kWave) {
+            const uint32_t e = e0 + (uint32_t)lane;
+            if (e < nqw) {
+                const uint32_t d = qw[e];
+                atomicAdd(&sm.cnt[d >> 1], 1u << ((d & 1u) << 4));
+                atomicOr(&sm.gbit[(d / G) % NT], 1u << (d / (G * NT)));
+            }
+        }
+        wave_sync();   // (the queue is reused by the next pass)
     };
     if (hany) {
         hload(0);
@@ -492,10 +514,10 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
                                              (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
                 if (s < XQ) {
                     const uint32_t sw = (uint32_t)wv * XQ + s;
-                    sm.xg[sw] = (uint16_t)(j * NT + tid);
+                    sm.u.x.xg[sw] = (uint16_t)(j * NT + tid);
 #pragma unroll
                     for (int k = 0; k < G; k += 4)
-                        *reinterpret_cast<float4*>(&sm.xv[sw * G + k]) =
+                        *reinterpret_cast<float4*>(&sm.u.x.xv[sw * G + k]) =
                             make_float4(v[j * G + k], v[j * G + k + 1], v[j * G + k + 2], v[j * G + k + 3]);
                 }
             }
@@ -508,61 +530,49 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
     }
     PROF_W0(wg_x(), 4);
 
-    // ---- exceptions: a group per lane, penalties as apply_penalties
-    // (sampling.cpp:34-39: once per distinct id, with its count) ----
+    // ---- exceptions: an element per lane, in rounds of 64 over this wave's
+    // list; penalties as apply_penalties (sampling.cpp:34-39: once per
+    // distinct id, with its count) ----
     const uint32_t nx = min(nxa, XQ);
-    float xp[XR][G];    // penalised logits of this lane's exceptions (-inf: none)
-    uint32_t xe[XR];    // their first id (none: past any slice)
+    const uint32_t nxe = nx * G;                 // elements of the list
+    const uint32_t xbase = (uint32_t)wv * XQ * G;   // this wave's part of xv
+    float xp[XE];       // penalised logits (-inf: none, or past the slice)
+    uint32_t xi[XE];    // their ids
 #pragma unroll
-    for (int r = 0; r < XR; ++r) {
-        xe[r] = 0xfffffff0u;
-#pragma unroll
-        for (int k = 0; k < G; ++k) xp[r][k] = NEG;
-    }
-    if (nx) {
+    for (int r = 0; r < XE; ++r) { xp[r] = NEG; xi[r] = kNoIdx; }
+    const int xw = kSsWaves + wv;
+    if (nxe) {
         const double inv_rp = 1.0 / (double)P.repeat_penalty;
 #pragma unroll
-        for (int r = 0; r < XR; ++r) {
-            const uint32_t s = (uint32_t)r * kWave + (uint32_t)lane;
-            if (s < nx) {
-                const uint32_t gx = sm.xg[(uint32_t)wv * XQ + s];
-                xe[r] = lo + gx * G;
-                uint32_t cw[G / 2];
-#pragma unroll
-                for (int k = 0; k < G / 2; ++k) cw[k] = sm.cnt[gx * (G / 2) + k];
-                if (gx == 0u) cw[0] -= zpad;   // (the padding's zeros, all at position 0)
-#pragma unroll
-                for (int k = 0; k < G; ++k) {
-                    const float x = sm.xv[((uint32_t)wv * XQ + s) * G + k];
-                    const uint32_t c = (cw[k / 2] >> ((k & 1) * 16)) & 0xffffu;
-                    xp[r][k] = c ? penalize_fast(x, c, P, inv_rp) : x;
+        for (int r = 0; r < XE; ++r) {
+            if ((uint32_t)r * kWave < nxe) {   // (wave-uniform)
+                const uint32_t e = (uint32_t)r * kWave + (uint32_t)lane;
+                if (e < nxe) {
+                    const uint32_t pos = (uint32_t)sm.u.x.xg[(uint32_t)wv * XQ + e / G] * G + e % G;
+                    uint32_t c = (sm.cnt[pos >> 1] >> ((pos & 1u) << 4)) & 0xffffu;
+                    if (pos == 0u) c -= zpad;   // (the padding's zeros, all at position 0)
+                    const float x = sm.u.x.xv[xbase + e];
+                    xp[r] = c ? penalize_fast(x, c, P, inv_rp) : x;
+                    xi[r] = lo + pos;
                 }
             }
         }
         // this wave's exception partial: max, first index, bulk
         float xm = NEG;
 #pragma unroll
-        for (int r = 0; r < XR; ++r)
-#pragma unroll
-            for (int k = 0; k < G; ++k) xm = fmaxf(xm, xp[r][k]);
+        for (int r = 0; r < XE; ++r) xm = fmaxf(xm, xp[r]);
         const float xmw = wave_max(xm);
-        const int xw = kSsWaves + wv;
         if (greedy) {
-            // (the lowest id among this lane's exceptions at the max: the
-            // list holds groups in no particular order)
             uint32_t bi = kNoIdx, mi = kNoIdx;
             float br = 0.0f, mv = NEG, mrr = 0.0f;
             if (xm == xmw) {
 #pragma unroll
-                for (int r = 0; r < XR; ++r)
-#pragma unroll
-                    for (int k = 0; k < G; ++k) {
-                        const uint32_t e = xe[r] + k;
-                        if (xp[r][k] == xmw && e < hi && e < bi) {
-                            bi = e;
-                            br = sm.xv[((uint32_t)wv * XQ + (uint32_t)r * kWave + (uint32_t)lane) * G + k];
-                        }
+                for (int r = 0; r < XE; ++r) {
+                    if (xp[r] == xmw && xi[r] < hi && xi[r] < bi) {
+                        bi = xi[r];
+                        br = sm.u.x.xv[xbase + (uint32_t)r * kWave + (uint32_t)lane];
                     }
+                }
             }
             const uint32_t bi0 = bi;
             bi = wave_min_u(bi);
@@ -570,28 +580,22 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
             br = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(br), ob ? __builtin_ctzll(ob) : 0));
             if (mrow) {
                 float xmm = NEG;
-                bool al[XR][G];
+                bool al[XE];
 #pragma unroll
-                for (int r = 0; r < XR; ++r)
-#pragma unroll
-                    for (int k = 0; k < G; ++k) {
-                        const uint32_t e = xe[r] + k;
-                        const uint32_t ec = e < hi ? e : lo;   // (an id of the row)
-                        al[r][k] = e < hi && ((mrow[ec >> 5] >> (ec & 31u)) & 1u);
-                        xmm = al[r][k] ? fmaxf(xmm, xp[r][k]) : xmm;
-                    }
+                for (int r = 0; r < XE; ++r) {
+                    const uint32_t ec = xi[r] < hi ? xi[r] : lo;   // (an id of the row)
+                    al[r] = xi[r] < hi && ((mrow[ec >> 5] >> (ec & 31u)) & 1u);
+                    xmm = al[r] ? fmaxf(xmm, xp[r]) : xmm;
+                }
                 mv = wave_max(xmm);
                 if (xmm == mv) {
 #pragma unroll
-                    for (int r = 0; r < XR; ++r)
-#pragma unroll
-                        for (int k = 0; k < G; ++k) {
-                            const uint32_t e = xe[r] + k;
-                            if (al[r][k] && xp[r][k] == mv && e < mi) {
-                                mi = e;
-                                mrr = sm.xv[((uint32_t)wv * XQ + (uint32_t)r * kWave + (uint32_t)lane) * G + k];
-                            }
+                    for (int r = 0; r < XE; ++r) {
+                        if (al[r] && xp[r] == mv && xi[r] < mi) {
+                            mi = xi[r];
+                            mrr = sm.u.x.xv[xbase + (uint32_t)r * kWave + (uint32_t)lane];
                         }
+                    }
                 }
                 const uint32_t mi0 = mi;
                 mi = wave_min_u(mi);
@@ -607,15 +611,14 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
             if (stoch && xmw != NEG) {
                 const float bb = -xmw * kk;
 #pragma unroll
-                for (int r = 0; r < XR; ++r)
-#pragma unroll
-                    for (int k = 0; k < G; ++k) xs += fast_exp2(fmaf(xp[r][k], kk, bb));
+                for (int r = 0; r < XE; ++r) {
+                    if ((uint32_t)r * kWave < nxe) xs += fast_exp2(fmaf(xp[r], kk, bb));
+                }
                 xs = wave_sum_f(xs) * fast_exp2(-fmaf(xmw, kk, bb));
             }
             if (lane == 0) { sm.pmax[xw] = xmw; sm.bref[xw] = xmw; sm.bulk[xw] = xs; }
         }
     } else if (lane == 0) {
-        const int xw = kSsWaves + wv;
         sm.pmax[xw] = NEG; sm.pidx[xw] = kNoIdx; sm.praw[xw] = 0.0f;
         sm.mmax[xw] = NEG; sm.midx[xw] = kNoIdx; sm.mrw[xw] = 0.0f;
         sm.bref[xw] = NEG; sm.bulk[xw] = 0.0f;
@@ -702,15 +705,12 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
             }
         }
 #pragma unroll
-        for (int r = 0; r < XR; ++r) {
-#pragma unroll
-            for (int k = 0; k < G; ++k) {
-                if (xp[r][k] >= t && xe[r] + k < hi) {
-                    const uint32_t s = atomicAdd(&sm.nwin, 1u);
-                    if (s < kWinLds) {
-                        sm.wk[s] = rank_key(xp[r][k], xe[r] + k);
-                        sm.wr[s] = sm.xv[((uint32_t)wv * XQ + (uint32_t)r * kWave + (uint32_t)lane) * G + k];
-                    }
+        for (int r = 0; r < XE; ++r) {
+            if (xp[r] >= t && xi[r] < hi) {
+                const uint32_t s = atomicAdd(&sm.nwin, 1u);
+                if (s < kWinLds) {
+                    sm.wk[s] = rank_key(xp[r], xi[r]);
+                    sm.wr[s] = sm.u.x.xv[xbase + (uint32_t)r * kWave + (uint32_t)lane];
                 }
             }
         }
@@ -719,8 +719,8 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
     __syncthreads();   // B3
     PROF_W0(wg_x(), 8);
 
-    // ---- publish: header (waves 0 and 2), top-n (wave 1), window / top-k
-    // entries (wave 2), all plain stores for row_fin ----
+    // ---- publish: header (waves 0, 2 and 3), top-n (wave 1), window /
+    // top-k entries (wave 2), all plain stores for row_fin ----
     const bool wins = stoch || topk;
     if (wv == 0) {
         const bool lw = lane < (int)kXParts;
@@ -739,32 +739,7 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
         float ma = lw ? sm.pmax[wl] : NEG;
         uint32_t ia = kNoIdx, im = kNoIdx, na = 0;
         float ra = 0.0f, mm = NEG, rm = 0.0f;
-        double bk = 0.0, be = 0.0;
         if (stoch) {
-            // bulk: each partial rescaled to the slice max ms by
-            // 2^((ref - ms) kk) in f32, summed in f64; its bound: f32 exp2 and
-            // the per-lane and cross-lane f32 sums within 2^-19 of the bulk,
-            // the rescale's argument and exp2 within (|dw| + 1) 2^-22, and the
-            // offsets' roundings within 2^-22 sum c|t| (the entropy bound over
-            // the slice's terms relative to ms; the terms within rounding of
-            // their reference through the largest |ref kk|)
-            const float ref = lw ? sm.bref[wl] : NEG;
-            const float part0 = lw ? sm.bulk[wl] : 0.0f;
-            const float dw = ref != NEG && part0 > 0.0f ? (ref - ms) * kk : 0.0f;
-            const float part = ref != NEG && part0 > 0.0f ? part0 * fast_exp2(dw) : 0.0f;
-            const float errw = part * (fabsf(dw) + 1.0f) * 0x1p-22f;
-            double pw[kXParts], ew = 0.0;
-            float mabs = fabsf(ms);
-#pragma unroll
-            for (int w = 0; w < (int)kXParts; ++w) {
-                pw[w] = (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), w));
-                ew += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(errw), w));
-                const float rw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ref), w));
-                mabs = rw != NEG ? fmaxf(mabs, fabsf(rw)) : mabs;
-            }
-            bk = (((pw[0] + pw[1]) + (pw[2] + pw[3])) + ((pw[4] + pw[5]) + (pw[6] + pw[7])));
-            be = ent_bound(bk * (1.0 + 0x1p-18), len, mabs * kk) * 0x1p-22 + bk * 0x1p-19 + ew +
-                 (double)len * 0x1p-120;
             ma = ms;
         } else if (greedy) {
             ia = lw ? sm.pidx[wl] : kNoIdx;
@@ -793,12 +768,42 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
             case 2: hw = pack2(__float_as_uint(ma), ia); break;
             case 3: hw = pack2(__float_as_uint(mm), im); break;
             case 4: hw = pack2(na, nts); break;
-            case 5: hw = d_bits(bk); break;
-            case 6: hw = d_bits(be); break;
             case 7: hw = pack2(__float_as_uint(ra), __float_as_uint(rm)); break;
             default: break;
         }
-        if (lane >= 1 && lane < (int)rec::kHdr) myrec[lane] = hw;   // (word 0: wave 2)
+        if ((lane >= 1 && lane <= 4) || lane == 7) myrec[lane] = hw;   // (word 0: wave 2; 5, 6: wave 3)
+    } else if (wv == 3) {
+        // header words 5 and 6 (window rows): the bulk, each partial rescaled
+        // to the slice max ms by 2^((ref - ms) kk) in f32, summed in f64; its
+        // bound: f32 exp2 and the per-lane and cross-lane f32 sums within
+        // 2^-19 of the bulk, the rescale's argument and exp2 within
+        // (|dw| + 1) 2^-22, and the offsets' roundings within 2^-22 sum c|t|
+        // (the entropy bound over the slice's terms relative to ms; the terms
+        // within rounding of their reference through the largest |ref kk|)
+        double bk = 0.0, be = 0.0;
+        if (stoch) {
+            const bool lw = lane < (int)kXParts;
+            const int wl = lw ? lane : 0;
+            const float ref = lw ? sm.bref[wl] : NEG;
+            const float part0 = lw ? sm.bulk[wl] : 0.0f;
+            const float dw = ref != NEG && part0 > 0.0f ? (ref - ms) * kk : 0.0f;
+            const float part = ref != NEG && part0 > 0.0f ? part0 * fast_exp2(dw) : 0.0f;
+            const float errw = part * (fabsf(dw) + 1.0f) * 0x1p-22f;
+            double pw[kXParts], ew = 0.0;
+            float mabs = fabsf(ms);
+#pragma unroll
+            for (int w = 0; w < (int)kXParts; ++w) {
+                pw[w] = (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), w));
+                ew += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(errw), w));
+                const float rw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ref), w));
+                mabs = rw != NEG ? fmaxf(mabs, fabsf(rw)) : mabs;
+            }
+            bk = (((pw[0] + pw[1]) + (pw[2] + pw[3])) + ((pw[4] + pw[5]) + (pw[6] + pw[7])));
+            be = ent_bound(bk * (1.0 + 0x1p-18), len, mabs * kk) * 0x1p-22 + bk * 0x1p-19 + ew +
+                 (double)len * 0x1p-120;
+        }
+        if (lane == 5) myrec[5] = d_bits(bk);
+        if (lane == 6) myrec[6] = d_bits(be);
     } else if (wv == 1) {
         // slice top-n: rank the candidates, store the first nts
         const uint32_t nts = min(ntop, len);
@@ -862,7 +867,7 @@ struct FinSmem {
         } f;
         ExactSmem<kFinThreads, kFbBins, kFbCap, kFbHistCap> ex;
     } u;
-    double log_z, fin_S, fin_rel;
+    double log_z, fin_S, fin_rel, fin_invS;
     float chosen_raw, fin_maxl;
     uint32_t fin_fb, fin_L0;
     uint32_t tk_ns[kSsMaxSlices];                    // top-k rows: entries of each slice's list,
@@ -872,7 +877,7 @@ struct FinSmem {
     SampleArgs args;   // the kernel arguments (exact_row reads them from here)
 };
 
-constexpr uint32_t kSpecWin = 4;    // window entries fetched per slice per round
+constexpr uint32_t kSpecWin = 8;    // window entries fetched per slice per round
 
 // Raw log-normaliser over the slices (logprobs_from, sampling.cpp:150-190),
 // and the slices' top-n lists staged in LDS for fin_topn_merge. The
@@ -953,6 +958,7 @@ __device__ __forceinline__ void fin_norm(const uint64_t (&hd)[rec::kHdr], uint32
     const double eps = wave_sum(es * (berr + fabs(d_s) * bulk * 0x1p-22));
     if (lane == 0) {
         sm.fin_S = Sf;
+        sm.fin_invS = 1.0 / Sf;
         sm.fin_rel = 2.0 * eps / Sf + 0x1p-50;
     }
 }
@@ -1236,6 +1242,7 @@ __device__ __forceinline__ void fin_merge_topk(uint32_t S, uint32_t K, FinSmem& 
     const double Sf = wave_sum(w);
     if (lane == 0) {
         sm.fin_S = Sf;
+        sm.fin_invS = 1.0 / Sf;
         sm.fin_rel = 0x1p-45;   // tree vs sequential summation of at most 64 terms
         sm.fin_L0 = Ke;
         sm.fin_maxl = maxl;
@@ -1254,7 +1261,7 @@ __device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, Fi
     bool uncertain = false;
     uint32_t keep_p = 0xffffffffu, keep = 0;
     const double tp = (double)P.top_p;
-    const double inv_S = 1.0 / Sf;
+    const double inv_S = sm.fin_invS;   // (1 / S, computed beside S)
     const double mp = (double)P.min_p;
     // one inclusive scan of the weights per 64 entries serves the top-p sums
     // (cum = W / S), the kept mass and the draw
