@@ -149,6 +149,19 @@ void lcs_destroy(lcs_ctx* ctx);
  * (sampling.hpp:70-89) as called from engine.cpp:430-442. */
 int lcs_sample(lcs_ctx* ctx, const lcs_batch* batch, const lcs_out* out, void* stream);
 
+/* lcs_sample without a context, allocating nothing: for callers that cannot
+ * call hipMalloc (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid it). No counterpart in the reference. Runs on the current
+ * device with the same batch, outputs and results as lcs_sample; its
+ * workspace is one static device array per GPU (about 20 MiB, held until the
+ * process ends), sized for rows <= 32, any vocabulary up to 262144, n_top <=
+ * 20 and penalty windows up to 8192. More rows return LCS_ERR_CAPACITY with
+ * nothing launched. Calls share that array: calls that overlap on one GPU
+ * (two streams, or two threads) race and must be serialised by the caller.
+ * Its status bits are not readable (lcs_get_status needs a context); failures
+ * are reported by lcs_last_error(NULL). */
+int lcs_sample_noalloc(const lcs_batch* batch, const lcs_out* out, void* stream);
+
 /* Batched greedy verify: replaces the argmax loop of engine.cpp:357-396 and
  * adds the draft logprob (sampling.cpp:241-261 with chosen = draft). */
 int lcs_verify(lcs_ctx* ctx, const lcs_verify_batch* batch, const lcs_verify_out* out,
@@ -165,7 +178,8 @@ enum lcs_status_bits {
     LCS_STATUS_SELECT = 2u          /* a selection bin exceeded its capacity */
 };
 
-/* Message of the last failure on ctx (or of the last lcs_create when NULL). */
+/* Message of the last failure on ctx (or, when NULL, of the last lcs_create
+ * or lcs_sample_noalloc on this thread). */
 const char* lcs_last_error(const lcs_ctx* ctx);
 
 #ifdef __cplusplus

@@ -1,10 +1,12 @@
 // C ABI of the sampler (include/locus_sampler.h): context workspace,
 // argument validation and kernel dispatch. No call after lcs_create
-// allocates device memory.
+// allocates device memory; lcs_sample_noalloc allocates none at all (its
+// workspace is a static device array, see below).
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -165,8 +167,21 @@ const char* lcs_last_error(const lcs_ctx* c) {
     return c ? c->err.c_str() : g_create_error.c_str();
 }
 
-int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
-    if (!c) return LCS_ERR_INVALID_ARG;
+}  // extern "C"
+
+namespace {
+
+// Clears n words (a kernel rather than a memset, so that a captured graph
+// holds no memset node).
+__global__ void clear_words(uint32_t* w, uint32_t n) {
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) w[i] = 0u;
+}
+
+// lcs_sample on the workspace of c (a context, or the no-alloc entry's view
+// of its static array); validation first, nothing is launched on an error.
+// clear_n > 0: the first clear_n words at c->counters (the arrival counters
+// and the status word) are zeroed ahead of the kernels.
+int sample_impl(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream, uint32_t clear_n) {
     if (!b || !o) return fail(c, LCS_ERR_INVALID_ARG, "null batch or output");
     if (b->rows == 0) return LCS_OK;
     if (b->dtype != LCS_F32 && b->dtype != LCS_BF16) return fail(c, LCS_ERR_INVALID_ARG, "dtype");
@@ -268,10 +283,114 @@ int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
     DeviceGuard g(c->device);
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t e = hipSuccess;
+    if (clear_n) {
+        hipLaunchKernelGGL(clear_words, dim3(1), dim3(256), 0, st, c->counters, clear_n);
+        if ((e = hipGetLastError()) != hipSuccess) return hip_fail(c, e, "workspace clear launch");
+    }
     if (any_general && (e = lcs::launch_general(a, st)) != hipSuccess) return hip_fail(c, e, "general kernel launch");
     if (any_slice && (e = lcs::launch_slice(a, st)) != hipSuccess) return hip_fail(c, e, "slice kernel launch");
     if (any_nucleus && (e = lcs::launch_nucleus(a, st)) != hipSuccess) return hip_fail(c, e, "nucleus kernels launch");
     return LCS_OK;
+}
+
+// ---- the no-alloc entry point's workspace ----
+// One static device array per GPU (each device holds its own copy, at its own
+// address), carved like a context for kNoAllocRows rows, the largest vocabulary
+// and the general path's largest penalty window. Host code never uses the
+// array's name as an address: the per-device address comes from
+// hipGetSymbolAddress on the first call on that device.
+constexpr uint32_t kNoAllocRows = 32;
+constexpr uint32_t kNoAllocHist = lcs::kGenHistCap;
+constexpr size_t kAlign = 256;
+constexpr size_t up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
+constexpr size_t kSzRecs = up((size_t)kNoAllocRows * lcs::kMaxSlices * lcs::rec::kWords * 4);
+constexpr size_t kSzSrecs = up((size_t)kNoAllocRows * lcs::kSsMaxSlices * lcs::rec::kWords64 * 8);
+constexpr size_t kSzCounters = up((size_t)kNoAllocRows * 4);
+constexpr size_t kSzStatus = up(4);
+constexpr size_t kSzD = up((size_t)kNoAllocRows * kNoAllocHist * 4);
+constexpr size_t kSzNrow = up((size_t)kNoAllocRows * sizeof(lcs::NucRow));
+constexpr size_t kNhElems = (size_t)kNoAllocRows * lcs::kMaxSlices * lcs::kNucBins;
+constexpr size_t kSzNhCnt = up(kNhElems * 4);
+constexpr size_t kSzNhMass = up(kNhElems * 8);
+constexpr size_t kSzNlist = up((size_t)kNoAllocRows * lcs::kNucList * 8);
+constexpr size_t kOffRecs = 0;
+constexpr size_t kOffSrecs = kOffRecs + kSzRecs;
+constexpr size_t kOffCounters = kOffSrecs + kSzSrecs;   // counters, then status: cleared by each call
+constexpr size_t kOffStatus = kOffCounters + kSzCounters;
+constexpr size_t kOffDIds = kOffStatus + kSzStatus;
+constexpr size_t kOffDRaw = kOffDIds + kSzD;
+constexpr size_t kOffDPen = kOffDRaw + kSzD;
+constexpr size_t kOffNrow = kOffDPen + kSzD;
+constexpr size_t kOffNhCnt = kOffNrow + kSzNrow;
+constexpr size_t kOffNhMass = kOffNhCnt + kSzNhCnt;
+constexpr size_t kOffNlist = kOffNhMass + kSzNhMass;
+constexpr size_t kScratchBytes = kOffNlist + kSzNlist;   // about 20 MiB
+static_assert(kScratchBytes <= (24u << 20), "the no-alloc workspace stays modest");
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_ptr[kMaxDevices] = {};   // per device: the address of `scratch`
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+extern "C" {
+
+int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
+    if (!c) return LCS_ERR_INVALID_ARG;
+    return sample_impl(c, b, o, stream, 0u);
+}
+
+int lcs_sample_noalloc(const lcs_batch* b, const lcs_out* o, void* stream) {
+    g_create_error.clear();
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices || !is_gfx950(dev)) {
+        g_create_error = "lcs_sample_noalloc: the current device is not a usable gfx950";
+        return LCS_ERR_NO_DEVICE;
+    }
+    unsigned char* base = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        if (!g_scratch_ptr[dev]) {
+            void* p = nullptr;
+            const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !p) {
+                g_create_error = std::string("lcs_sample_noalloc: hipGetSymbolAddress: ") + hipGetErrorString(e);
+                return LCS_ERR_HIP;
+            }
+            g_scratch_ptr[dev] = static_cast<unsigned char*>(p);
+        }
+        base = g_scratch_ptr[dev];
+    }
+    // a context view of the static workspace: nothing here allocates device
+    // memory (the string stays empty unless a call fails)
+    lcs_ctx w;
+    w.device = dev;
+    w.max_rows = kNoAllocRows;
+    w.max_vocab = lcs::kMaxVocab;
+    w.max_hist = kNoAllocHist;
+    w.max_top = lcs::kTopMax;
+    w.max_slices = lcs::kMaxSlices;
+    w.recs = reinterpret_cast<uint32_t*>(base + kOffRecs);
+    w.srecs = reinterpret_cast<uint64_t*>(base + kOffSrecs);
+    w.counters = reinterpret_cast<uint32_t*>(base + kOffCounters);
+    w.status = reinterpret_cast<uint32_t*>(base + kOffStatus);
+    w.d_ids = reinterpret_cast<uint32_t*>(base + kOffDIds);
+    w.d_raw = reinterpret_cast<float*>(base + kOffDRaw);
+    w.d_pen = reinterpret_cast<float*>(base + kOffDPen);
+    w.nrow = reinterpret_cast<lcs::NucRow*>(base + kOffNrow);
+    w.nh_cnt = reinterpret_cast<uint32_t*>(base + kOffNhCnt);
+    w.nh_mass = reinterpret_cast<double*>(base + kOffNhMass);
+    w.nlist = reinterpret_cast<uint64_t*>(base + kOffNlist);
+    if (b && o && b->rows > kNoAllocRows) {
+        g_create_error = "lcs_sample_noalloc: rows above " + std::to_string(kNoAllocRows);
+        return LCS_ERR_CAPACITY;
+    }
+    // the counters and the status word (adjacent) start at zero on every call
+    const int rc = sample_impl(&w, b, o, stream, (uint32_t)((kSzCounters + kSzStatus) / 4));
+    if (rc != LCS_OK) g_create_error = "lcs_sample_noalloc: " + w.err;
+    return rc;
 }
 
 int lcs_verify(lcs_ctx* c, const lcs_verify_batch* b, const lcs_verify_out* o, void* stream) {

@@ -72,6 +72,8 @@ def lib():
         L.lcs_destroy.argtypes = [_P]
         L.lcs_sample.restype = C.c_int
         L.lcs_sample.argtypes = [_P, C.POINTER(_Batch), C.POINTER(_Out), _P]
+        L.lcs_sample_noalloc.restype = C.c_int
+        L.lcs_sample_noalloc.argtypes = [C.POINTER(_Batch), C.POINTER(_Out), _P]
         L.lcs_verify.restype = C.c_int
         L.lcs_verify.argtypes = [_P, C.POINTER(_VBatch), C.POINTER(_VOut), _P]
         L.lcs_last_error.restype = C.c_char_p
@@ -244,9 +246,10 @@ class Sampler:
 
     def sample_dev(self, d, out, n_top: int | None = None, want_lp: bool | None = None,
                    has_mask=None, flags_extra: int = 0, use_host_params: bool = True, stream=None,
-                   lp_ids=None):
+                   lp_ids=None, noalloc: bool = False):
         """Enqueues lcs_sample on device buffers from upload()/alloc_out();
-        `lp_ids` (device int32 per row) makes chosen_lp report those ids."""
+        `lp_ids` (device int32 per row) makes chosen_lp report those ids;
+        `noalloc` calls lcs_sample_noalloc (no context) instead."""
         w = d["w"]
         want_lp = w.want_logprobs if want_lp is None else want_lp
         n_top = w.n_top if n_top is None else n_top
@@ -274,8 +277,13 @@ class Sampler:
         o.top_lp = _dptr(out.get("top_lp"))
         o.diag = _dptr(out.get("diag"))
         self._keep = (ph, b, o, lp_ids)
-        self._check(lib().lcs_sample(self.ctx, C.byref(b), C.byref(o),
-                                     _stream_handle(self.torch, stream)))
+        sh = _stream_handle(self.torch, stream)
+        if noalloc:
+            rc = lib().lcs_sample_noalloc(C.byref(b), C.byref(o), sh)
+            if rc != LCS_OK:
+                raise SamplerError(f"lcs error {rc}: {lib().lcs_last_error(None).decode()}")
+            return
+        self._check(lib().lcs_sample(self.ctx, C.byref(b), C.byref(o), sh))
 
     def sample(self, w, **kw):
         """Uploads a Workload, samples it, and returns host numpy results."""
