@@ -131,6 +131,19 @@ def copy_ceiling(mib: int = 1024, reps: int = 10) -> float:
     return 2 * n * 4 / sec / 1e9
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the CPU baseline."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(name, budget_s=10.0, threads=1):
     """The reference sampler (compiled from the reference's own sources,
     oracle/_ref) on this host, rows in order as the reference engine samples
@@ -157,9 +170,89 @@ def cpu_baseline(name, budget_s=10.0, threads=1):
             break
     if w.n_seq:
         kind = "port"  # the reference has no batched verify; the oracle restates its loop
-    return {"value": rows_done / el, "unit": "rows/s", "cores": threads, "kind": kind,
+    return {"value": rows_done / el, "unit": "rows/s", "cores": threads, "kind": kind, "cpu": cpu_model(),
             "sample": f"{reps} x {name} batch ({w.rows} rows, V={w.vocab}), "
                       f"{'single thread' if threads == 1 else f'{threads} threads'}, {el:.1f} s"}
+
+
+def synthetic_pieces(V: int = 128256, seed: int = 20261204) -> list[bytes]:
+    """A tokenizer-like piece table of V entries: the 256 single bytes, then
+    pieces of 1-10 bytes mixing word fragments (with and without a leading
+    space), digits, JSON punctuation, quotes and escapes."""
+    rng = np.random.default_rng(seed)
+    pieces = [bytes([b]) for b in range(256)]
+    letters = np.frombuffer(b"etaoinshrdlucmfwypvbgkjqxz", dtype=np.uint8)
+    punct = [b"{", b"}", b"[", b"]", b":", b",", b'"', b'":', b'",', b'{"', b'"}', b"\\n", b"\\\"", b" {", b"},"]
+    while len(pieces) < V:
+        k = rng.random()
+        if k < 0.70:
+            n = int(rng.integers(1, 9))
+            w = bytes(letters[np.minimum(rng.geometric(0.12, n) - 1, 25)])
+            pieces.append((b" " if rng.random() < 0.5 else b"") + w)
+        elif k < 0.82:
+            pieces.append(str(int(rng.integers(0, 10 ** int(rng.integers(1, 4))))).encode())
+        elif k < 0.95:
+            pieces.append(punct[int(rng.integers(0, len(punct)))] + (b" " if rng.random() < 0.3 else b""))
+        else:
+            pieces.append(bytes(rng.integers(32, 127, int(rng.integers(1, 6))).astype(np.uint8)))
+    return pieces[:V]
+
+
+def mask_bench(budget_s: float = 5.0):
+    """Host cost of one JSON allow-mask at V=128256 (the per-step host work of a
+    constrained row, server.cpp:160-171): the reference's per-token allows()
+    loop (a grammar copy fed each piece; the compiled reference when its build
+    is present, else the oracle's restatement) against JsonMaskBuilder (trie
+    walk), cold (a state not seen before) and cached (a state seen before),
+    over the grammar states of a JSON document fed byte by byte."""
+    from locus_amd import host_lib as H
+    from oracle import pyoracle as O
+    V = 128256
+    pieces = synthetic_pieces(V)
+    doc = b'{"name": "sampler", "ids": [12, 7, 3005], "ok": true, "nested": {"x": -1.5e3, "s": "a\\"b"}}'
+    blob = np.frombuffer(b"".join(pieces), dtype=np.uint8).copy()
+    off = np.zeros(len(pieces) + 1, dtype=np.uint64)
+    off[1:] = np.cumsum([len(p) for p in pieces])
+    out = np.zeros((V + 31) // 32, dtype=np.uint32)
+    kind = "reference" if O.ref_available() else "port"
+    # (1) per-token allows(): one mask per prefix length until the budget ends
+    t0, n_ref = time.perf_counter(), 0
+    for i in range(len(doc)):
+        pre = np.frombuffer(doc[:i], dtype=np.uint8).copy() if i else np.zeros(1, dtype=np.uint8)
+        if kind == "reference":
+            rc = O.ref().ref_json_mask(pre.ctypes.data, i, blob.ctypes.data, off.ctypes.data, V, V, out.ctypes.data)
+            assert rc == 0
+        else:
+            g = O.OracleJson()
+            assert g.feed_all(doc[:i])
+            g.mask(pieces, V)
+        n_ref += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    ref_ms = (time.perf_counter() - t0) / n_ref * 1e3
+    # (2) the trie builder: every state of the document, cold, then again cached
+    mb = H.MaskBuilder(pieces, cache_entries=4096)
+    states = []
+    g = H.JsonGrammar()
+    for i in range(len(doc) + 1):
+        states.append(g.clone())
+        if i < len(doc):
+            assert g.feed(doc[i])
+    cold, warm = [], []
+    for st in states:
+        _, m0 = mb.cache_stats()
+        t0 = time.perf_counter()
+        mb.build(st, V)
+        dt = time.perf_counter() - t0
+        (cold if mb.cache_stats()[1] > m0 else warm).append(dt)
+    for st in states:   # every state again: all from the cache
+        t0 = time.perf_counter()
+        mb.build(st, V)
+        warm.append(time.perf_counter() - t0)
+    return {"vocab": V, "states": len(states), "distinct_states": len(cold),
+            "allows_loop_ms": ref_ms, "allows_loop_kind": kind, "allows_loop_masks": n_ref,
+            "trie_cold_ms": float(np.mean(cold)) * 1e3, "trie_cold_max_ms": float(np.max(cold)) * 1e3,
+            "trie_cached_ms": float(np.mean(warm)) * 1e3, "cpu": cpu_model()}
 
 
 def copy_calibration(mib: int, reps: int = 20):
@@ -285,7 +378,12 @@ def main():
                     help="threads of the all-cores CPU baseline (0: skip it)")
     ap.add_argument("--kernel", default="slice_stats|row_fin")
     ap.add_argument("--copy-bytes", type=int, default=256 << 20)
+    ap.add_argument("--mask-bench", action="store_true",
+                    help="only time the host JSON allow-mask at V=128256 (CPU)")
     args = ap.parse_args()
+    if args.mask_bench:
+        print(json.dumps(mask_bench()))
+        return
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace, args.kernel))
         return

@@ -6,6 +6,19 @@
  * stay on the device, and then applies sample_from's per-request effects in
  * row order.
  *
+ * sample_step() is a template over the caller's request type, so the engine
+ * passes its own locus::engine::Request (engine.hpp:43-63) and its own
+ * LogprobEntry (engine.hpp:36-40); this header defines neither. A request
+ * type needs the members sample_from reads and advances:
+ *   sampling       model::SamplingParams
+ *   rng            std::mt19937_64
+ *   generated      std::vector<tok::TokenId>
+ *   constraint     model::TokenConstraint*, or a smart pointer to one
+ *   logprobs_opt   {bool enabled; uint32_t top;}
+ *   logprobs       a vector of {token, logprob, top (vector<model::TokenLogprob>)}
+ * locus::sampler::SampleRequest below is such a type for callers without an
+ * engine (tests, benches).
+ *
  * Per request, and with the same results as sample_from:
  * - one mt19937_64 output is drawn when temperature > 0, none when greedy;
  * - the id is sampled with penalties over `generated` and the constraint;
@@ -22,8 +35,10 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <memory>
 #include <random>
 #include <span>
+#include <type_traits>
 #include <vector>
 
 #include "locus/model/sampling.hpp"
@@ -31,28 +46,14 @@
 
 namespace locus::engine {
 
-/** Per-request logprobs configuration (engine.hpp:29-33). */
-struct LogprobsOpt {
-    bool enabled = false;
-    std::uint32_t top = 0;
-};
-
-/** Chosen token's log-probability plus its top alternatives (engine.hpp:36-40). */
-struct LogprobEntry {
-    tok::TokenId token = 0;
-    float logprob = 0.0f;
-    std::vector<model::TokenLogprob> top;
-};
-
-/** The sampling state of one request (the fields of Request,
- * engine.hpp:43-63, that sample_from reads and advances). */
-struct SampleRequest {
-    model::SamplingParams sampling;
-    std::mt19937_64 rng;
-    std::vector<tok::TokenId> generated;
-    model::TokenConstraint* constraint = nullptr;   // borrowed; may be null
-    LogprobsOpt logprobs_opt;
-    std::vector<LogprobEntry> logprobs;
+/** What sample_from reads from one request (borrowed for one step). */
+struct SampleRow {
+    const model::SamplingParams* sampling = nullptr;
+    std::mt19937_64* rng = nullptr;
+    const std::vector<tok::TokenId>* generated = nullptr;
+    const model::TokenConstraint* constraint = nullptr;   // may be null
+    bool logprobs = false;                                // logprobs_opt.enabled
+    std::uint32_t top = 0;                                // logprobs_opt.top
 };
 
 class BatchSampler {
@@ -71,15 +72,97 @@ class BatchSampler {
      * elements (device memory, f32 or bf16, not modified). Enqueued on
      * `stream` (the sampler's own stream when null), then synchronised; the
      * requests are updated in row order and the sampled ids returned.
-     * Throws std::invalid_argument on sizes beyond the constructor's limits
-     * and std::runtime_error on device errors.
+     * Every row's limits are checked before any rng is advanced: on
+     * std::invalid_argument (sizes beyond the constructor's limits) no
+     * request has changed. std::runtime_error on device errors.
      */
+    template <class Request>
     std::vector<tok::TokenId> sample_step(const void* logits, lcs_dtype dtype, std::uint32_t row_stride,
-                                          std::span<SampleRequest* const> reqs, hipStream_t stream = nullptr);
+                                          std::span<Request* const> reqs, hipStream_t stream = nullptr) {
+        std::vector<SampleRow> rows;
+        rows.reserve(reqs.size());
+        for (Request* q : reqs) {
+            rows.push_back(SampleRow{&q->sampling, &q->rng, &q->generated, constraint_of(q->constraint),
+                                     q->logprobs_opt.enabled, q->logprobs_opt.top});
+        }
+        run(logits, dtype, row_stride, rows, stream);
+        // sample_from's effects, in row order (engine.cpp:430-442)
+        std::vector<tok::TokenId> out(reqs.size());
+        for (std::size_t r = 0; r < reqs.size(); ++r) {
+            Request& q = *reqs[r];
+            const tok::TokenId next = id(r);
+            out[r] = next;
+            if (auto* c = constraint_of(q.constraint)) c->commit(next);
+            q.generated.push_back(next);
+            if (q.logprobs_opt.enabled) {
+                typename decltype(q.logprobs)::value_type e;
+                e.token = next;
+                e.logprob = logprob(r);
+                const std::span<const std::int32_t> ti = top_ids(r);
+                const std::span<const float> tl = top_logprobs(r);
+                e.top.reserve(ti.size());
+                for (std::size_t j = 0; j < ti.size(); ++j) e.top.push_back(model::TokenLogprob{ti[j], tl[j]});
+                q.logprobs.push_back(std::move(e));
+            }
+        }
+        return out;
+    }
+
+    template <class Request>
+    std::vector<tok::TokenId> sample_step(const void* logits, lcs_dtype dtype, std::uint32_t row_stride,
+                                          const std::vector<Request*>& reqs, hipStream_t stream = nullptr) {
+        return sample_step(logits, dtype, row_stride, std::span<Request* const>(reqs.data(), reqs.size()),
+                           stream);
+    }
+
+    /** The step without the request updates: validates every row, draws the
+     * uniforms, samples, and leaves the results readable through id(),
+     * logprob(), top_ids() and top_logprobs() until the next run. */
+    void run(const void* logits, lcs_dtype dtype, std::uint32_t row_stride, std::span<const SampleRow> rows,
+             hipStream_t stream = nullptr);
+    tok::TokenId id(std::size_t row) const;
+    float logprob(std::size_t row) const;
+    /** min(logprobs top, V) alternatives of a row with logprobs enabled. */
+    std::span<const std::int32_t> top_ids(std::size_t row) const;
+    std::span<const float> top_logprobs(std::size_t row) const;
 
   private:
+    template <class P>
+    static model::TokenConstraint* constraint_of(const P& p) {
+        if constexpr (std::is_pointer_v<P>)
+            return p;
+        else
+            return p.get();
+    }
     struct Buffers;
     Buffers* b_;
 };
 
 }  // namespace locus::engine
+
+namespace locus::sampler {
+
+/** Request types for callers without an engine; field for field the sampling
+ * part of engine.hpp:29-63 (a distinct namespace, so a translation unit may
+ * include both this header and the engine's). */
+struct LogprobsOpt {
+    bool enabled = false;
+    std::uint32_t top = 0;
+};
+
+struct LogprobEntry {
+    tok::TokenId token = 0;
+    float logprob = 0.0f;
+    std::vector<model::TokenLogprob> top;
+};
+
+struct SampleRequest {
+    model::SamplingParams sampling;
+    std::mt19937_64 rng;
+    std::vector<tok::TokenId> generated;
+    model::TokenConstraint* constraint = nullptr;   // borrowed; may be null
+    LogprobsOpt logprobs_opt;
+    std::vector<LogprobEntry> logprobs;
+};
+
+}  // namespace locus::sampler

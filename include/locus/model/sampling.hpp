@@ -1,8 +1,10 @@
 /*
  * Host C++ API of the MI355X sampler, keeping the reference's sampler
- * interface (src/locus/model/sampling.hpp:13-89 and argmax of
- * src/locus/model/llama.hpp:352) so existing callers and tests compile
- * unchanged. Every computation runs on the GPU through the C ABI of
+ * interface (src/locus/model/sampling.hpp:13-89) so existing callers and tests
+ * compile unchanged. argmax (llama.hpp:352, llama.cpp:1237-1245) is not part
+ * of it: the reference's own definition keeps serving host spans, and the
+ * device greedy path is sample() with temperature <= 0 (or lcs_sample /
+ * lcs_verify on device-resident rows). Every computation runs on the GPU through the C ABI of
  * locus_sampler.h; there is no CPU fallback: without a usable gfx950 device
  * the calls throw std::runtime_error.
  *
@@ -80,8 +82,5 @@ tok::TokenId sample(std::span<float> logits, const SamplingParams& p,
  */
 void logprobs_from(std::span<const float> logits, tok::TokenId chosen, std::uint32_t n_top,
                    float& chosen_lp, std::vector<TokenLogprob>& top);
-
-/** argmax of llama.hpp:352: first index of the maximum. */
-tok::TokenId argmax(std::span<const float> logits);
 
 }  // namespace locus::model

@@ -3,7 +3,7 @@
  *
  * The drop-in boundary for the reference's per-step sampling path. The
  * reference has no C ABI for it: its callers use free C++ functions
- * (src/locus/model/sampling.hpp:70-89, llama.hpp:351-352) on host spans, one
+ * (src/locus/model/sampling.hpp:70-89, llama.hpp:352) on host spans, one
  * row at a time (engine.cpp:423-450, engine.cpp:357-396). This ABI is what a
  * backend-registry entry (registry.hpp:107-131) or any FFI binds: plain
  * pointers and sizes, no exceptions, stream-ordered and asynchronous.
@@ -88,7 +88,7 @@ typedef struct lcs_batch {
 } lcs_batch;
 
 /* Per-row diagnostics (optional output): the survivor set of the reference's
- * candidate walk (sampling.cpp:160-238). */
+ * candidate walk (sampling.cpp:70-147). */
 typedef struct lcs_row_diag {
     uint32_t n_cand;    /* candidates after the constraint */
     uint32_t keep;      /* survivors after top-k, top-p, min-p (0 for greedy) */
@@ -163,7 +163,7 @@ int lcs_sample(lcs_ctx* ctx, const lcs_batch* batch, const lcs_out* out, void* s
 int lcs_sample_noalloc(const lcs_batch* batch, const lcs_out* out, void* stream);
 
 /* Batched greedy verify: replaces the argmax loop of engine.cpp:357-396 and
- * adds the draft logprob (sampling.cpp:241-261 with chosen = draft). */
+ * adds the draft logprob (sampling.cpp:150-170 with chosen = draft). */
 int lcs_verify(lcs_ctx* ctx, const lcs_verify_batch* batch, const lcs_verify_out* out,
                void* stream);
 

@@ -7,6 +7,11 @@ with the tree to the GPU box).
   sampling API over the C ABI, JSON grammar and mask builder, n-gram draft,
   backend registry) and its C ABI (include/locus_host.h).
 * tests/cpp/test_host - the host layer's C++ test program.
+
+build_sanitized() (called by the CPU tests, not by build_all) compiles the
+host layer, its test program and a driver of the CPU oracle with g++ under
+AddressSanitizer and UndefinedBehaviorSanitizer, into _build/asan/. It builds
+no device code: the host layer's HIP calls go to the unmodified runtime.
 """
 from __future__ import annotations
 
@@ -87,6 +92,39 @@ def build_host(jobs: int = 4) -> str:
           "-Wl,-rpath," + os.path.relpath(HERE, os.path.dirname(TEST_HOST)).join(["$ORIGIN/", ""])])
     os.replace(TEST_HOST + ".tmp", TEST_HOST)
     return HOST_SO
+
+
+ASAN_DIR = os.path.join(BUILD, "asan")
+SAN_FLAGS = ["-std=c++20", "-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
+             "-fno-sanitize-recover=undefined"]
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+
+
+def build_sanitized(jobs: int = 4) -> dict:
+    """Host layer + tests/cpp/test_host, and tests/cpp/oracle_asan over
+    oracle/oracle.cpp, built with g++ -fsanitize=address,undefined. Returns
+    the two programs' paths."""
+    os.makedirs(ASAN_DIR, exist_ok=True)
+    hip = ["-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROCM, "include"), "-I" + INCLUDE]
+    objs, cmds = [], []
+    for src in HOST_SOURCES:
+        obj = os.path.join(ASAN_DIR, src.replace(".cpp", ".o"))
+        objs.append(obj)
+        cmds.append(["g++", *SAN_FLAGS, "-fPIC", "-Wall", *hip, "-c", os.path.join(HERE, "host", src), "-o", obj])
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(_run, cmds))
+    so = os.path.join(ASAN_DIR, "liblocus_host_asan.so")
+    rocm_lib = os.path.join(ROCM, "lib")
+    links = ["-L" + HERE, "-llocus_sampler", "-L" + rocm_lib, "-lamdhip64",
+             "-Wl,-rpath," + HERE, "-Wl,-rpath," + rocm_lib]
+    _run(["g++", "-shared", "-fsanitize=address,undefined", "-o", so, *objs, *links])
+    test_host = os.path.join(ASAN_DIR, "test_host_asan")
+    _run(["g++", *SAN_FLAGS, *hip, os.path.join(ROOT, "tests", "cpp", "test_host.cpp"), "-o", test_host,
+          "-L" + ASAN_DIR, "-llocus_host_asan", "-Wl,-rpath," + ASAN_DIR, *links])
+    oracle = os.path.join(ASAN_DIR, "oracle_asan")
+    _run(["g++", *SAN_FLAGS, "-ffp-contract=off", os.path.join(ROOT, "tests", "cpp", "oracle_asan.cpp"),
+          os.path.join(ROOT, "oracle", "oracle.cpp"), "-o", oracle, "-lpthread"])
+    return {"test_host": test_host, "oracle": oracle}
 
 
 def build_all() -> None:

@@ -19,7 +19,7 @@ __device__ __forceinline__ uint32_t wg_x() { return __builtin_amdgcn_workgroup_i
 
 // ---------------------------------------------------------------- keys ----
 // Order-preserving 32-bit key of a float; -0.0 is folded onto +0.0 so the two
-// compare equal, as `a.first > b.first` treats them (sampling.cpp:178-180).
+// compare equal, as `a.first > b.first` treats them (sampling.cpp:87-89).
 __device__ __forceinline__ uint32_t fkey(float v) {
     uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -54,7 +54,7 @@ __device__ __forceinline__ float fmul(float a, float b) { return __fmul_rn(a, b)
 __device__ __forceinline__ float fadd(float a, float b) { return __fadd_rn(a, b); }
 __device__ __forceinline__ float fdiv(float a, float b) { return __fdiv_rn(a, b); }
 
-// Penalised logit exactly as apply_penalties (sampling.cpp:124-130).
+// Penalised logit exactly as apply_penalties (sampling.cpp:33-39).
 __device__ __forceinline__ float penalize(float l, uint32_t count, const lcs_params& p) {
     if (p.repeat_penalty != 1.0f) {
         l = l > 0.0f ? fdiv(l, p.repeat_penalty) : fmul(l, p.repeat_penalty);
@@ -85,13 +85,13 @@ __device__ __forceinline__ bool penalties_active(const lcs_params& p) {
     return !(p.repeat_penalty == 1.0f && p.frequency_penalty == 0.0f &&
              p.presence_penalty == 0.0f);
 }
-// Tempered offset (cand_i - maxl) * inv_t in float (sampling.cpp:197-198).
+// Tempered offset (cand_i - maxl) * inv_t in float (sampling.cpp:106-107).
 __device__ __forceinline__ float tempered(float p, float maxl, float inv_t) {
     return fmul(fsub(p, maxl), inv_t);
 }
 
 // exp(x) in f64, inline and branch-free, for the weights exp((double)x) of
-// tempered offsets x <= 0 (sampling.cpp:104-105). x = n ln2 + r with
+// tempered offsets x <= 0 (sampling.cpp:105-108). x = n ln2 + r with
 // n = rint(x / ln2), |r| <= ln2 / 2; ln2 is split Cody-Waite style into a
 // 32-bit head (n * head exact for |n| < 2^21) and a tail. exp(r) is the
 // Taylor polynomial of degree 13 (truncation below 5e-18 relative) in Horner

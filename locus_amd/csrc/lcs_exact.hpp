@@ -163,7 +163,7 @@ __device__ void bitonic_sort_u32(uint32_t* a, uint32_t n) {
 }
 
 // Writes the logprob outputs of a row: chosen lp and top-n from sorted rank
-// keys (logprobs_from, sampling.cpp:241-281).
+// keys (logprobs_from, sampling.cpp:150-190).
 __device__ __forceinline__ void write_logprobs(const SampleArgs& a, uint32_t row, int32_t id,
                                                float chosen_raw, double log_z,
                                                const uint64_t* top, uint32_t ntop) {
@@ -353,7 +353,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
     }
 
     if (greedy) {
-        // argmax over penalised candidates (sampling.cpp:143-158)
+        // argmax over penalised candidates (sampling.cpp:52-67)
         if (tid == 0) {
             const int32_t id = (int32_t)maxi;
             a.ids[row] = id;
@@ -845,7 +845,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
                     kept_sum = sm.out_kept_sum;
                 }
             }
-            // draw (sampling.cpp:226-238)
+            // draw (sampling.cpp:135-147)
             const double r0 = a.u[row] * (kept_sum - 0.0) + 0.0;
             const ExactSeg rr = region_for_mass(r0, keep);
             ExactSeg need[2] = {rr, region_for_count(keep - 1)};

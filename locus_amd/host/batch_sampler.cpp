@@ -36,6 +36,11 @@ T* host_alloc(std::size_t n) {
 struct BatchSampler::Buffers {
     int device = 0;
     std::uint32_t max_rows = 0, vocab = 0, max_hist = 0, max_top = 0, words = 0;
+    // the last run: its rows, alternatives per row in the output arrays, and
+    // per row whether logprobs were asked for and how many alternatives
+    std::uint32_t rows = 0, n_top = 0;
+    std::vector<std::uint8_t> lp_on;
+    std::vector<std::uint32_t> want_h;
     lcs_ctx* ctx = nullptr;
     hipStream_t own = nullptr;
     // host (pinned)
@@ -89,6 +94,8 @@ BatchSampler::BatchSampler(int device, std::uint32_t max_rows, std::uint32_t voc
     b.max_hist = std::max<std::uint32_t>(max_hist, 1);
     b.max_top = max_top;
     b.words = (vocab + 31u) / 32u;
+    b.lp_on.assign(max_rows, 0);
+    b.want_h.assign(max_rows, 0);
     try {
         check(hipSetDevice(device), "hipSetDevice");
         b.ctx = lcs_create(device, max_rows, vocab, b.max_hist, std::max<std::uint32_t>(max_top, 1));
@@ -128,35 +135,47 @@ BatchSampler::~BatchSampler() {
     delete b_;
 }
 
-std::vector<tok::TokenId> BatchSampler::sample_step(const void* logits, lcs_dtype dtype, std::uint32_t row_stride,
-                                                    std::span<SampleRequest* const> reqs, hipStream_t stream) {
+void BatchSampler::run(const void* logits, lcs_dtype dtype, std::uint32_t row_stride,
+                       std::span<const SampleRow> reqs, hipStream_t stream) {
     Buffers& b = *b_;
     const std::uint32_t rows = static_cast<std::uint32_t>(reqs.size());
-    if (rows == 0) return {};
+    b.rows = 0;
+    b.n_top = 0;
+    if (rows == 0) return;
     if (rows > b.max_rows) throw std::invalid_argument("BatchSampler: more requests than max_rows");
     const std::uint32_t V = b.vocab;
-    // per-request arrays in row order (sample_from's inputs)
+    // every limit first, so that a rejected step leaves every rng untouched
+    std::uint32_t n_top = 0;
     bool any_mask = false, any_lp = false, any_hist = false;
-    std::uint32_t n_top = 0, off = 0;
+    for (const SampleRow& q : reqs) {
+        const std::size_t w = std::min<std::size_t>(q.generated->size(), q.sampling->repeat_last_n);
+        if (w > b.max_hist) throw std::invalid_argument("BatchSampler: penalty window above max_hist");
+        if (q.logprobs) {
+            any_lp = true;
+            n_top = std::max(n_top, std::min(q.top, V));
+        }
+        any_mask = any_mask || q.constraint != nullptr;
+        any_hist = any_hist || w > 0;
+    }
+    if (n_top > b.max_top) throw std::invalid_argument("BatchSampler: logprobs top above max_top");
+    // per-request arrays in row order (sample_from's inputs)
+    std::uint32_t off = 0;
     for (std::uint32_t r = 0; r < rows; ++r) {
-        SampleRequest& q = *reqs[r];
+        const SampleRow& q = reqs[r];
         static_assert(sizeof(model::SamplingParams) == sizeof(lcs_params), "SamplingParams must match lcs_params");
-        std::memcpy(&b.params_h[r], &q.sampling, sizeof(lcs_params));
+        std::memcpy(&b.params_h[r], q.sampling, sizeof(lcs_params));
         // the penalties see the trailing repeat_last_n ids of `generated`
         // (sampling.cpp:22-24): only those travel
-        const std::size_t n = q.generated.size();
-        const std::size_t w = std::min<std::size_t>(n, q.sampling.repeat_last_n);
-        if (w > b.max_hist) throw std::invalid_argument("BatchSampler: penalty window above max_hist");
+        const std::size_t n = q.generated->size();
+        const std::size_t w = std::min<std::size_t>(n, q.sampling->repeat_last_n);
         b.hoff_h[r] = off;
-        std::memcpy(b.hist_h + off, q.generated.data() + (n - w), w * sizeof(std::int32_t));
+        std::memcpy(b.hist_h + off, q.generated->data() + (n - w), w * sizeof(std::int32_t));
         off += static_cast<std::uint32_t>(w);
-        any_hist = any_hist || w > 0;
         // one engine output per stochastic row, none per greedy row (sampling.cpp:139-140)
-        b.u_h[r] = q.sampling.temperature > 0.0f ? std::generate_canonical<double, 53>(q.rng) : 0.0;
+        b.u_h[r] = q.sampling->temperature > 0.0f ? std::generate_canonical<double, 53>(*q.rng) : 0.0;
         // the constraint as allow bits (sampling.cpp:78-81 asks allows() per token)
         b.has_h[r] = q.constraint != nullptr ? 1u : 0u;
         if (q.constraint) {
-            any_mask = true;
             std::uint32_t* m = b.mask_h + (std::size_t)r * b.words;
             if (!q.constraint->allow_mask(V, m)) {
                 std::memset(m, 0, b.words * sizeof(std::uint32_t));
@@ -164,13 +183,10 @@ std::vector<tok::TokenId> BatchSampler::sample_step(const void* logits, lcs_dtyp
                     if (q.constraint->allows(static_cast<tok::TokenId>(t))) m[t >> 5] |= 1u << (t & 31u);
             }
         }
-        if (q.logprobs_opt.enabled) {
-            any_lp = true;
-            n_top = std::max(n_top, std::min(q.logprobs_opt.top, V));
-        }
+        b.lp_on[r] = q.logprobs ? 1u : 0u;
+        b.want_h[r] = q.logprobs ? std::min(q.top, V) : 0u;
     }
     b.hoff_h[rows] = off;
-    if (n_top > b.max_top) throw std::invalid_argument("BatchSampler: logprobs top above max_top");
     hipStream_t st = stream ? stream : b.own;
     check(hipSetDevice(b.device), "hipSetDevice");
     check(hipMemcpyAsync(b.params_d, b.params_h, rows * sizeof(lcs_params), hipMemcpyHostToDevice, st), "copy");
@@ -215,29 +231,38 @@ std::vector<tok::TokenId> BatchSampler::sample_step(const void* logits, lcs_dtyp
         }
     }
     check(hipStreamSynchronize(st), "hipStreamSynchronize");
-    std::uint32_t status = 0;
-    if (lcs_get_status(b.ctx, &status, 1) != LCS_OK || status != 0)
-        throw std::runtime_error("BatchSampler: sampler device status " + std::to_string(status));
-    // sample_from's effects, in row order (engine.cpp:430-442)
-    std::vector<tok::TokenId> out(rows);
+    // A row the kernels could not serve comes back as id -1 (locus_sampler.h),
+    // so the status word is read only then.
     for (std::uint32_t r = 0; r < rows; ++r) {
-        SampleRequest& q = *reqs[r];
-        const tok::TokenId next = b.ids_h[r];
-        out[r] = next;
-        if (q.constraint) q.constraint->commit(next);
-        q.generated.push_back(next);
-        if (q.logprobs_opt.enabled) {
-            LogprobEntry e;
-            e.token = next;
-            e.logprob = b.lp_h[r];
-            const std::uint32_t k = std::min(q.logprobs_opt.top, V);
-            e.top.reserve(k);
-            for (std::uint32_t j = 0; j < k; ++j)
-                e.top.push_back({b.top_ids_h[(std::size_t)r * n_top + j], b.top_lp_h[(std::size_t)r * n_top + j]});
-            q.logprobs.push_back(std::move(e));
+        if (b.ids_h[r] < 0) {
+            std::uint32_t status = 0;
+            (void)lcs_get_status(b.ctx, &status, 1);
+            throw std::runtime_error("BatchSampler: row " + std::to_string(r) + " not sampled (device status " +
+                                     std::to_string(status) + ")");
         }
     }
-    return out;
+    b.rows = rows;
+    b.n_top = n_top;
+}
+
+tok::TokenId BatchSampler::id(std::size_t row) const {
+    if (row >= b_->rows) throw std::out_of_range("BatchSampler: row beyond the last step");
+    return b_->ids_h[row];
+}
+
+float BatchSampler::logprob(std::size_t row) const {
+    if (row >= b_->rows) throw std::out_of_range("BatchSampler: row beyond the last step");
+    return b_->lp_on[row] ? b_->lp_h[row] : 0.0f;
+}
+
+std::span<const std::int32_t> BatchSampler::top_ids(std::size_t row) const {
+    if (row >= b_->rows) throw std::out_of_range("BatchSampler: row beyond the last step");
+    return {b_->top_ids_h + row * b_->n_top, b_->want_h[row]};
+}
+
+std::span<const float> BatchSampler::top_logprobs(std::size_t row) const {
+    if (row >= b_->rows) throw std::out_of_range("BatchSampler: row beyond the last step");
+    return {b_->top_lp_h + row * b_->n_top, b_->want_h[row]};
 }
 
 }  // namespace locus::engine

@@ -18,7 +18,7 @@ bool digit(std::uint8_t b) { return b >= '0' && b <= '9'; }
 bool hex(std::uint8_t b) {
     return digit(b) || (b >= 'a' && b <= 'f') || (b >= 'A' && b <= 'F');
 }
-// bytes allowed after a backslash other than 'u' (grammar.cpp:127-131)
+// bytes allowed after a backslash other than 'u' (grammar.cpp:120-131)
 bool simple_escape(std::uint8_t b) {
     return std::strchr("\"\\/bfnrt", b) != nullptr && b != 0;
 }

@@ -2,7 +2,9 @@
 #include "locus/backend/sampler_registry.hpp"
 
 #include <array>
+#include <atomic>
 #include <cstdlib>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 
@@ -10,33 +12,56 @@ namespace locus::backend {
 
 namespace {
 
+constexpr std::size_t kMaxEntries = 8;
+
 bool hip_usable() {
     int n = 0;
     return lcs_probe(&n) == LCS_OK && n > 0;
 }
 
-const std::array<SamplerBackend, 1>& table() {
-    static const std::array<SamplerBackend, 1> t{{
-        {"hip", "MI355X (gfx950) HIP sampler: penalties, top-k/top-p/min-p, JSON mask, logprobs, verify",
-         hip_usable(), true, SamplerOps{&lcs_sample, &lcs_verify, false}},
-    }};
+// Fixed storage, so that a span handed out before a registration stays valid:
+// entries are written once, then published by the count.
+struct Table {
+    std::array<SamplerBackend, kMaxEntries> e{};
+    std::atomic<std::size_t> n{0};
+    std::mutex m;
+    Table() {
+        SamplerOps ops;
+        ops.sample_batch = &lcs_sample;
+        ops.verify_batch = &lcs_verify;
+        ops.sample = &model::sample;
+        ops.logprobs_from = &model::logprobs_from;
+        ops.mt_safe = true;
+        e[0] = SamplerBackend{"hip",
+                              "MI355X (gfx950) HIP sampler: penalties, top-k/top-p/min-p, JSON mask, logprobs, verify",
+                              hip_usable(), true, ops};
+        n.store(1, std::memory_order_release);
+    }
+};
+
+Table& table() {
+    static Table t;
     return t;
 }
 
 }  // namespace
 
-std::span<const SamplerBackend> sampler_backends() { return table(); }
+std::span<const SamplerBackend> sampler_backends() {
+    Table& t = table();
+    return {t.e.data(), t.n.load(std::memory_order_acquire)};
+}
 
 const SamplerBackend* find_sampler_backend(std::string_view name) {
-    for (const SamplerBackend& b : table())
+    for (const SamplerBackend& b : sampler_backends())
         if (b.name == name) return &b;
     return nullptr;
 }
 
 const SamplerBackend& best_sampler_backend() {
-    for (const SamplerBackend& b : table())
+    for (const SamplerBackend& b : sampler_backends())
         if (b.available && b.selectable) return b;
-    throw std::runtime_error("no usable sampler backend: the HIP sampler needs a gfx950 device");
+    throw std::runtime_error(
+        "no usable sampler backend: the HIP sampler needs a gfx950 device and no fallback is registered");
 }
 
 const SamplerBackend& resolve_sampler_backend(std::string_view choice) {
@@ -48,9 +73,22 @@ const SamplerBackend& resolve_sampler_backend(std::string_view choice) {
     if (name.empty()) return best_sampler_backend();
     const SamplerBackend* b = find_sampler_backend(name);
     if (b == nullptr) throw std::invalid_argument("unknown sampler backend: " + std::string(name));
-    if (!b->available || !b->selectable)
-        throw std::invalid_argument("sampler backend not usable on this machine: " + std::string(name));
+    if (!b->available) throw std::invalid_argument("sampler backend not available on this machine: " + std::string(name));
+    if (!b->selectable)
+        throw std::invalid_argument("sampler backend not selectable: " + std::string(name));
     return *b;
+}
+
+bool register_sampler_backend(const SamplerBackend& b) {
+    Table& t = table();
+    std::lock_guard<std::mutex> lock(t.m);
+    const std::size_t n = t.n.load(std::memory_order_relaxed);
+    if (n == kMaxEntries || b.name.empty()) return false;
+    for (std::size_t i = 0; i < n; ++i)
+        if (t.e[i].name == b.name) return false;
+    t.e[n] = b;
+    t.n.store(n + 1, std::memory_order_release);
+    return true;
 }
 
 }  // namespace locus::backend

@@ -1,5 +1,5 @@
 // Per-row host entry points of the sampler API (reference:
-// src/locus/model/sampling.hpp:70-89, llama.hpp:352) over the batched C ABI.
+// src/locus/model/sampling.hpp:70-89) over the batched C ABI.
 // Each call copies one row to the device, runs lcs_sample on a per-thread
 // stream and copies the results back.
 #include <hip/hip_runtime.h>
@@ -222,33 +222,6 @@ void logprobs_from(std::span<const float> logits, tok::TokenId chosen, std::uint
     s.finish();
     top.clear();
     for (std::uint32_t j = 0; j < k; ++j) top.push_back(TokenLogprob{ids_h[j], lps_h[j]});
-}
-
-tok::TokenId argmax(std::span<const float> logits) {
-    const std::uint32_t V = checked_vocab(logits.size());
-    RowSession& s = session();
-    s.reserve(V, 0);
-    const lcs_params lp = to_lcs(SamplingParams{});
-    const double u = 0.0;
-    check(hipMemcpyAsync(s.logits, logits.data(), V * sizeof(float), hipMemcpyHostToDevice, s.st), "copy logits");
-    check(hipMemcpyAsync(s.params, &lp, sizeof lp, hipMemcpyHostToDevice, s.st), "copy params");
-    check(hipMemcpyAsync(s.u, &u, sizeof u, hipMemcpyHostToDevice, s.st), "copy u");
-    lcs_batch b{};
-    b.rows = 1;
-    b.vocab = V;
-    b.dtype = LCS_F32;
-    b.row_stride = s.stride;
-    b.logits = s.logits;
-    b.params = s.params;
-    b.params_host = &lp;
-    b.u = s.u;
-    lcs_out o{};
-    o.ids = s.ids;
-    s.run(b, o);
-    tok::TokenId id = -1;
-    check(hipMemcpyAsync(&id, s.ids, sizeof id, hipMemcpyDeviceToHost, s.st), "copy id");
-    s.finish();
-    return id;
 }
 
 }  // namespace locus::model

@@ -8,17 +8,17 @@
 // sampling.cpp: CMakeLists.txt:83-99 gives -mfma only to matvec_avx2.cpp).
 //
 // Functions and the reference lines they restate:
-//   orc_sample        src/locus/model/sampling.cpp:136-239 (sample) with
-//                     apply_penalties sampling.cpp:107-132 and, for the greedy
+//   orc_sample        src/locus/model/sampling.cpp:45-148 (sample) with
+//                     apply_penalties sampling.cpp:16-41 and, for the greedy
 //                     branch, argmax src/locus/model/llama.cpp:1237-1245.
 //                     The draw is std::uniform_real_distribution<double>
 //                     (0, kept_sum) over one mt19937_64 output, i.e.
 //                     r = u * (kept_sum - 0) + 0 with u from
 //                     generate_canonical (libstdc++ random.tcc:3348-3380,
 //                     random.h:1868-1870); u is passed in.
-//   orc_logprobs      sampling.cpp:241-281 (logprobs_from).
+//   orc_logprobs      sampling.cpp:150-190 (logprobs_from).
 //   orc_argmax        llama.cpp:1237-1245.
-//   orc_json_*        src/locus/model/grammar.cpp:75-260 (JsonGrammar) and the
+//   orc_json_*        src/locus/model/grammar.cpp:16-201 (JsonGrammar) and the
 //                     per-token allows() of server.cpp:154-185.
 //   orc_ngram_draft   src/locus/model/speculative.cpp:7-28.
 //   orc_verify        engine.cpp:357-396 acceptance rule + logprobs_from
@@ -32,14 +32,19 @@
 // from its threshold, in CDF units. Tests use the margins to identify the
 // documented near-tie rows and the tie flags for exact-tie rows.
 //
-// Parity pinning (what checks each function, see tests/test_oracle_*.py):
+// Parity pinning (what checks each function, all in tests/test_oracle.py):
 //   orc_sample/orc_logprobs/orc_argmax: golden vectors produced by the
-//     compiled reference (oracle/_ref) in tests/golden/*.json, the reference's
-//     own KATs (tests/test_sampling.cpp), and closed forms (numpy log-softmax,
-//     brute-force sorted prefixes).
-//   orc_json_*: the reference's KATs (tests/test_grammar.cpp) and golden
-//     accept/reject vectors from oracle/_ref.
-//   orc_ngram_draft: KATs (tests/test_speculative.cpp) + brute force.
+//     compiled reference (oracle/_ref) in tests/golden/configs.json and
+//     edge.json, the reference's own KATs (tests/test_sampling.cpp), and
+//     closed forms (numpy log-softmax, brute-force sorted prefixes).
+//   orc_json_feed/orc_json_complete: the compiled reference's accept counts
+//     and complete() on 353 golden strings (tests/golden/grammar.json) and the
+//     reference's KATs (tests/test_grammar.cpp:28-77).
+//   orc_json_mask: the compiled reference's masks in grammar.json.
+//   orc_ngram_draft: the compiled reference's drafts on 200 golden cases
+//     (tests/golden/ngram.json), its KATs (tests/test_speculative.cpp:9-32)
+//     and a brute-force statement of the rule.
+//   orc_verify: golden argmax / draft logprob / acceptance in configs.json.
 //   orc_mt_u: the C++ standard's check value for mt19937_64 ([rand.predef]).
 #include <algorithm>
 #include <cmath>
@@ -335,7 +340,7 @@ void logprobs_impl(const float* logits, uint32_t V, int32_t chosen,
     }
 }
 
-// ----- JsonGrammar restatement (grammar.cpp:75-260) -----
+// ----- JsonGrammar restatement (grammar.cpp:16-201) -----
 enum class GS : uint8_t {
     Val, ArrStart, ObjStart, ObjKey, Colon, InStr, StrEsc, StrU, InNum, Kw, AfterVal
 };
@@ -512,7 +517,7 @@ void orc_sample_batch(float* logits, uint32_t rows, uint32_t V, uint64_t row_str
 }
 
 // Speculative verify per row (engine.cpp:357-396 with logprobs_from
-// sampling.cpp:241-281): argmax, lp(draft), acceptance per sequence.
+// sampling.cpp:150-190): argmax, lp(draft), acceptance per sequence.
 void orc_verify(const void* logits, int bf16, uint32_t n_seq, uint32_t rows_per_seq,
                 uint32_t V, uint64_t row_stride, const int32_t* draft,
                 int32_t* argmax_ids, float* draft_lp, uint32_t* accept_len,

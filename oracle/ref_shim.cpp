@@ -48,7 +48,7 @@ locus::model::SamplingParams to_ref(const Params& p) {
 }
 
 // Bitmask-backed constraint in the shape of the reference test's AllowSet
-// (tests/test_sampling.cpp:18-24): bit t&31 of word t>>5.
+// (tests/test_sampling.cpp:18-24, as a bitmask): bit t&31 of word t>>5.
 struct MaskConstraint : locus::model::TokenConstraint {
     const uint32_t* words = nullptr;
     bool allows(locus::tok::TokenId t) const override {

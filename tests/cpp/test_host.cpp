@@ -16,7 +16,9 @@
 #include <string>
 #include <vector>
 
+#include <dlfcn.h>
 #include <hip/hip_runtime.h>
+#include <unistd.h>
 
 #include "locus/backend/sampler_registry.hpp"
 #include "locus/engine/batch_sampler.hpp"
@@ -151,24 +153,59 @@ static void test_ngram() {
     CHECK((ngram_draft(std::vector<TokenId>{3, 3, 3}, 1, 5) == std::vector<TokenId>{3}));
 }
 
+// A stand-in for the application's CPU sampler (the integration registers the
+// reference's own sample()/logprobs_from() this way): greedy on the first max.
+static TokenId first_max(std::span<float> l, const SamplingParams&, std::span<const TokenId>, std::mt19937_64&,
+                         const TokenConstraint*) {
+    std::size_t best = 0;
+    for (std::size_t i = 1; i < l.size(); ++i)
+        if (l[i] > l[best]) best = i;
+    return static_cast<TokenId>(best);
+}
+
 static void test_registry(bool gpu) {
     using namespace locus::backend;
-    const auto all = sampler_backends();
-    CHECK(all.size() == 1 && all[0].name == "hip");
+    {
+        const auto all = sampler_backends();
+        CHECK(all.size() == 1 && all[0].name == "hip");
+        CHECK(all[0].ops.sample_batch != nullptr && all[0].ops.sample != nullptr);
+    }
     CHECK(find_sampler_backend("hip") != nullptr);
     CHECK(find_sampler_backend("scalar") == nullptr);
     CHECK(throws<std::invalid_argument>([] { resolve_sampler_backend("scalar"); }));
     CHECK(throws<std::invalid_argument>([] { resolve_sampler_backend("bogus"); }));
     if (gpu) {
-        CHECK(all[0].available);
+        CHECK(sampler_backends()[0].available);
         CHECK(resolve_sampler_backend("").name == "hip");
         CHECK(resolve_sampler_backend("hip").name == "hip");
         CHECK(best_sampler_backend().ops.sample_batch != nullptr);
     } else {
-        CHECK(!all[0].available);
+        CHECK(!sampler_backends()[0].available);
         CHECK(throws<std::runtime_error>([] { best_sampler_backend(); }));
         CHECK(throws<std::invalid_argument>([] { resolve_sampler_backend("hip"); }));
     }
+    // the fallback hook: after the application registers its CPU sampler,
+    // best_sampler_backend() never throws (registry.cpp:105-111)
+    const auto before = sampler_backends();
+    SamplerOps ops;
+    ops.sample = &first_max;
+    CHECK(register_sampler_backend({"scalar", "application CPU sampler", true, true, ops}));
+    CHECK(!register_sampler_backend({"scalar", "a second one", true, true, ops}));   // name taken
+    CHECK(!register_sampler_backend({"hip", "shadow", true, true, ops}));
+    CHECK(before.size() == 1 && before[0].name == "hip");   // earlier spans stay valid
+    CHECK(sampler_backends().size() == 2 && sampler_backends()[1].name == "scalar");
+    CHECK(resolve_sampler_backend("scalar").ops.sample == &first_max);
+    const SamplerBackend& best = best_sampler_backend();
+    CHECK(best.name == (gpu ? "hip" : "scalar"));
+    std::vector<float> l{1.0f, 3.0f, 2.0f};
+    std::mt19937_64 rng(1);
+    CHECK(best.ops.sample(l, SamplingParams{}, {}, rng, nullptr) == 1);
+    CHECK(&resolve_sampler_backend("") == &best);
+    ::setenv("LOCUS_SAMPLER_BACKEND", "scalar", 1);
+    CHECK(resolve_sampler_backend("").name == "scalar");
+    ::setenv("LOCUS_SAMPLER_BACKEND", "bogus", 1);
+    CHECK(throws<std::invalid_argument>([] { resolve_sampler_backend(""); }));
+    ::unsetenv("LOCUS_SAMPLER_BACKEND");
 }
 
 namespace {
@@ -270,8 +307,8 @@ static void test_sampling_gpu() {
         CHECK(lp3 == 0.0f && one.empty());
     }
     {
-        const std::vector<float> l{0.5f, 2.0f, -1.0f, 2.0f};
-        CHECK(argmax(l) == 1);   // first index of the max
+        std::vector<float> l{0.5f, 2.0f, -1.0f, 2.0f};
+        CHECK(sample(l, SamplingParams{}, none, rng) == 1);   // greedy: first index of the max
     }
     {
         // JSON mask through allow_mask(): a sampled row only draws allowed tokens
@@ -293,15 +330,54 @@ static void test_sampling_gpu() {
     }
 }
 
-// BatchSampler (one lcs_sample per step) against the per-row API driven the
-// way Engine::sample_from drives it (engine.cpp:423-450): same requests, seeds
-// and logits; ids, histories and constraint states must agree step by step,
-// logprobs within 1e-5. The per-row API runs the exact path (it writes the
-// penalised logits back), the batch the sliced paths, so this also checks
-// the paths against each other.
+// The CPU oracle (oracle/liboracle.so, test infrastructure): the reference's
+// sample() and logprobs_from() restated, loaded from the tree next to this
+// program as the checker.
+namespace {
+struct OracleParams {   // orc_params == SamplingParams, field for field
+    float temperature;
+    std::uint32_t top_k;
+    float top_p, min_p, repeat_penalty, frequency_penalty, presence_penalty;
+    std::uint32_t repeat_last_n;
+};
+using OrcSample = std::int32_t (*)(float*, std::uint32_t, const OracleParams*, const std::int32_t*, std::uint32_t,
+                                   double, const std::uint32_t*, void*);
+using OrcLogprobs = void (*)(const float*, std::uint32_t, std::int32_t, std::uint32_t, float*, std::int32_t*, float*,
+                             std::uint32_t*);
+struct Oracle {
+    OrcSample sample = nullptr;
+    OrcLogprobs logprobs = nullptr;
+};
+Oracle load_oracle() {
+    char exe[4096] = {0};
+    const ssize_t n = readlink("/proc/self/exe", exe, sizeof exe - 1);
+    std::string dir = n > 0 ? std::string(exe, static_cast<std::size_t>(n)) : std::string("tests/cpp/test_host");
+    dir = dir.substr(0, dir.rfind('/'));
+    const std::string path = dir + "/../../oracle/liboracle.so";
+    void* h = dlopen(path.c_str(), RTLD_NOW | RTLD_LOCAL);
+    if (!h) throw std::runtime_error("the oracle is not built: " + path);
+    Oracle o;
+    o.sample = reinterpret_cast<OrcSample>(dlsym(h, "orc_sample"));
+    o.logprobs = reinterpret_cast<OrcLogprobs>(dlsym(h, "orc_logprobs"));
+    if (!o.sample || !o.logprobs) throw std::runtime_error("oracle symbols missing");
+    return o;
+}
+}  // namespace
+
+// BatchSampler (one lcs_sample per step) against two twins driven the way
+// Engine::sample_from drives a request (engine.cpp:423-450), each with its own
+// copy of the requests (same seeds, histories, constraint states):
+//   b: the per-row API (sample()/logprobs_from() on the device);
+//   c: the CPU oracle (the reference's sample()/logprobs_from() restated),
+//      with u drawn from the request's mt19937_64 as the reference draws it
+//      and the constraint's allow words as its candidate filter.
+// Ids, histories, constraint states and RNG positions must agree step by
+// step, logprobs within 1e-5. The per-row API runs the exact path (it writes
+// the penalised logits back), the batch the sliced paths, so this also
+// checks the paths against each other.
 static void test_batch_gpu() {
     using locus::engine::BatchSampler;
-    using locus::engine::SampleRequest;
+    using locus::sampler::SampleRequest;
     constexpr std::uint32_t V = 5003, B = 8, K = 5, STRIDE = (V + 3) / 4 * 4;
     std::vector<std::string> pieces = synthetic_pieces();
     std::mt19937_64 pr(11);
@@ -313,8 +389,9 @@ static void test_batch_gpu() {
         pieces.push_back(t);
     }
     auto mb = std::make_shared<const JsonMaskBuilder>(pieces);
-    JsonTokenConstraint ca(mb), cb(mb);
-    std::vector<SampleRequest> a(B), b(B);
+    JsonTokenConstraint ca(mb), cb(mb), cc(mb);
+    const Oracle orc = load_oracle();
+    std::vector<SampleRequest> a(B), b(B), c(B);
     for (std::uint32_t r = 0; r < B; ++r) {
         SamplingParams& p = a[r].sampling;
         switch (r) {
@@ -332,9 +409,12 @@ static void test_batch_gpu() {
         for (int i = 0; i < 30; ++i) a[r].generated.push_back(static_cast<TokenId>(pr() % V));
         if (r == 1 || r == 2 || r == 6) a[r].logprobs_opt = {true, r == 1 ? 5u : (r == 2 ? 3u : 1u)};
         b[r] = a[r];
+        c[r] = a[r];
     }
     a[4].constraint = &ca;
     b[4].constraint = &cb;
+    c[4].constraint = &cc;
+    std::vector<std::uint32_t> words((V + 31) / 32);
     std::vector<SampleRequest*> ap(B);
     for (std::uint32_t r = 0; r < B; ++r) ap[r] = &a[r];
     BatchSampler bs(0, B, V, 4096, 20);
@@ -370,17 +450,62 @@ static void test_batch_gpu() {
                 for (std::size_t j = 0; j < top.size() && j < e.top.size(); ++j)
                     CHECK(e.top[j].token == top[j].token && std::fabs(e.top[j].logprob - top[j].logprob) <= 1e-5f);
             }
+            // Engine::sample_from on request c[r], through the oracle
+            SampleRequest& o = c[r];
+            std::vector<float> orow(raw);
+            OracleParams op;
+            std::memcpy(&op, &o.sampling, sizeof op);
+            const std::size_t nh = o.generated.size(), w = std::min<std::size_t>(nh, o.sampling.repeat_last_n);
+            const double u = o.sampling.temperature > 0.0f ? std::generate_canonical<double, 53>(o.rng) : 0.0;
+            const std::uint32_t* m = nullptr;
+            if (o.constraint) {
+                CHECK(o.constraint->allow_mask(V, words.data()));
+                m = words.data();
+            }
+            const TokenId oid = orc.sample(orow.data(), V, &op, o.generated.data() + (nh - w),
+                                           static_cast<std::uint32_t>(w), u, m, nullptr);
+            if (o.constraint) o.constraint->commit(oid);
+            o.generated.push_back(oid);
+            if (oid != ids[r]) std::fprintf(stderr, "batch step %u row %u: batch %d oracle %d\n", step, r, ids[r], oid);
+            CHECK(oid == ids[r]);
+            CHECK(a[r].generated == o.generated);
+            if (o.logprobs_opt.enabled) {
+                const std::uint32_t k = std::min(o.logprobs_opt.top, V);
+                float lp = 0.0f;
+                std::vector<std::int32_t> tid(k + 1);
+                std::vector<float> tlp(k + 1);
+                orc.logprobs(raw.data(), V, oid, k, &lp, tid.data(), tlp.data(), nullptr);
+                const auto& e = a[r].logprobs.back();
+                CHECK(std::fabs(e.logprob - lp) <= 1e-5f);
+                CHECK(e.top.size() == k);
+                for (std::size_t j = 0; j < k && j < e.top.size(); ++j)
+                    CHECK(e.top[j].token == tid[j] && std::fabs(e.top[j].logprob - tlp[j]) <= 1e-5f);
+            }
         }
-        CHECK(a[3].rng() == b[3].rng());   // one engine output per stochastic row and step
-        CHECK(a[0].rng() == b[0].rng());   // none for greedy
+        // engine states compared without advancing them: one output per
+        // stochastic row and step, none for greedy rows
+        for (std::uint32_t r = 0; r < B; ++r) CHECK(a[r].rng == b[r].rng && a[r].rng == c[r].rng);
     }
-    for (std::uint32_t t = 0; t < V; t += 97) CHECK(ca.allows(static_cast<TokenId>(t)) == cb.allows(static_cast<TokenId>(t)));
+    for (std::uint32_t t = 0; t < V; t += 97) {
+        CHECK(ca.allows(static_cast<TokenId>(t)) == cb.allows(static_cast<TokenId>(t)));
+        CHECK(ca.allows(static_cast<TokenId>(t)) == cc.allows(static_cast<TokenId>(t)));
+    }
     (void)hipFree(dlog);
     // limits
     std::vector<SampleRequest> many(B + 1);
     std::vector<SampleRequest*> mp;
     for (auto& q : many) mp.push_back(&q);
     CHECK(throws<std::invalid_argument>([&] { bs.sample_step(nullptr, LCS_F32, STRIDE, mp); }));
+    // a limit met by a later row rejects the step before any rng advances
+    std::vector<SampleRequest> lim(2);
+    lim[0].sampling.temperature = 1.0f;
+    lim[0].rng.seed(7);
+    lim[1].logprobs_opt = {true, 21};   // above max_top
+    std::vector<SampleRequest*> lp{&lim[0], &lim[1]};
+    CHECK(throws<std::invalid_argument>([&] { bs.sample_step(nullptr, LCS_F32, STRIDE, lp); }));
+    std::mt19937_64 fresh(7);
+    CHECK(lim[0].rng() == fresh());
+    CHECK(lim[0].generated.empty() && lim[1].generated.empty());
 }
 
 int main(int argc, char** argv) {

@@ -236,3 +236,97 @@ def test_checks_have_teeth_against_planted_mistake():
             caught = True
             break
     assert caught
+
+
+# ---- grammar and n-gram restatements (orc_json_*, orc_ngram_draft) ----------
+
+def test_oracle_json_matches_reference_strings():
+    """orc_json_feed / orc_json_complete against the compiled reference's
+    JsonGrammar (grammar.cpp:57-201) on every golden string: the number of
+    bytes accepted before the first rejection, and complete() after them."""
+    fx = load("grammar.json")
+    assert len(fx["strings"]) > 300
+    for s in fx["strings"]:
+        g = O.OracleJson()
+        n = 0
+        for b in s["bytes"]:
+            if not g.feed(b):
+                break
+            n += 1
+        assert n == s["accepted"], bytes(s["bytes"])
+        assert int(g.complete()) == s["complete"], bytes(s["bytes"])
+
+
+def test_oracle_json_masks_match_reference_masks():
+    """orc_json_mask (per-token allows() of server.cpp:160-171 over a copy of
+    the grammar) against masks the compiled reference's JsonGrammar produced."""
+    fx = load("grammar.json")
+    pieces = [bytes(p) for p in fx["pieces"]]
+    checked = 0
+    for m in fx["masks"]:
+        g = O.OracleJson()
+        ok = all(g.feed(b) for b in m["prefix"])
+        assert ok == (m["rc"] == 0)
+        if ok:
+            assert g.mask(pieces, fx["vocab"]).tolist() == m["mask"], bytes(m["prefix"])
+            checked += 1
+    assert checked >= 5
+
+
+def test_oracle_json_kats():
+    """The reference's own grammar KATs (tests/test_grammar.cpp:28-77)."""
+    def accepts_complete(t):
+        g = O.OracleJson()
+        return g.feed_all(t) and g.complete()
+
+    def rejects(t):
+        return not O.OracleJson().feed_all(t)
+    for t in [b'{}', b'[]', b'"hi"', b'123', b'-1.5e3', b'true', b'false', b'null', b'{"a":1}',
+              b'[1,2,3]', b'{"a":[1,{"b":"c"}],"d":null}', b'  {  "x" : 1 }  ', b'[ -0.5 , 2 ]']:
+        assert accepts_complete(t), t
+    for t in [b'{', b'{"a"', b'{"a":', b'[1,', b'"ab', b'tr', b'-', b'[1']:
+        g = O.OracleJson()
+        assert g.feed_all(t) and not g.complete(), t
+    for t in [b'{,}', b'[,]', b'[1,]', b'{"a" 1}', b'{1:2}', b'trux', b'{}x', b'01a', b'[1 2]', b'}']:
+        assert rejects(t), t
+    for t in [b'[12,34]', b'{"n":42}', b'42', b'42   ']:
+        assert accepts_complete(t), t
+    assert rejects(b'42x')
+    g = O.OracleJson()
+    assert g.feed_all(b'{}') and g.complete()
+    assert g.feed(ord(' ')) and g.complete()
+    assert not g.feed(ord('x'))
+
+
+def test_oracle_ngram_matches_reference():
+    """orc_ngram_draft against the compiled reference's ngram_draft
+    (speculative.cpp:7-28) on every golden case."""
+    fx = load("ngram.json")
+    assert len(fx) >= 100
+    for c in fx:
+        assert O.ngram_draft(c["ctx"], c["ngram"], c["max_draft"]) == c["draft"], c
+
+
+def test_oracle_ngram_kats_and_brute_force():
+    """The reference's KATs (tests/test_speculative.cpp:9-32) and a brute-force
+    statement of the rule: the most recent earlier occurrence of the trailing
+    n-gram, continued by up to max_draft tokens."""
+    assert O.ngram_draft([1, 2, 3, 4, 1, 2, 3], 2, 3) == [4, 1, 2]
+    assert O.ngram_draft([9, 9, 5, 9, 9, 7, 9, 9], 2, 2) == [7, 9]
+    assert O.ngram_draft([5, 6, 7], 2, 3) == []
+    assert O.ngram_draft([1, 2], 2, 3) == []
+    assert O.ngram_draft([5, 6, 7], 0, 3) == []
+
+    def brute(ctx, n, k):
+        if n == 0 or len(ctx) <= n or k == 0:
+            return []
+        tail = ctx[-n:]
+        for s in range(len(ctx) - n - 1, -1, -1):
+            if ctx[s:s + n] == tail:
+                return ctx[s + n:s + n + k]
+        return []
+    rng = np.random.default_rng(5)
+    for _ in range(2000):
+        ctx = rng.integers(0, 4, int(rng.integers(0, 30))).tolist()
+        n, k = int(rng.integers(1, 4)), int(rng.integers(0, 6))
+        assert O.ngram_draft(ctx, n, k) == brute(ctx, n, k), (ctx, n, k)
