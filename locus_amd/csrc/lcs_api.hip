@@ -26,7 +26,6 @@ struct lcs_ctx {
     uint32_t max_slices = 0;
     uint32_t* recs = nullptr;
     uint64_t* srecs = nullptr;
-    uint32_t* counters = nullptr;
     uint32_t* d_ids = nullptr;
     float* d_raw = nullptr;
     float* d_pen = nullptr;
@@ -126,7 +125,6 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t 
     hipError_t e = hipSuccess;
     if ((e = hipMalloc(&c->recs, rec_bytes)) != hipSuccess ||
         (e = hipMalloc(&c->srecs, srec_bytes)) != hipSuccess ||
-        (e = hipMalloc(&c->counters, (size_t)max_rows * 4)) != hipSuccess ||
         (e = hipMalloc(&c->d_ids, d_elems * 4)) != hipSuccess ||
         (e = hipMalloc(&c->d_raw, d_elems * 4)) != hipSuccess ||
         (e = hipMalloc(&c->d_pen, d_elems * 4)) != hipSuccess ||
@@ -135,7 +133,6 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t 
         (e = hipMalloc(&c->nh_cnt, nh_elems * 4)) != hipSuccess ||
         (e = hipMalloc(&c->nh_mass, nh_elems * 8)) != hipSuccess ||
         (e = hipMalloc(&c->nlist, nuc_rows * lcs::kNucList * 8)) != hipSuccess ||
-        (e = hipMemset(c->counters, 0, (size_t)max_rows * 4)) != hipSuccess ||
         (e = hipMemset(c->status, 0, 4)) != hipSuccess ||
         (e = hipDeviceSynchronize()) != hipSuccess) {
         g_create_error = std::string("lcs_create: ") + hipGetErrorString(e);
@@ -151,7 +148,6 @@ void lcs_destroy(lcs_ctx* c) {
     (void)hipDeviceSynchronize();
     (void)hipFree(c->recs);
     (void)hipFree(c->srecs);
-    (void)hipFree(c->counters);
     (void)hipFree(c->d_ids);
     (void)hipFree(c->d_raw);
     (void)hipFree(c->nrow);
@@ -179,9 +175,8 @@ __global__ void clear_words(uint32_t* w, uint32_t n) {
 
 // lcs_sample on the workspace of c (a context, or the no-alloc entry's view
 // of its static array); validation first, nothing is launched on an error.
-// clear_n > 0: the first clear_n words at c->counters (the arrival counters
-// and the status word) are zeroed ahead of the kernels.
-int sample_impl(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream, uint32_t clear_n) {
+// clear_status: the status word is zeroed ahead of the kernels.
+int sample_impl(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream, bool clear_status) {
     if (!b || !o) return fail(c, LCS_ERR_INVALID_ARG, "null batch or output");
     if (b->rows == 0) return LCS_OK;
     if (b->dtype != LCS_F32 && b->dtype != LCS_BF16) return fail(c, LCS_ERR_INVALID_ARG, "dtype");
@@ -258,7 +253,6 @@ int sample_impl(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream, 
     a.top_lp = o->top_lp;
     a.diag = o->diag;
     a.recs = c->recs;
-    a.counters = c->counters;
     a.d_ids = c->d_ids;
     a.d_raw = c->d_raw;
     a.d_pen = c->d_pen;
@@ -283,8 +277,8 @@ int sample_impl(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream, 
     DeviceGuard g(c->device);
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t e = hipSuccess;
-    if (clear_n) {
-        hipLaunchKernelGGL(clear_words, dim3(1), dim3(256), 0, st, c->counters, clear_n);
+    if (clear_status) {
+        hipLaunchKernelGGL(clear_words, dim3(1), dim3(64), 0, st, c->status, 1u);
         if ((e = hipGetLastError()) != hipSuccess) return hip_fail(c, e, "workspace clear launch");
     }
     if (any_general && (e = lcs::launch_general(a, st)) != hipSuccess) return hip_fail(c, e, "general kernel launch");
@@ -305,7 +299,6 @@ constexpr size_t kAlign = 256;
 constexpr size_t up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
 constexpr size_t kSzRecs = up((size_t)kNoAllocRows * lcs::kMaxSlices * lcs::rec::kWords * 4);
 constexpr size_t kSzSrecs = up((size_t)kNoAllocRows * lcs::kSsMaxSlices * lcs::rec::kWords64 * 8);
-constexpr size_t kSzCounters = up((size_t)kNoAllocRows * 4);
 constexpr size_t kSzStatus = up(4);
 constexpr size_t kSzD = up((size_t)kNoAllocRows * kNoAllocHist * 4);
 constexpr size_t kSzNrow = up((size_t)kNoAllocRows * sizeof(lcs::NucRow));
@@ -315,8 +308,7 @@ constexpr size_t kSzNhMass = up(kNhElems * 8);
 constexpr size_t kSzNlist = up((size_t)kNoAllocRows * lcs::kNucList * 8);
 constexpr size_t kOffRecs = 0;
 constexpr size_t kOffSrecs = kOffRecs + kSzRecs;
-constexpr size_t kOffCounters = kOffSrecs + kSzSrecs;   // counters, then status: cleared by each call
-constexpr size_t kOffStatus = kOffCounters + kSzCounters;
+constexpr size_t kOffStatus = kOffSrecs + kSzSrecs;   // cleared by each call
 constexpr size_t kOffDIds = kOffStatus + kSzStatus;
 constexpr size_t kOffDRaw = kOffDIds + kSzD;
 constexpr size_t kOffDPen = kOffDRaw + kSzD;
@@ -339,7 +331,7 @@ extern "C" {
 
 int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
     if (!c) return LCS_ERR_INVALID_ARG;
-    return sample_impl(c, b, o, stream, 0u);
+    return sample_impl(c, b, o, stream, false);
 }
 
 int lcs_sample_noalloc(const lcs_batch* b, const lcs_out* o, void* stream) {
@@ -374,7 +366,6 @@ int lcs_sample_noalloc(const lcs_batch* b, const lcs_out* o, void* stream) {
     w.max_slices = lcs::kMaxSlices;
     w.recs = reinterpret_cast<uint32_t*>(base + kOffRecs);
     w.srecs = reinterpret_cast<uint64_t*>(base + kOffSrecs);
-    w.counters = reinterpret_cast<uint32_t*>(base + kOffCounters);
     w.status = reinterpret_cast<uint32_t*>(base + kOffStatus);
     w.d_ids = reinterpret_cast<uint32_t*>(base + kOffDIds);
     w.d_raw = reinterpret_cast<float*>(base + kOffDRaw);
@@ -387,8 +378,8 @@ int lcs_sample_noalloc(const lcs_batch* b, const lcs_out* o, void* stream) {
         g_create_error = "lcs_sample_noalloc: rows above " + std::to_string(kNoAllocRows);
         return LCS_ERR_CAPACITY;
     }
-    // the counters and the status word (adjacent) start at zero on every call
-    const int rc = sample_impl(&w, b, o, stream, (uint32_t)((kSzCounters + kSzStatus) / 4));
+    // the status word starts at zero on every call
+    const int rc = sample_impl(&w, b, o, stream, true);
     if (rc != LCS_OK) g_create_error = "lcs_sample_noalloc: " + w.err;
     return rc;
 }

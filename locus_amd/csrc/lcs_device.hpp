@@ -441,16 +441,11 @@ __device__ __forceinline__ uint32_t next_pow2(uint32_t n) {
     return p;
 }
 
-// ------------------------------------- cross-workgroup coherent traffic ----
-// Records that another workgroup reads in the same kernel are written and
-// read with device-scope relaxed atomics (written through to the coherence
-// point, read past the non-coherent caches). A workgroup publishes with
-// these stores, then a barrier, then one thread arrives at the row's counter
-// (arrive_rmw): an agent-scope release RMW orders every record store of the
-// workgroup (made visible to that thread by the barrier) before its count,
-// and the workgroup that sees the final count takes an agent-scope acquire
-// fence before anything reads the records, so its reads see every earlier
-// arrival's stores (the RMWs form one release sequence).
+// ------------------------------------------- device-scope word traffic ----
+// Relaxed device-scope atomic loads and stores (written through to, and read
+// from, the device coherence point). The sampler's workgroups never wait on
+// one another: records are written by one kernel and read by the next, and
+// the kernel boundary orders them.
 __device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -472,14 +467,6 @@ __device__ __forceinline__ double ld_dev_d(const double* p) {
     return __longlong_as_double(static_cast<long long>(ld_dev_u64(reinterpret_cast<const uint64_t*>(p))));
 }
 __device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
-// The arrival at a row counter (see above): true in the arrival that completes
-// the count of `expected`, which has then taken the acquire fence.
-__device__ __forceinline__ bool arrive_rmw(uint32_t* counter, uint32_t expected) {
-    const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = prev == expected - 1u;
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    return last;
-}
 // ------------------------------------------------------- scalar loads ----
 // Read-only per-row words through the scalar cache (SMEM): waiting for them
 // does not wait for the vector loads in flight. For data the kernel never

@@ -27,9 +27,8 @@ constexpr uint32_t kSsMaxSlices = kMaxVocab / kSsMax;       // 32
 constexpr uint32_t kSsTopKMerge = 2048;  // slices x top_k entries row_fin merges
 constexpr int kFinThreads = 256;         // row_fin workgroup
 
-// Slice record (64-bit words): the nucleus passes write and read it within a
-// kernel (device-scope stores, agent-scope release / acquire arrival);
-// slice_stats writes it with plain stores for the next kernel, row_fin.
+// Slice record (64-bit words): a pass's slice workgroups write it, the pass's
+// per-row finalize kernel reads it (the kernel boundary orders the two).
 namespace rec {
 constexpr uint32_t kHdr = 8;         // header words:
 // 0: f32 raw max | u16 window entries << 32 | u16 flags << 48
@@ -128,7 +127,6 @@ struct SampleArgs {   // (at most 128 dwords: kernels stage it in LDS, two dword
     lcs_row_diag* diag;
     // workspace
     uint32_t* recs;          // nucleus: rows x slices x rec::kWords
-    uint32_t* counters;      // rows
     uint64_t* srecs;         // sliced path: rows x kSsMaxSlices x rec::kWords64
     uint32_t ss_slices;      // sliced path: slices per row (<= kSsMaxSlices)
     uint32_t ss_len;         // sliced path: elements per slice (multiple of 8, <= kSsMax)

@@ -305,18 +305,14 @@ __device__ __forceinline__ uint32_t nuc_sub(float f, uint32_t b0, uint32_t b1) {
     return c > 0.0f ? (uint32_t)c : 0u;
 }
 
-// Arrival at the row's counter after this workgroup's stores are complete;
-// true in every thread of the last arrival.
-__device__ __forceinline__ bool nuc_arrive(uint32_t* counter, uint32_t S, NucSmem& sm) {
-    wait_all_memory();
-    __syncthreads();
-    if (tid_x() == 0) {
-        const bool last = arrive_rmw(counter, S);
-        if (last) st_dev(counter, 0u);
-        sm.l.last = last ? 1u : 0u;
-    }
-    __syncthreads();
-    return sm.l.last != 0u;
+// Row and mode of a finalize workgroup (one per row of the launch); false
+// when the row is not on the nucleus path.
+__device__ __forceinline__ bool nuc_fin_row(const SampleArgs& a, uint32_t& row, lcs_params& P, bool& masked) {
+    row = a.nuc_row0 + wg_x();
+    if (row >= a.rows) return false;
+    P = scalar_load(a.params + row);
+    masked = a.mask != nullptr && (a.has_mask == nullptr || scalar_load_u8(a.has_mask + row) != 0);
+    return row_mode(P, masked, a.vocab) == kModeNucleus;
 }
 
 // Row and mode for a nucleus launch; false when this workgroup has no work.
@@ -518,7 +514,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
             }
         }
     }
-    if (!nuc_arrive(a.counters + row, S, sm)) return;
+}
+
+// The row state and top-n logprobs from pass A's records (one workgroup per
+// row; the kernel boundary orders the records before these reads).
+template <int G>
+__global__ __launch_bounds__(NT) void nuc_stats_fin(SampleArgs a) {
+    NucSmem& sm = g_nuc;
+    uint32_t row;
+    lcs_params P;
+    bool masked;
+    if (!nuc_fin_row(a, row, P, masked)) return;
+    const uint32_t tid = tid_x(), S = a.slices;
+    const int lane = lane_id(), wv = (int)(tid / kWave);
+    const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
+    const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
+    const float NEG = -__builtin_huge_valf();
+    (void)tid;
 
     // ---- the row's state (wave 0) and logprobs (wave 1) ----
     const uint64_t* recs = reinterpret_cast<const uint64_t*>(a.recs) + (uint64_t)row * S * rec::kWords64;
@@ -680,7 +692,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         st_dev(gc + b, sm.u.h.cnt[b]);
         st_dev_d(gm + b, sm.u.h.mass[b]);
     }
-    if (!nuc_arrive(a.counters + row, S, sm)) return;
+}
+
+// Pass B's histograms merged per row and the plan of bin ranges (one
+// workgroup per row, after the kernel boundary).
+template <int G>
+__global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
+    NucSmem& sm = g_nuc;
+    uint32_t row;
+    lcs_params P;
+    bool masked;
+    if (!nuc_fin_row(a, row, P, masked)) return;
+    const uint32_t tid = tid_x(), S = a.slices;
+    const uint32_t wrow = row - a.nuc_row0;
+    NucRow* nr = a.nrow + wrow;
+    if (nr->flags & kNucFallback) return;   // resolved by the exact path
+    const float sx = nr->sx;
+    const double inv_sx = 1.0 / (double)sx;
 
     // ---- the row's histogram: merged, then inclusive prefix sums ----
     constexpr uint32_t BPT = kNucBins / NT;   // bins per thread
@@ -1223,12 +1251,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     NucRow* nr = a.nrow + wrow;
     const uint32_t flags = scalar_load(&nr->flags);
     const bool exact = (flags & kNucFallback) != 0u;
-    if (exact && slice != 0) {   // slice 0 resolves the row by the exact path
+    if (exact) {   // nuc_select_fin resolves the row by the exact path
         wait_all_memory();
         return;
     }
-    bool run_fin = exact;
-    if (!exact) {
+    {
     const float maxl = scalar_load(&nr->maxl);
     const float sx = scalar_load(&nr->sx);
     const bool use_mask = scalar_load(&nr->use_mask) != 0u;
@@ -1309,36 +1336,50 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
             }
         }
     }
-    run_fin = nuc_arrive(a.counters + row, S, sm);
     }
-    if (!run_fin) return;
-    if (tid == 0) stash_args(&sm.l.args, a);
+    (void)S;
+}
+
+// Pass C's decisions, one workgroup per row after the kernel boundary: the
+// exact path for a row the plan could not serve, else the exact decisions
+// over the compacted ranges.
+template <int G>
+__global__ __launch_bounds__(NT) void nuc_select_fin_kernel(SampleArgs a) {
+    NucSmem& sm = g_nuc;
+    uint32_t row;
+    lcs_params P;
+    bool masked;
+    if (!nuc_fin_row(a, row, P, masked)) return;
+    const bool exact = (a.nrow[row - a.nuc_row0].flags & kNucFallback) != 0u;
+    if (tid_x() == 0) stash_args(&sm.l.args, a);
     __syncthreads();
     nuc_select_fin<G>(row, exact);
 }
 
-// Host launchers: three passes per chunk of kNucRows rows.
+// Host launchers: per chunk of kNucRows rows, three slice-parallel passes,
+// each followed by its per-row finalize (the kernel boundaries order every
+// record a finalize reads after the stores that wrote it).
+template <int G>
+static void launch_passes(const SampleArgs& a, uint32_t nrows, hipStream_t st) {
+    const dim3 grid(nrows * a.slices), block(NT), rgrid(nrows);
+    hipLaunchKernelGGL(nuc_stats<G>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
+                       a.vocab, a.nuc_row0, a.all_nucleus, a);
+    hipLaunchKernelGGL(nuc_stats_fin<G>, rgrid, block, 0, st, a);
+    hipLaunchKernelGGL(nuc_hist<G>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
+                       a.vocab, a.nuc_row0, a.all_nucleus, a);
+    hipLaunchKernelGGL(nuc_hist_fin<G>, rgrid, block, 0, st, a);
+    hipLaunchKernelGGL(nuc_select<G>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
+                       a.vocab, a.nuc_row0, a.all_nucleus, a);
+    hipLaunchKernelGGL(nuc_select_fin_kernel<G>, rgrid, block, 0, st, a);
+}
+
 hipError_t launch_nucleus(const SampleArgs& a0, hipStream_t st) {
     for (uint32_t r0 = 0; r0 < a0.rows; r0 += kNucRows) {
         SampleArgs a = a0;
         a.nuc_row0 = r0;
         const uint32_t nrows = min(kNucRows, a0.rows - r0);
-        const dim3 grid(nrows * a.slices), block(NT);
-        if (a.dtype == LCS_BF16) {
-            hipLaunchKernelGGL(nuc_stats<8>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
-                               a.vocab, a.nuc_row0, a.all_nucleus, a);
-            hipLaunchKernelGGL(nuc_hist<8>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
-                               a.vocab, a.nuc_row0, a.all_nucleus, a);
-            hipLaunchKernelGGL(nuc_select<8>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
-                               a.vocab, a.nuc_row0, a.all_nucleus, a);
-        } else {
-            hipLaunchKernelGGL(nuc_stats<4>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
-                               a.vocab, a.nuc_row0, a.all_nucleus, a);
-            hipLaunchKernelGGL(nuc_hist<4>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
-                               a.vocab, a.nuc_row0, a.all_nucleus, a);
-            hipLaunchKernelGGL(nuc_select<4>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
-                               a.vocab, a.nuc_row0, a.all_nucleus, a);
-        }
+        if (a.dtype == LCS_BF16) launch_passes<8>(a, nrows, st);
+        else launch_passes<4>(a, nrows, st);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
