@@ -255,6 +255,57 @@ def mask_bench(budget_s: float = 5.0):
             "trie_cached_ms": float(np.mean(warm)) * 1e3, "cpu": cpu_model()}
 
 
+def draft_bench(n_seq: int = 512, ctx_len: int = 4096, ngram: int = 3, max_draft: int = 7,
+                steps: int = 200, cpu_seconds: float = 3.0):
+    """Batched n-gram drafts on the device (lcs_ngram_draft) for C5's 512
+    sequences, each with a 4096-token context over a 64-token alphabet
+    (matches are found near the end), against the reference's per-sequence
+    ngram_draft (speculative.cpp:7-28) on one host core."""
+    import ctypes as C
+    import torch
+
+    from locus_amd import sampler as SM
+    from oracle import pyoracle as O
+    rng = np.random.default_rng(20261205)
+    ctxs = rng.integers(0, 64, (n_seq, ctx_len)).astype(np.int32)
+    s = SM.Sampler(device=0, max_rows=n_seq, max_vocab=1024, max_hist=64, max_top=4)
+    got, _ = s.ngram_draft(list(ctxs), ngram, max_draft)
+    dev = torch.device("cuda", 0)
+    off = torch.from_numpy((np.arange(n_seq + 1, dtype=np.uint32) * ctx_len).view(np.int32)).to(dev)
+    ids = torch.from_numpy(ctxs.reshape(-1)).to(dev)
+    dr = torch.empty((n_seq, max_draft), dtype=torch.int32, device=dev)
+    ln = torch.empty(n_seq, dtype=torch.int32, device=dev)
+    b = SM._DBatch(n_seq, ngram, max_draft, SM._dptr(off), SM._dptr(ids))
+    o = SM._DOut(SM._dptr(dr), SM._dptr(ln))
+    L = SM.lib()
+    stream = torch.cuda.current_stream()
+    h = s.stream_handle(stream)
+    for _ in range(10):
+        L.lcs_ngram_draft(s.ctx, C.byref(b), C.byref(o), h)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        L.lcs_ngram_draft(s.ctx, C.byref(b), C.byref(o), h)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / steps * 1e3
+    s.close()
+    kind = "reference" if O.ref_available() else "port"
+    t0, reps = time.perf_counter(), 0
+    while time.perf_counter() - t0 < cpu_seconds:
+        for c in ctxs:
+            if kind == "reference":
+                out = np.zeros(max_draft, dtype=np.int32)
+                O.ref().ref_ngram_draft(c.ctypes.data, ctx_len, ngram, max_draft, out.ctypes.data)
+            else:
+                O.ngram_draft(c, ngram, max_draft)
+        reps += 1
+    cpu_us = (time.perf_counter() - t0) / reps * 1e6
+    return {"n_seq": n_seq, "ctx_len": ctx_len, "ngram": ngram, "max_draft": max_draft,
+            "mean_draft_len": float(np.mean([len(g) for g in got])), "gpu_us_per_call": us,
+            "cpu_us_per_batch": cpu_us, "cpu_kind": kind, "cpu_cores": 1, "cpu": cpu_model()}
+
+
 def copy_calibration(mib: int, reps: int = 20):
     """A plain device copy of known size (for scaling FETCH_SIZE/WRITE_SIZE:
     each dispatch must read and write exactly `mib` MiB)."""
@@ -380,9 +431,14 @@ def main():
     ap.add_argument("--copy-bytes", type=int, default=256 << 20)
     ap.add_argument("--mask-bench", action="store_true",
                     help="only time the host JSON allow-mask at V=128256 (CPU)")
+    ap.add_argument("--draft-bench", action="store_true",
+                    help="only time batched n-gram drafts on the device against the CPU reference")
     args = ap.parse_args()
     if args.mask_bench:
         print(json.dumps(mask_bench()))
+        return
+    if args.draft_bench:
+        print(json.dumps(draft_bench()))
         return
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace, args.kernel))

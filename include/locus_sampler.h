@@ -135,6 +135,22 @@ typedef struct lcs_verify_out {
     uint32_t* accept_len;      /* per sequence: leading rows whose argmax == draft */
 } lcs_verify_out;
 
+/* Prompt-lookup drafts for a batch of device-resident contexts: per
+ * sequence, the reference's ngram_draft (src/locus/model/speculative.cpp:7-28,
+ * declared at speculative.hpp:9-19). */
+typedef struct lcs_draft_batch {
+    uint32_t n_seq;
+    uint32_t ngram;            /* 0..64 (0: every draft empty) */
+    uint32_t max_draft;        /* 0..256 */
+    const uint32_t* ctx_off;   /* n_seq + 1 CSR offsets into ctx_ids */
+    const int32_t* ctx_ids;    /* each sequence's context (prompt + generated) */
+} lcs_draft_batch;
+
+typedef struct lcs_draft_out {
+    int32_t* draft;            /* n_seq x max_draft; entries past the draft are -1 */
+    uint32_t* draft_len;       /* n_seq: the draft's length (0..max_draft) */
+} lcs_draft_out;
+
 /* Number of usable gfx950 devices (0 when none). Replaces the runtime probe
  * that sets Backend::available (registry.cpp:148-223, cuda_stub.cpp:29). */
 int lcs_probe(int* n_devices);
@@ -166,6 +182,11 @@ int lcs_sample_noalloc(const lcs_batch* batch, const lcs_out* out, void* stream)
  * adds the draft logprob (sampling.cpp:150-170 with chosen = draft). */
 int lcs_verify(lcs_ctx* ctx, const lcs_verify_batch* batch, const lcs_verify_out* out,
                void* stream);
+
+/* Batched n-gram drafts: replaces the per-sequence host call of
+ * engine.cpp:328-329 (speculative.cpp:7-28) when contexts live on the device.
+ * Drafts feed lcs_verify. Allocates nothing. */
+int lcs_ngram_draft(lcs_ctx* ctx, const lcs_draft_batch* batch, const lcs_draft_out* out, void* stream);
 
 /* Sticky device-side status bits of ctx (LCS_STATUS_*), set by kernels that
  * met an input they could not serve (the affected rows get id -1). Blocking:

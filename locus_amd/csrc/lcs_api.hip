@@ -18,6 +18,7 @@ hipError_t launch_slice(const SampleArgs& a, hipStream_t st);
 hipError_t launch_general(const SampleArgs& a, hipStream_t st);
 hipError_t launch_nucleus(const SampleArgs& a, hipStream_t st);
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t st);
+hipError_t launch_draft(const DraftArgs& a, hipStream_t st);
 }  // namespace lcs
 
 struct lcs_ctx {
@@ -412,6 +413,31 @@ int lcs_verify(lcs_ctx* c, const lcs_verify_batch* b, const lcs_verify_out* o, v
     DeviceGuard g(c->device);
     const hipError_t e = lcs::launch_verify(a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(c, e, "verify kernel launch");
+    return LCS_OK;
+}
+
+int lcs_ngram_draft(lcs_ctx* c, const lcs_draft_batch* b, const lcs_draft_out* o, void* stream) {
+    if (!c) return LCS_ERR_INVALID_ARG;
+    if (!b || !o) return fail(c, LCS_ERR_INVALID_ARG, "null draft argument");
+    if (b->n_seq == 0) return LCS_OK;
+    if (!b->ctx_off || !b->ctx_ids || !o->draft_len || (b->max_draft > 0 && !o->draft)) {
+        return fail(c, LCS_ERR_INVALID_ARG, "null draft pointer");
+    }
+    if (b->ngram > lcs::kDraftMaxNgram || b->max_draft > lcs::kDraftMaxLen) {
+        return fail(c, LCS_ERR_INVALID_ARG, "ngram must be <= 64 and max_draft <= 256");
+    }
+    if (b->n_seq > c->max_rows) return fail(c, LCS_ERR_CAPACITY, "n_seq above max_rows");
+    lcs::DraftArgs a{};
+    a.n_seq = b->n_seq;
+    a.ngram = b->ngram;
+    a.max_draft = b->max_draft;
+    a.ctx_off = b->ctx_off;
+    a.ctx_ids = b->ctx_ids;
+    a.draft = o->draft;
+    a.draft_len = o->draft_len;
+    DeviceGuard g(c->device);
+    const hipError_t e = lcs::launch_draft(a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(c, e, "draft kernel launch");
     return LCS_OK;
 }
 

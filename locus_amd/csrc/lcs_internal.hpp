@@ -158,6 +158,18 @@ struct VerifyArgs {
     uint32_t* accept_len;
 };
 
+// n-gram drafts (lcs_draft.hip)
+constexpr uint32_t kDraftMaxNgram = 64;
+constexpr uint32_t kDraftMaxLen = 256;
+constexpr uint32_t kNoDraft = 0xffffffffu;
+struct DraftArgs {
+    uint32_t n_seq, ngram, max_draft;
+    const uint32_t* ctx_off;
+    const int32_t* ctx_ids;
+    int32_t* draft;
+    uint32_t* draft_len;
+};
+
 // status bits
 constexpr uint32_t kStatusHistCap = 1u;   // a penalty window exceeded the capacity
 constexpr uint32_t kStatusBinCap = 2u;    // selection could not narrow a bin (unexpected)

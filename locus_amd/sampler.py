@@ -50,6 +50,15 @@ class _VOut(C.Structure):
     _fields_ = [("argmax_ids", _P), ("draft_lp", _P), ("accept_len", _P)]
 
 
+class _DBatch(C.Structure):
+    _fields_ = [("n_seq", C.c_uint32), ("ngram", C.c_uint32), ("max_draft", C.c_uint32),
+                ("ctx_off", _P), ("ctx_ids", _P)]
+
+
+class _DOut(C.Structure):
+    _fields_ = [("draft", _P), ("draft_len", _P)]
+
+
 class SamplerError(RuntimeError):
     pass
 
@@ -76,6 +85,8 @@ def lib():
         L.lcs_sample_noalloc.argtypes = [C.POINTER(_Batch), C.POINTER(_Out), _P]
         L.lcs_verify.restype = C.c_int
         L.lcs_verify.argtypes = [_P, C.POINTER(_VBatch), C.POINTER(_VOut), _P]
+        L.lcs_ngram_draft.restype = C.c_int
+        L.lcs_ngram_draft.argtypes = [_P, C.POINTER(_DBatch), C.POINTER(_DOut), _P]
         L.lcs_last_error.restype = C.c_char_p
         L.lcs_last_error.argtypes = [_P]
         L.lcs_get_status.restype = C.c_int
@@ -326,6 +337,30 @@ class Sampler:
         return {"argmax_ids": torch.full((w.rows,), -7, dtype=torch.int32, device=dev),
                 "draft_lp": torch.zeros(w.rows, dtype=torch.float32, device=dev),
                 "accept_len": torch.full((w.n_seq,), 99, dtype=torch.int32, device=dev)}
+
+    def ngram_draft(self, contexts, ngram: int, max_draft: int):
+        """Batched prompt-lookup drafts (lcs_ngram_draft) for a list of token
+        sequences; returns (drafts: list of lists, raw (n_seq, max_draft) array)."""
+        torch = self.torch
+        dev = torch.device("cuda", self.device)
+        n = len(contexts)
+        off = np.zeros(n + 1, dtype=np.uint32)
+        off[1:] = np.cumsum([len(c) for c in contexts])
+        ids = np.concatenate([np.asarray(c, dtype=np.int32) for c in contexts]) if off[-1] else np.zeros(1, np.int32)
+        off_d = torch.from_numpy(off.view(np.int32)).to(dev)
+        ids_d = torch.from_numpy(ids).to(dev)
+        dr = torch.full((n, max(max_draft, 1)), -7, dtype=torch.int32, device=dev)
+        ln = torch.full((n,), 999, dtype=torch.int32, device=dev)
+        b = _DBatch()
+        b.n_seq, b.ngram, b.max_draft = n, ngram, max_draft
+        b.ctx_off, b.ctx_ids = _dptr(off_d), _dptr(ids_d)
+        o = _DOut()
+        o.draft, o.draft_len = _dptr(dr), _dptr(ln)
+        self._check(lib().lcs_ngram_draft(self.ctx, C.byref(b), C.byref(o), None))
+        torch.cuda.synchronize()
+        raw = dr.cpu().numpy()[:, :max_draft]
+        lens = ln.cpu().numpy()
+        return [raw[i, :lens[i]].tolist() for i in range(n)], raw
 
     def verify(self, w):
         d = self.upload(w)
