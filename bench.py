@@ -306,6 +306,86 @@ def draft_bench(n_seq: int = 512, ctx_len: int = 4096, ngram: int = 3, max_draft
             "cpu_us_per_batch": cpu_us, "cpu_kind": kind, "cpu_cores": 1, "cpu": cpu_model()}
 
 
+def lmhead_bench(rows: int = 64, vocab: int = 128256, hidden: int = 4096, steps: int = 50,
+                 cpu_seconds: float = 3.0):
+    """The fused lm-head product (lcs_lmhead) at the decode shape of C2
+    (B = 64, V = 128256) with a 4096-wide hidden state: bf16 x and weight,
+    f32 accumulation; timed without and with the f32 logits written, beside
+    the unfused path (torch's bf16 GEMM to bf16 logits, then lcs_verify on
+    them). The product reads the weight once per launch, so HBM bounds it:
+    algorithmic bytes = weight + x + the epilogue's records (written and read
+    once) + the per-row outputs."""
+    import ctypes as C
+    import torch
+
+    from locus_amd import sampler as SM
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randn((rows, hidden), generator=gen, device=dev).to(torch.bfloat16)
+    w = (torch.randn((vocab, hidden), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    s = SM.Sampler(device=0, max_rows=rows, max_vocab=vocab, max_hist=64, max_top=4)
+    stream = torch.cuda.current_stream()
+    h = s.stream_handle(stream)
+    L = SM.lib()
+    am = torch.empty(rows, dtype=torch.int32, device=dev)
+    lz = torch.empty(rows, dtype=torch.float32, device=dev)
+    lg = torch.empty((rows, vocab), dtype=torch.float32, device=dev)
+
+    def timed(fn):
+        for _ in range(5):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps * 1e3
+
+    b = SM._LBatch(rows, vocab, hidden, 0, SM._dptr(x), SM._dptr(w), None)
+    o_fused = SM._LOut(None, 0, SM._dptr(am), SM._dptr(lz), None, None)
+    o_logits = SM._LOut(SM._dptr(lg), vocab, SM._dptr(am), SM._dptr(lz), None, None)
+    us_fused = timed(lambda: L.lcs_lmhead(s.ctx, C.byref(b), C.byref(o_fused), h))
+    us_logits = timed(lambda: L.lcs_lmhead(s.ctx, C.byref(b), C.byref(o_logits), h))
+    # unfused: library GEMM (bf16 logits), then the verify kernels over them
+    lb = torch.empty((rows, vocab), dtype=torch.bfloat16, device=dev)
+    dr = torch.zeros(rows, dtype=torch.int32, device=dev)
+    dlp = torch.empty(rows, dtype=torch.float32, device=dev)
+    acc = torch.empty(rows, dtype=torch.int32, device=dev)
+    vb = SM._VBatch(rows, 1, vocab, SM.LCS_BF16, vocab, SM._dptr(lb), SM._dptr(dr))
+    vo = SM._VOut(SM._dptr(am), SM._dptr(dlp), SM._dptr(acc))
+
+    def unfused():
+        torch.mm(x, w.t(), out=lb)
+        L.lcs_verify(s.ctx, C.byref(vb), C.byref(vo), h)
+    us_unfused = timed(unfused)
+    us_gemm = timed(lambda: torch.mm(x, w.t(), out=lb))
+    s.close()
+    nblocks = (vocab + 255) // 256
+    alg = vocab * hidden * 2 + rows * hidden * 2 + 2 * rows * nblocks * 16 + rows * 8
+    alg_logits = alg + rows * vocab * 4
+    # CPU: a float32 product of the same shape (numpy's BLAS, all cores) on a
+    # sample of the vocabulary, scaled to the whole
+    xc = x.float().cpu().numpy()
+    cols = min(vocab, 8192)
+    wc = w[:cols].float().cpu().numpy()
+    t0, reps = time.perf_counter(), 0
+    while time.perf_counter() - t0 < cpu_seconds:
+        np.dot(xc, wc.T)
+        reps += 1
+    cpu_us = (time.perf_counter() - t0) / reps * 1e6 * vocab / cols
+    return {"workload": f"lm-head {rows} x {vocab} x {hidden} bf16 (f32 accumulation)",
+            "us_fused": us_fused, "us_with_logits": us_logits,
+            "us_unfused_gemm_plus_verify": us_unfused, "us_library_gemm_alone": us_gemm,
+            "roofline": {"bound": "hbm", "algorithmic_bytes": alg,
+                         "achieved": alg / (us_fused * 1e-6) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": alg / (us_fused * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                         "with_logits_frac": alg_logits / (us_logits * 1e-6) / 1e9 / HBM_PEAK_GBS},
+            "tflops_fused": 2.0 * rows * vocab * hidden / (us_fused * 1e-6) / 1e12,
+            "cpu_us_f32_product": cpu_us, "cpu_kind": "numpy f32 matmul", "cpu": cpu_model(),
+            "cpu_threads": int(os.environ.get("OMP_NUM_THREADS", "0") or 0)}
+
+
 def copy_calibration(mib: int, reps: int = 20):
     """A plain device copy of known size (for scaling FETCH_SIZE/WRITE_SIZE:
     each dispatch must read and write exactly `mib` MiB)."""
@@ -433,7 +513,12 @@ def main():
                     help="only time the host JSON allow-mask at V=128256 (CPU)")
     ap.add_argument("--draft-bench", action="store_true",
                     help="only time batched n-gram drafts on the device against the CPU reference")
+    ap.add_argument("--lmhead-bench", action="store_true",
+                    help="only time the fused lm-head product at the decode shape")
     args = ap.parse_args()
+    if args.lmhead_bench:
+        print(json.dumps(lmhead_bench()))
+        return
     if args.mask_bench:
         print(json.dumps(mask_bench()))
         return

@@ -151,6 +151,33 @@ typedef struct lcs_draft_out {
     uint32_t* draft_len;       /* n_seq: the draft's length (0..max_draft) */
 } lcs_draft_out;
 
+/* The lm-head product with the sampler's first statistics in its epilogue:
+ * logits = x w^T for bf16 x (rows x hidden, the normed hidden states) and w
+ * (vocab x hidden, the output weight), accumulated in f32 - the reference's
+ * matvec(out_w, norm(x)) per token (src/locus/model/llama.cpp:512-513,
+ * 754-761). From the epilogue, without re-reading the logits: each row's
+ * argmax (llama.cpp:1237-1245) and log-normaliser, the log-probability of a
+ * draft token (logprobs_from with chosen = draft, sampling.cpp:150-170) and
+ * each sequence's acceptance length (engine.cpp:357-383). */
+typedef struct lcs_lmhead_batch {
+    uint32_t rows;             /* hidden vectors, <= the context's max_rows */
+    uint32_t vocab;            /* <= the context's max_vocab */
+    uint32_t hidden;           /* multiple of 64 */
+    uint32_t rows_per_seq;     /* 1..64 rows per sequence (accept_len), or 0 */
+    const void* x;             /* rows x hidden bf16, 16-byte aligned */
+    const void* w;             /* vocab x hidden bf16, 16-byte aligned */
+    const int32_t* draft;      /* rows, or NULL: the token whose logprob each row reports */
+} lcs_lmhead_batch;
+
+typedef struct lcs_lmhead_out {
+    float* logits;             /* rows x ld_logits f32, or NULL: not written */
+    uint64_t ld_logits;        /* elements between rows of logits (>= vocab) */
+    int32_t* argmax_ids;       /* rows */
+    float* log_z;              /* rows: log sum exp of the row, or NULL */
+    float* draft_lp;           /* rows (when draft != NULL), 0 for ids outside [0, vocab) */
+    uint32_t* accept_len;      /* rows / rows_per_seq, or NULL */
+} lcs_lmhead_out;
+
 /* Number of usable gfx950 devices (0 when none). Replaces the runtime probe
  * that sets Backend::available (registry.cpp:148-223, cuda_stub.cpp:29). */
 int lcs_probe(int* n_devices);
@@ -187,6 +214,11 @@ int lcs_verify(lcs_ctx* ctx, const lcs_verify_batch* batch, const lcs_verify_out
  * engine.cpp:328-329 (speculative.cpp:7-28) when contexts live on the device.
  * Drafts feed lcs_verify. Allocates nothing. */
 int lcs_ngram_draft(lcs_ctx* ctx, const lcs_draft_batch* batch, const lcs_draft_out* out, void* stream);
+
+/* The fused lm-head product (see lcs_lmhead_batch); no counterpart call in
+ * the reference, which computes the logits with matvec and reads them again
+ * in argmax / logprobs_from. Allocates nothing. */
+int lcs_lmhead(lcs_ctx* ctx, const lcs_lmhead_batch* batch, const lcs_lmhead_out* out, void* stream);
 
 /* Sticky device-side status bits of ctx (LCS_STATUS_*), set by kernels that
  * met an input they could not serve (the affected rows get id -1). Blocking:

@@ -19,6 +19,7 @@ hipError_t launch_general(const SampleArgs& a, hipStream_t st);
 hipError_t launch_nucleus(const SampleArgs& a, hipStream_t st);
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t st);
 hipError_t launch_draft(const DraftArgs& a, hipStream_t st);
+hipError_t launch_lmhead(const LmArgs& a, hipStream_t st);
 }  // namespace lcs
 
 struct lcs_ctx {
@@ -31,6 +32,7 @@ struct lcs_ctx {
     float* d_raw = nullptr;
     float* d_pen = nullptr;
     uint32_t* status = nullptr;
+    lcs::LmRec* lmrecs = nullptr;   // lm-head epilogue records: max_rows x blocks of kLmCols
     // nucleus path workspace (kNucRows rows at a time)
     lcs::NucRow* nrow = nullptr;
     uint32_t* nh_cnt = nullptr;
@@ -130,6 +132,8 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t 
         (e = hipMalloc(&c->d_raw, d_elems * 4)) != hipSuccess ||
         (e = hipMalloc(&c->d_pen, d_elems * 4)) != hipSuccess ||
         (e = hipMalloc(&c->status, 4)) != hipSuccess ||
+        (e = hipMalloc(&c->lmrecs, (size_t)max_rows * ((max_vocab + lcs::kLmCols - 1) / lcs::kLmCols) *
+                                       sizeof(lcs::LmRec))) != hipSuccess ||
         (e = hipMalloc(&c->nrow, nuc_rows * sizeof(lcs::NucRow))) != hipSuccess ||
         (e = hipMalloc(&c->nh_cnt, nh_elems * 4)) != hipSuccess ||
         (e = hipMalloc(&c->nh_mass, nh_elems * 8)) != hipSuccess ||
@@ -157,6 +161,7 @@ void lcs_destroy(lcs_ctx* c) {
     (void)hipFree(c->nlist);
     (void)hipFree(c->d_pen);
     (void)hipFree(c->status);
+    (void)hipFree(c->lmrecs);
     delete c;
 }
 
@@ -438,6 +443,49 @@ int lcs_ngram_draft(lcs_ctx* c, const lcs_draft_batch* b, const lcs_draft_out* o
     DeviceGuard g(c->device);
     const hipError_t e = lcs::launch_draft(a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(c, e, "draft kernel launch");
+    return LCS_OK;
+}
+
+int lcs_lmhead(lcs_ctx* c, const lcs_lmhead_batch* b, const lcs_lmhead_out* o, void* stream) {
+    if (!c) return LCS_ERR_INVALID_ARG;
+    if (!b || !o) return fail(c, LCS_ERR_INVALID_ARG, "null lm-head argument");
+    if (b->rows == 0) return LCS_OK;
+    if (!b->x || !b->w || !o->argmax_ids) return fail(c, LCS_ERR_INVALID_ARG, "null x / w / argmax_ids");
+    if ((reinterpret_cast<uintptr_t>(b->x) & 15u) || (reinterpret_cast<uintptr_t>(b->w) & 15u)) {
+        return fail(c, LCS_ERR_INVALID_ARG, "x and w must be 16-byte aligned");
+    }
+    if (b->hidden == 0 || b->hidden % 64 != 0) return fail(c, LCS_ERR_INVALID_ARG, "hidden must be a positive multiple of 64");
+    if (b->vocab == 0) return fail(c, LCS_ERR_INVALID_ARG, "vocab must be positive");
+    if (o->logits && o->ld_logits < b->vocab) return fail(c, LCS_ERR_INVALID_ARG, "ld_logits < vocab");
+    if (b->rows_per_seq > 64 || (b->rows_per_seq && b->rows % b->rows_per_seq)) {
+        return fail(c, LCS_ERR_INVALID_ARG, "rows_per_seq must be 0 or 1..64 and divide rows");
+    }
+    if (b->draft && !o->draft_lp) return fail(c, LCS_ERR_INVALID_ARG, "draft given without draft_lp");
+    if (o->accept_len && (!b->draft || !b->rows_per_seq)) {
+        return fail(c, LCS_ERR_INVALID_ARG, "accept_len needs draft and rows_per_seq");
+    }
+    if (b->rows > c->max_rows || b->vocab > c->max_vocab) {
+        return fail(c, LCS_ERR_CAPACITY, "rows or vocab above the context limits");
+    }
+    lcs::LmArgs a{};
+    a.x = static_cast<const uint16_t*>(b->x);
+    a.w = static_cast<const uint16_t*>(b->w);
+    a.rows = b->rows;
+    a.vocab = b->vocab;
+    a.hidden = b->hidden;
+    a.nblocks = (b->vocab + lcs::kLmCols - 1) / lcs::kLmCols;
+    a.rows_per_seq = b->rows_per_seq;
+    a.ld_logits = o->ld_logits;
+    a.draft = b->draft;
+    a.logits = o->logits;
+    a.argmax_ids = o->argmax_ids;
+    a.log_z = o->log_z;
+    a.draft_lp = b->draft ? o->draft_lp : nullptr;
+    a.accept_len = o->accept_len;
+    a.recs = c->lmrecs;
+    DeviceGuard g(c->device);
+    const hipError_t e = lcs::launch_lmhead(a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(c, e, "lm-head kernel launch");
     return LCS_OK;
 }
 

@@ -170,6 +170,30 @@ struct DraftArgs {
     uint32_t* draft_len;
 };
 
+// lm-head product with the first statistics in its epilogue (lcs_lmhead.hip)
+constexpr uint32_t kLmRows = 64;    // rows per product launch (4 MFMA row tiles)
+constexpr uint32_t kLmCols = 256;   // vocabulary columns per workgroup: one record block
+struct LmRec {                      // per (row, block of kLmCols columns)
+    float max;                      // the block's largest logit
+    uint32_t idx;                   // its first column; bit 31: the block holds the row's draft token
+    float sum;                      // sum of exp(logit - max) over the block
+    float draft;                    // the draft token's logit (when bit 31 of idx is set)
+};
+constexpr uint32_t kLmDraftBit = 0x80000000u;
+struct LmArgs {
+    const uint16_t* x;              // rows x hidden bf16
+    const uint16_t* w;              // vocab x hidden bf16
+    uint32_t rows, vocab, hidden, m0, nblocks, rows_per_seq;
+    uint64_t ld_logits;             // elements between logits rows
+    const int32_t* draft;
+    float* logits;
+    int32_t* argmax_ids;
+    float* log_z;
+    float* draft_lp;
+    uint32_t* accept_len;
+    LmRec* recs;                    // rows x nblocks
+};
+
 // status bits
 constexpr uint32_t kStatusHistCap = 1u;   // a penalty window exceeded the capacity
 constexpr uint32_t kStatusBinCap = 2u;    // selection could not narrow a bin (unexpected)

@@ -1,0 +1,254 @@
+// The lm-head product with the sampler's first statistics in its epilogue,
+// for MI355X (gfx950): logits = X W^T in bf16 on the matrix cores (f32
+// accumulation), and per (row, block of 256 vocabulary columns) the block's
+// argmax (first index), its sum of exponentials against the block max, and
+// the logit of the row's draft token when the block holds it. A per-sequence
+// finalize then gives each row's argmax and log-normaliser, the draft's
+// log-probability and each sequence's acceptance length, so greedy and
+// speculative-verify rows need no second read of the logits (and no logits
+// at all when the caller does not ask for them).
+//
+// Reference: the output projection matvec(out_w, norm(x)) per decode token
+// (src/locus/model/llama.cpp:512-513, batched at 754-761; Ops::matvec,
+// backend/registry.hpp:14-15), then argmax (llama.cpp:1237-1245) and
+// logprobs_from with chosen = draft (sampling.cpp:150-170) per row and the
+// acceptance rule of engine.cpp:357-383 per sequence.
+//
+// Tiling: a workgroup of four waves computes 64 rows x 256 columns; each wave
+// holds 4 x 4 tiles of 16 x 16 (v_mfma_f32_16x16x32_bf16: lane l carries
+// 8 consecutive k of row l % 16 of A, the same k of column l % 16 of B, and
+// returns rows 4 (l / 16) + i of column l % 16 of C). Operands come straight
+// from memory, 16 bytes per lane per fragment: each lane reads 8 consecutive
+// bf16 of an X row and of a W row (W is the K-contiguous vocab-major
+// weight), two k-steps in flight. Every weight byte is read once per launch
+// (the bound for decode batches: the weight matrix dominates the traffic).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "lcs_device.hpp"
+#include "lcs_internal.hpp"
+
+namespace lcs {
+
+namespace {
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kLmThreads = 256;
+constexpr float kL2E = 1.4426950408889634f;
+
+__device__ __forceinline__ bf16x8 ld_frag(const uint16_t* p) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
+}
+
+// Lanes 16q .. 16q+15 (a DPP row) end holding the row's minimum of the
+// 64-bit keys (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror).
+__device__ __forceinline__ uint64_t row16_min_u64(uint64_t v) {
+    v = u64_min(v, dpp_u64<0xB1>(~0ull, v));
+    v = u64_min(v, dpp_u64<0x4E>(~0ull, v));
+    v = u64_min(v, dpp_u64<0x141>(~0ull, v));
+    v = u64_min(v, dpp_u64<0x140>(~0ull, v));
+    return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __int_as_float(dpp_i<0xB1>(0, __float_as_int(v)));
+    v += __int_as_float(dpp_i<0x4E>(0, __float_as_int(v)));
+    v += __int_as_float(dpp_i<0x141>(0, __float_as_int(v)));
+    v += __int_as_float(dpp_i<0x140>(0, __float_as_int(v)));
+    return v;
+}
+}  // namespace
+
+// a.m0: first row of this launch's chunk (<= kLmRows rows)
+__global__ __launch_bounds__(kLmThreads, 2) void lmhead_kernel(LmArgs a) {
+    __shared__ uint64_t pkey[kLmThreads / kWave][kLmRows];   // per wave: row's best (rank key)
+    __shared__ float psum[kLmThreads / kWave][kLmRows];
+    __shared__ float pdraft[kLmRows];
+    __shared__ uint32_t pfound[kLmRows];
+    const uint32_t tid = tid_x();
+    const int lane = lane_id(), wv = (int)(tid / kWave);
+    const uint32_t nb = wg_x();
+    const uint32_t K = a.hidden, V = a.vocab;
+    const uint32_t m0 = a.m0, mrows = min((uint32_t)kLmRows, a.rows - m0);
+    const uint32_t nw = nb * (uint32_t)kLmCols + (uint32_t)wv * 64u;   // this wave's first column
+    const uint32_t lr = (uint32_t)lane & 15u, kq = (uint32_t)lane >> 4;
+    // fragment rows: A rows past the chunk and B columns past the vocabulary
+    // read row 0 / column 0 (in bounds) and are masked in the epilogue
+    const uint16_t* xr[4];
+    const uint16_t* wr[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t r = (uint32_t)t * 16u + lr;
+        xr[t] = a.x + (uint64_t)(m0 + (r < mrows ? r : 0u)) * K + kq * 8u;
+        const uint32_t c = nw + (uint32_t)t * 16u + lr;
+        wr[t] = a.w + (uint64_t)(c < V ? c : 0u) * K + kq * 8u;
+    }
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    bf16x8 a0[4], b0[4], a1[4], b1[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) { a0[t] = ld_frag(xr[t]); b0[t] = ld_frag(wr[t]); }
+    for (uint32_t k0 = 0; k0 < K; k0 += 64u) {   // (K is a multiple of 64)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) { a1[t] = ld_frag(xr[t] + k0 + 32u); b1[t] = ld_frag(wr[t] + k0 + 32u); }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[i], b0[j], acc[i][j], 0, 0, 0);
+        if (k0 + 64u < K) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) { a0[t] = ld_frag(xr[t] + k0 + 64u); b0[t] = ld_frag(wr[t] + k0 + 64u); }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[i], b1[j], acc[i][j], 0, 0, 0);
+    }
+
+    // ---- epilogue: acc[i][j][e] is row 16 i + 4 kq + e, column nw + 16 j + lr
+    if (tid < kLmRows) { pdraft[tid] = 0.0f; pfound[tid] = 0u; }
+    if (a.logits) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t r = (uint32_t)i * 16u + kq * 4u + (uint32_t)e;
+                if (r < mrows) {
+                    float* out = a.logits + (uint64_t)(m0 + r) * a.ld_logits;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t c = nw + (uint32_t)j * 16u + lr;
+                        if (c < V) out[c] = acc[i][j][e];
+                    }
+                }
+            }
+    }
+    __syncthreads();   // (pdraft initialised)
+    // per row: this wave's best (value, first column) over its 64 columns, as
+    // a rank key (value descending, column ascending)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t r = (uint32_t)i * 16u + kq * 4u + (uint32_t)e;
+            uint64_t best = ~0ull;
+            const int32_t dr = (a.draft && r < mrows) ? a.draft[m0 + r] : -1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t c = nw + (uint32_t)j * 16u + lr;
+                if (c < V) {
+                    const uint64_t k = rank_key(acc[i][j][e], c);
+                    best = k < best ? k : best;
+                    if ((int32_t)c == dr) { pdraft[r] = acc[i][j][e]; pfound[r] = kLmDraftBit; }
+                }
+            }
+            best = row16_min_u64(best);
+            if (lr == 0u) pkey[wv][r] = best;
+        }
+    __syncthreads();
+    // the block's max per row (all four waves' keys), then sums of exp(v - max)
+    float bmax[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t r = (uint32_t)i * 16u + kq * 4u + (uint32_t)e;
+            const uint64_t k = u64_min(u64_min(pkey[0][r], pkey[1][r]), u64_min(pkey[2][r], pkey[3][r]));
+            bmax[i][e] = rank_val(k);
+        }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t r = (uint32_t)i * 16u + kq * 4u + (uint32_t)e;
+            // (v - max) first: it is exact or nearly so, where a fused
+            // v * log2(e) - max * log2(e) would carry the rounding of the
+            // large product max * log2(e) into every term
+            const float bm = bmax[i][e];
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t c = nw + (uint32_t)j * 16u + lr;
+                if (c < V) s += __builtin_amdgcn_exp2f((acc[i][j][e] - bm) * kL2E);
+            }
+            s = row16_sum(s);
+            if (lr == 0u) psum[wv][r] = s;
+        }
+    __syncthreads();
+    // one record per row of the chunk
+    if (tid < mrows) {
+        const uint32_t r = tid;
+        const uint64_t k = u64_min(u64_min(pkey[0][r], pkey[1][r]), u64_min(pkey[2][r], pkey[3][r]));
+        LmRec rec;
+        rec.max = rank_val(k);
+        rec.idx = rank_idx(k) | pfound[r];
+        rec.sum = (psum[0][r] + psum[1][r]) + (psum[2][r] + psum[3][r]);
+        rec.draft = pdraft[r];
+        a.recs[(uint64_t)(m0 + r) * a.nblocks + nb] = rec;
+    }
+}
+
+// One workgroup per sequence (rows_per_seq rows; a row is its own sequence
+// when rows_per_seq is 0): wave w merges rows w, w + 4, ... from their
+// blocks' records (the kernel boundary orders them after the product).
+__global__ __launch_bounds__(kLmThreads) void lmhead_fin(LmArgs a) {
+    __shared__ int32_t am[64];
+    const uint32_t tid = tid_x();
+    const int lane = lane_id(), wv = (int)(tid / kWave);
+    const uint32_t R = a.rows_per_seq ? a.rows_per_seq : 1u;
+    const uint32_t seq = wg_x();
+    for (uint32_t j = (uint32_t)wv; j < R; j += kLmThreads / kWave) {
+        const uint32_t row = seq * R + j;
+        const LmRec* rr = a.recs + (uint64_t)row * a.nblocks;
+        uint64_t best = ~0ull;
+        for (uint32_t b = (uint32_t)lane; b < a.nblocks; b += kWave) {
+            const uint64_t k = rank_key(rr[b].max, rr[b].idx & ~kLmDraftBit);
+            best = k < best ? k : best;
+        }
+        best = wave_min_u64(best);
+        const float M = rank_val(best);
+        double z = 0.0;
+        float dl = 0.0f;
+        bool has = false;
+        for (uint32_t b = (uint32_t)lane; b < a.nblocks; b += kWave) {
+            const LmRec rc = rr[b];
+            z += (double)rc.sum * (double)__builtin_amdgcn_exp2f((rc.max - M) * kL2E);
+            if (rc.idx & kLmDraftBit) { dl = rc.draft; has = true; }
+        }
+        z = wave_sum(z);
+        const uint64_t own = ballot(has);
+        dl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dl), own ? __builtin_ctzll(own) : 0));
+        const double log_z = log_f64(z) + (double)M;
+        if (lane == 0) {
+            a.argmax_ids[row] = (int32_t)rank_idx(best);
+            if (a.log_z) a.log_z[row] = (float)log_z;
+            if (a.draft_lp) a.draft_lp[row] = own ? (float)((double)dl - log_z) : 0.0f;
+            am[j] = (int32_t)rank_idx(best);
+        }
+    }
+    if (!a.accept_len || !a.draft) return;
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t acc = 0;
+        while (acc < R && am[acc] == a.draft[seq * R + acc]) ++acc;
+        a.accept_len[seq] = acc;
+    }
+}
+
+hipError_t launch_lmhead(const LmArgs& a0, hipStream_t st) {
+    LmArgs a = a0;
+    for (uint32_t m0 = 0; m0 < a0.rows; m0 += kLmRows) {
+        a.m0 = m0;
+        hipLaunchKernelGGL(lmhead_kernel, dim3(a.nblocks), dim3(kLmThreads), 0, st, a);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    const uint32_t nseq = a0.rows_per_seq ? a0.rows / a0.rows_per_seq : a0.rows;
+    hipLaunchKernelGGL(lmhead_fin, dim3(nseq), dim3(kLmThreads), 0, st, a0);
+    return hipGetLastError();
+}
+
+}  // namespace lcs

@@ -39,10 +39,13 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
     const float NEG = -__builtin_huge_valf();
 
     // per lane: running max om, the first group bg that reached it, and
-    // os = sum exp(v - om) (f32 group sums of exp2 accumulated in f64)
+    // os = sum exp(v - om) (f32 group sums of exp2 accumulated in f64). The
+    // terms are 2^fma(v, K, b) with b = RN(-om K): they share the exponent
+    // error e_b = om K + b (exact, by an fma), which corr = 2^-e_b takes out
+    // (without it a logit of magnitude 100 would cost ~5e-6 in log z)
     const uint32_t ng = (V + G - 1) / G;
-    float om = NEG;
-    double os = 0.0;
+    float om = NEG, b = 0.0f;
+    double os = 0.0, corr = 1.0;
     uint32_t bg = 0xffffffffu;
     for (uint32_t g0 = 0; g0 < ng; g0 += NT * U) {
         uint4 r[U];
@@ -68,9 +71,10 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
                 os = om == NEG ? 0.0 : os * (double)__builtin_amdgcn_exp2f((om - gm) * kL2E);
                 om = gm;
                 bg = gi;
+                b = -om * kL2E;
+                corr = (double)__builtin_amdgcn_exp2f(-fmaf(om, kL2E, b));
             }
             if (om != NEG) {
-                const float b = -om * kL2E;
                 float c[G];
 #pragma unroll
                 for (int k = 0; k < G; ++k) c[k] = __builtin_amdgcn_exp2f(fmaf(v[k], kL2E, b));
@@ -78,7 +82,7 @@ __global__ __launch_bounds__(kVerifyThreads) void verify_kernel(VerifyArgs a) {
                 for (int w = G / 2; w >= 1; w /= 2)
 #pragma unroll
                     for (int k = 0; k < w; ++k) c[k] += c[k + w];
-                os += (double)c[0];
+                os += (double)c[0] * corr;
             }
         }
     }

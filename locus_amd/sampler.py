@@ -59,6 +59,16 @@ class _DOut(C.Structure):
     _fields_ = [("draft", _P), ("draft_len", _P)]
 
 
+class _LBatch(C.Structure):
+    _fields_ = [("rows", C.c_uint32), ("vocab", C.c_uint32), ("hidden", C.c_uint32),
+                ("rows_per_seq", C.c_uint32), ("x", _P), ("w", _P), ("draft", _P)]
+
+
+class _LOut(C.Structure):
+    _fields_ = [("logits", _P), ("ld_logits", C.c_uint64), ("argmax_ids", _P), ("log_z", _P),
+                ("draft_lp", _P), ("accept_len", _P)]
+
+
 class SamplerError(RuntimeError):
     pass
 
@@ -87,6 +97,8 @@ def lib():
         L.lcs_verify.argtypes = [_P, C.POINTER(_VBatch), C.POINTER(_VOut), _P]
         L.lcs_ngram_draft.restype = C.c_int
         L.lcs_ngram_draft.argtypes = [_P, C.POINTER(_DBatch), C.POINTER(_DOut), _P]
+        L.lcs_lmhead.restype = C.c_int
+        L.lcs_lmhead.argtypes = [_P, C.POINTER(_LBatch), C.POINTER(_LOut), _P]
         L.lcs_last_error.restype = C.c_char_p
         L.lcs_last_error.argtypes = [_P]
         L.lcs_get_status.restype = C.c_int
@@ -361,6 +373,49 @@ class Sampler:
         raw = dr.cpu().numpy()[:, :max_draft]
         lens = ln.cpu().numpy()
         return [raw[i, :lens[i]].tolist() for i in range(n)], raw
+
+    def lmhead_dev(self, x, w, out, draft=None, rows_per_seq: int = 0, stream=None):
+        """The fused lm-head product (lcs_lmhead) on device tensors: x (rows,
+        hidden) and w (vocab, hidden) bf16, contiguous; `out` holds any of
+        "logits" (rows, >= vocab) f32, "argmax_ids", "log_z", "draft_lp",
+        "accept_len" (missing keys are not written; argmax_ids is required)."""
+        torch = self.torch
+        if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+            raise SamplerError("x and w must be bfloat16")
+        if not (x.is_contiguous() and w.is_contiguous()):
+            raise SamplerError("x and w must be contiguous")
+        b = _LBatch()
+        b.rows, b.hidden = x.shape
+        b.vocab = w.shape[0]
+        if w.shape[1] != b.hidden:
+            raise SamplerError("x and w disagree on hidden")
+        b.rows_per_seq = rows_per_seq
+        b.x, b.w, b.draft = _dptr(x), _dptr(w), _dptr(draft)
+        o = _LOut()
+        lg = out.get("logits")
+        if lg is not None:
+            if lg.dtype != torch.float32 or lg.stride(1) != 1:
+                raise SamplerError("logits must be f32 with unit column stride")
+            o.logits, o.ld_logits = _dptr(lg), lg.stride(0)
+        for k in ("argmax_ids", "log_z", "draft_lp", "accept_len"):
+            setattr(o, k, _dptr(out.get(k)))
+        self._keep = (b, o)
+        self._check(lib().lcs_lmhead(self.ctx, C.byref(b), C.byref(o),
+                                     _stream_handle(torch, stream)))
+
+    def alloc_lmhead_out(self, rows: int, vocab: int, logits: bool = True, draft: bool = False,
+                         n_seq: int = 0):
+        torch = self.torch
+        dev = torch.device("cuda", self.device)
+        out = {"argmax_ids": torch.full((rows,), -7, dtype=torch.int32, device=dev),
+               "log_z": torch.full((rows,), -7.0, dtype=torch.float32, device=dev)}
+        if logits:
+            out["logits"] = torch.full((rows, vocab), -7.0, dtype=torch.float32, device=dev)
+        if draft:
+            out["draft_lp"] = torch.full((rows,), -7.0, dtype=torch.float32, device=dev)
+        if n_seq:
+            out["accept_len"] = torch.full((n_seq,), 99, dtype=torch.int32, device=dev)
+        return out
 
     def verify(self, w):
         d = self.upload(w)

@@ -25,7 +25,7 @@ def declared_functions(prefix="lcs_", header="*.h"):
 def test_headers_declare_the_abi():
     names = declared_functions()
     for n in ["lcs_probe", "lcs_create", "lcs_destroy", "lcs_sample", "lcs_verify", "lcs_last_error",
-              "lcs_sample_noalloc", "lcs_ngram_draft"]:
+              "lcs_sample_noalloc", "lcs_ngram_draft", "lcs_lmhead"]:
         assert n in names
 
 

@@ -101,6 +101,27 @@ def test_fresh_inputs(sampler, name, rows):
     compare(w, run(sampler, w), O.sample_batch(w, threads=16), f"fresh-{name}")
 
 
+def test_large_magnitude_logits(sampler):
+    """Logits offset by +300: the f32 exp2 sums share an exponent error of up
+    to half an ulp of 300 log2(e) unless it is taken out; logprobs must stay
+    within 1e-5 (sliced, nucleus and verify paths)."""
+    import dataclasses
+    off = np.float32(300.0)
+    w2 = W.make("c2", rows=32, set_index=5)
+    w2 = dataclasses.replace(w2, logits=w2.logits + off)
+    compare(w2, run(sampler, w2), O.sample_batch(w2, threads=16), "offset-c2")
+    w3 = W.make("c3", rows=16, set_index=5)
+    w3 = dataclasses.replace(w3, logits=w3.logits + off, want_logprobs=True, n_top=3)
+    compare(w3, run(sampler, w3), O.sample_batch(w3, threads=16), "offset-c3")
+    w5 = W.make("c5", rows=64, set_index=5)
+    w5 = dataclasses.replace(w5, dtype="f32", logits=W.bf16_to_f32(w5.logits) + off)
+    g = sampler.verify(w5)
+    am, lp, acc = O.verify(w5, threads=16)
+    assert np.array_equal(g["argmax_ids"], am)
+    assert np.abs(g["draft_lp"] - lp).max() <= LOGPROB_TOL
+    assert np.array_equal(g["accept_len"].astype(np.uint32), acc)
+
+
 def test_full_size_c2(sampler):
     say("full c2")
     w = W.make("c2")
