@@ -172,7 +172,8 @@ struct DraftArgs {
 
 // lm-head product with the first statistics in its epilogue (lcs_lmhead.hip)
 constexpr uint32_t kLmRows = 64;    // rows per product launch (4 MFMA row tiles)
-constexpr uint32_t kLmCols = 256;   // vocabulary columns per workgroup: one record block
+constexpr uint32_t kLmWaveTiles = 4;                // 16-column MFMA tiles per wave
+constexpr uint32_t kLmCols = 4 * 16 * kLmWaveTiles;  // vocabulary columns per workgroup: one record block
 struct LmRec {                      // per (row, block of kLmCols columns)
     float max;                      // the block's largest logit
     uint32_t idx;                   // its first column; bit 31: the block holds the row's draft token

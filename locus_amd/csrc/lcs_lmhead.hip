@@ -17,11 +17,17 @@
 // Tiling: a workgroup of four waves computes 64 rows x 256 columns; each wave
 // holds 4 x 4 tiles of 16 x 16 (v_mfma_f32_16x16x32_bf16: lane l carries
 // 8 consecutive k of row l % 16 of A, the same k of column l % 16 of B, and
-// returns rows 4 (l / 16) + i of column l % 16 of C). Operands come straight
-// from memory, 16 bytes per lane per fragment: each lane reads 8 consecutive
-// bf16 of an X row and of a W row (W is the K-contiguous vocab-major
-// weight), two k-steps in flight. Every weight byte is read once per launch
-// (the bound for decode batches: the weight matrix dominates the traffic).
+// returns rows 4 (l / 16) + i of column l % 16 of C). The weight (W, the
+// K-contiguous vocab-major matrix) comes straight from HBM into registers,
+// 16 bytes per lane per fragment, 128 contiguous bytes of each of a wave's
+// 64 rows per k-step, three k-steps in flight; x (shared by the four waves)
+// is staged through LDS. Every weight byte is read once per launch of up to
+// 64 rows: the weight stream is the bound for decode batches.
+//
+// Measured (64 x 128256 x 4096, MI355X): the fused launch takes about as long
+// as the library GEMM alone writing bf16 logits, and less than that GEMM
+// followed by the verify kernels. Shapes whose block count lands just above
+// the 512 resident workgroups (two per CU) pay a tail round.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -36,6 +42,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kLmThreads = 256;
 constexpr float kL2E = 1.4426950408889634f;
+constexpr int kDepth = 3;   // weight k-steps in flight ahead of the product
+constexpr int kKC = 2;      // 32-wide k chunks per step: 128 bytes of each weight row
 
 __device__ __forceinline__ bf16x8 ld_frag(const uint16_t* p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
@@ -70,42 +78,107 @@ __global__ __launch_bounds__(kLmThreads, 2) void lmhead_kernel(LmArgs a) {
     const uint32_t nb = wg_x();
     const uint32_t K = a.hidden, V = a.vocab;
     const uint32_t m0 = a.m0, mrows = min((uint32_t)kLmRows, a.rows - m0);
-    const uint32_t nw = nb * (uint32_t)kLmCols + (uint32_t)wv * 64u;   // this wave's first column
+    constexpr int WC = (int)kLmWaveTiles;
+    const uint32_t nw = nb * (uint32_t)kLmCols + (uint32_t)wv * (16u * WC);   // this wave's first column
     const uint32_t lr = (uint32_t)lane & 15u, kq = (uint32_t)lane >> 4;
     // fragment rows: A rows past the chunk and B columns past the vocabulary
     // read row 0 / column 0 (in bounds) and are masked in the epilogue
     const uint16_t* xr[4];
-    const uint16_t* wr[4];
+    const uint16_t* wr[WC];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         const uint32_t r = (uint32_t)t * 16u + lr;
         xr[t] = a.x + (uint64_t)(m0 + (r < mrows ? r : 0u)) * K + kq * 8u;
+    }
+#pragma unroll
+    for (int t = 0; t < WC; ++t) {
         const uint32_t c = nw + (uint32_t)t * 16u + lr;
         wr[t] = a.w + (uint64_t)(c < V ? c : 0u) * K + kq * 8u;
     }
-    f32x4 acc[4][4];
+    f32x4 acc[4][WC];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    bf16x8 a0[4], b0[4], a1[4], b1[4];
+        for (int j = 0; j < WC; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // k-steps of 32 kKC wide. The weight fragments (the HBM stream, each
+    // wave its own columns) are software-pipelined kDepth steps deep in
+    // registers: those of step s + kDepth are requested while step s
+    // multiplies (a ring of kDepth + 1 buffers). The x fragments are common
+    // to the four waves: wave w fetches row tile w of step s + 1 during step
+    // s and stores it in an LDS double buffer (fragment-major, lane l's
+    // 16 bytes at l * 16, so reads and writes are conflict-free), from which
+    // every wave reads its A operands after the step's barrier. Every load is
+    // unconditional (steps past the end re-read the last one). Each
+    // workgroup starts at its own k-step (rot) and wraps round, so that the
+    // workgroups in flight do not all read the same offset of their rows.
+    const uint32_t nsteps = K / (32u * kKC);
+    const uint32_t rot = nb % nsteps;
+    auto koff = [&](uint32_t st) -> uint32_t {
+        uint32_t q = (st < nsteps ? st : nsteps - 1u) + rot;
+        q = q >= nsteps ? q - nsteps : q;
+        return q * 32u * kKC;
+    };
+    constexpr int NB = kDepth + 1;
+    constexpr uint32_t kXFrag = kWave * 16u;            // bytes per fragment
+    constexpr uint32_t kXBuf = 4u * kKC * kXFrag;       // bytes per step
+    __shared__ __attribute__((aligned(16))) unsigned char xs[2 * kXBuf];
+    const uint16_t* xw = xr[wv];                        // this wave's x row tile
+    bf16x8 bw[NB][kKC][WC], xv[kKC], af[kKC][4];
+    auto load_w = [&](int buf, uint32_t st) {
+        const uint32_t ko = koff(st);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) { a0[t] = ld_frag(xr[t]); b0[t] = ld_frag(wr[t]); }
-    for (uint32_t k0 = 0; k0 < K; k0 += 64u) {   // (K is a multiple of 64)
+        for (int c = 0; c < kKC; ++c)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) { a1[t] = ld_frag(xr[t] + k0 + 32u); b1[t] = ld_frag(wr[t] + k0 + 32u); }
+            for (int t = 0; t < WC; ++t) bw[buf][c][t] = ld_frag(wr[t] + ko + 32u * c);
+    };
+    auto load_x = [&](uint32_t st) {
+        const uint32_t ko = koff(st);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int c = 0; c < kKC; ++c) xv[c] = ld_frag(xw + ko + 32u * c);
+    };
+    auto put_x = [&](uint32_t st) {
+        unsigned char* b = xs + (st & 1u) * kXBuf + (uint32_t)lane * 16u;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[i], b0[j], acc[i][j], 0, 0, 0);
-        if (k0 + 64u < K) {
+        for (int c = 0; c < kKC; ++c)
+            *reinterpret_cast<bf16x8*>(b + ((uint32_t)wv * kKC + c) * kXFrag) = xv[c];
+    };
+    auto get_x = [&](uint32_t st) {
+        const unsigned char* b = xs + (st & 1u) * kXBuf + (uint32_t)lane * 16u;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) { a0[t] = ld_frag(xr[t] + k0 + 64u); b0[t] = ld_frag(wr[t] + k0 + 64u); }
-        }
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+            for (int c = 0; c < kKC; ++c)
+                af[c][t] = *reinterpret_cast<const bf16x8*>(b + ((uint32_t)t * kKC + c) * kXFrag);
+    };
+    auto step = [&](int u, uint32_t st) {
+        load_x(st + 1u);
+        load_w((u + kDepth) % NB, st + kDepth);
+        get_x(st);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[i], b1[j], acc[i][j], 0, 0, 0);
+        for (int c = 0; c < kKC; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < WC; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[c][i], bw[u][c][j], acc[i][j], 0, 0, 0);
+        put_x(st + 1u);
+        __syncthreads();
+    };
+    load_x(0u);
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u) load_w(u, (uint32_t)u);
+    put_x(0u);
+    __syncthreads();
+    const uint32_t nfull = nsteps / NB * NB;
+    for (uint32_t s0 = 0; s0 < nfull; s0 += NB) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) step(u, s0 + (uint32_t)u);
+    }
+    // the remaining steps (fewer than NB): their weights were requested by
+    // the loop's last round (or the prologue) into buffers 0, 1, ...
+#pragma unroll
+    for (int u = 0; u < NB - 1; ++u) {
+        if (nfull + (uint32_t)u < nsteps) step(u, nfull + (uint32_t)u);
     }
 
     // ---- epilogue: acc[i][j][e] is row 16 i + 4 kq + e, column nw + 16 j + lr
@@ -119,7 +192,7 @@ __global__ __launch_bounds__(kLmThreads, 2) void lmhead_kernel(LmArgs a) {
                 if (r < mrows) {
                     float* out = a.logits + (uint64_t)(m0 + r) * a.ld_logits;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
+                    for (int j = 0; j < WC; ++j) {
                         const uint32_t c = nw + (uint32_t)j * 16u + lr;
                         if (c < V) out[c] = acc[i][j][e];
                     }
@@ -137,7 +210,7 @@ __global__ __launch_bounds__(kLmThreads, 2) void lmhead_kernel(LmArgs a) {
             uint64_t best = ~0ull;
             const int32_t dr = (a.draft && r < mrows) ? a.draft[m0 + r] : -1;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < WC; ++j) {
                 const uint32_t c = nw + (uint32_t)j * 16u + lr;
                 if (c < V) {
                     const uint64_t k = rank_key(acc[i][j][e], c);
@@ -170,7 +243,7 @@ __global__ __launch_bounds__(kLmThreads, 2) void lmhead_kernel(LmArgs a) {
             const float bm = bmax[i][e];
             float s = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < WC; ++j) {
                 const uint32_t c = nw + (uint32_t)j * 16u + lr;
                 if (c < V) s += __builtin_amdgcn_exp2f((acc[i][j][e] - bm) * kL2E);
             }
