@@ -5,22 +5,24 @@
 //
 // Each pass cuts a row into `slices` workgroups of 256 threads (one HBM read
 // of <= 8192 logits each, 32 per thread in registers), as the sliced kernel
-// does. Every workgroup publishes a record; the row's last-arriving
-// workgroup combines them. No workgroup ever waits for another.
+// does. Every workgroup publishes a record; a per-row finalize kernel (one
+// workgroup per row, launched after the pass on the same stream, so the
+// kernel boundary orders the records before its reads) combines them. No
+// workgroup ever waits for another.
 //
 //   A  nuc_stats:  penalties and the constraint (sampling.cpp:16-41, 70-86);
 //                  the raw max, log-normaliser and top-n (logprobs_from,
 //                  sampling.cpp:150-190); the penalised candidate max (the
-//                  reference's maxl) and min. The last arrival writes the
-//                  row state and the top-n logprobs.
+//                  reference's maxl) and min. The row's finalize writes the
+//                  row state and the top-n logprobs (nuc_stats_fin).
 //   B  nuc_hist:   the reference's weights exp((double)((p - maxl) * inv_t))
 //                  (sampling.cpp:101-109) binned by the tempered offset into
-//                  kNucBins bins (counts, f64 masses). The last arrival
+//                  kNucBins bins (counts, f64 masses). The row's finalize
 //                  merges the row's histograms and plans the few bin ranges
 //                  that can hold the top-p crossing, the min-p cut and the
 //                  draw (sampling.cpp:113-147).
 //   C  nuc_select: the candidates of those ranges are compacted into a row
-//                  list; the last arrival rebuilds each range's sub-bin
+//                  list; the row's finalize rebuilds each range's sub-bin
 //                  masses, sorts only the decisive sub-bins' candidates (rank
 //                  key: logit, then id) and walks them in the reference's
 //                  order: top-k (the K-th candidate and the mass SK of the
@@ -876,7 +878,7 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
 }
 
 // ========================================================= C: nuc_select ==
-// The select pass's last arrival: exact decisions over the compacted ranges.
+// The select pass's row finalize: exact decisions over the compacted ranges.
 // Every thread of the workgroup calls it, with the kernel arguments staged
 // in g_nuc.l.args; out of line so that its live values do not crowd the
 // compaction pass.
@@ -898,7 +900,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     const uint32_t nrg = nr->nr;
     const float inv_t = fdiv(1.0f, P.temperature);
     const uint64_t* list = a.nlist + (uint64_t)wrow * kNucList;
-    // =========== last arrival: exact decisions over the compacted ranges ===
+    // =========== row finalize: exact decisions over the compacted ranges ===
     const uint32_t n_all = ld_dev(&nr->list_n);
     const uint32_t n = min(n_all, kNucList);
     NucRange rg[kNucRanges];

@@ -6,7 +6,7 @@
 // tempered softmax 99-109, top-p 111-123, min-p 124-133, draw 135-147;
 // logprobs_from 150-190) is split so that the logits are read once:
 //
-// * slice_stats: one workgroup per (row, slice of <= 4096 logits), 16 logits
+// * slice_stats: one workgroup per (row, slice of <= 8192 logits), 32 logits
 //   per thread in registers. It applies the row's penalties to its slice,
 //   then writes one record: raw max and sum of exponentials, the slice's
 //   top-n raw logits, its penalised max (and masked max), the normaliser's
