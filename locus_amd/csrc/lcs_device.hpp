@@ -441,31 +441,9 @@ __device__ __forceinline__ uint32_t next_pow2(uint32_t n) {
     return p;
 }
 
-// ------------------------------------------- device-scope word traffic ----
-// Relaxed device-scope atomic loads and stores (written through to, and read
-// from, the device coherence point). The sampler's workgroups never wait on
-// one another: records are written by one kernel and read by the next, and
+// The sampler's workgroups never wait on one another: records are written
+// by one kernel with plain stores and read by the next with plain loads, and
 // the kernel boundary orders them.
-__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
-    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev_f(float* p, float v) { st_dev(reinterpret_cast<uint32_t*>(p), __float_as_uint(v)); }
-__device__ __forceinline__ float ld_dev_f(const float* p) { return __uint_as_float(ld_dev(reinterpret_cast<const uint32_t*>(p))); }
-__device__ __forceinline__ void st_dev_u64(uint64_t* p, uint64_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t ld_dev_u64(const uint64_t* p) {
-    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev_d(double* p, double v) {
-    st_dev_u64(reinterpret_cast<uint64_t*>(p), static_cast<uint64_t>(__double_as_longlong(v)));
-}
-__device__ __forceinline__ double ld_dev_d(const double* p) {
-    return __longlong_as_double(static_cast<long long>(ld_dev_u64(reinterpret_cast<const uint64_t*>(p))));
-}
 __device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
 // ------------------------------------------------------- scalar loads ----
 // Read-only per-row words through the scalar cache (SMEM): waiting for them

@@ -501,7 +501,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
             case 5: hw = pack2(__float_as_uint(mnb), __float_as_uint(mnm)); break;
             default: break;
         }
-        if (lane < 6) st_dev_u64(myrec + lane, hw);
+        if (lane < 6) myrec[lane] = hw;
     } else if (wv == 1) {
         const uint32_t nts = min(ntop, in.len);
         const uint32_t ncc = min(sm.l.ncand, kNucCand);
@@ -512,7 +512,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
                 const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
-                if (e < ncc && rk[c] < nts) st_dev_u64(myrec + nrec::kTop + rk[c], k[c]);
+                if (e < ncc && rk[c] < nts) myrec[nrec::kTop + rk[c]] = k[c];
             }
         }
     }
@@ -540,8 +540,7 @@ __global__ __launch_bounds__(NT) void nuc_stats_fin(SampleArgs a) {
     const uint64_t* my = recs + (mine ? lane : 0) * rec::kWords64;
     NucRow* nr = a.nrow + (row - a.nuc_row0);
     if (wv == 0) {
-        const uint64_t h0 = ld_dev_u64(my + 0), h2 = ld_dev_u64(my + 2), h3 = ld_dev_u64(my + 3),
-                       h4 = ld_dev_u64(my + 4), h5 = ld_dev_u64(my + 5);
+        const uint64_t h0 = my[0], h2 = my[2], h3 = my[3], h4 = my[4], h5 = my[5];
         // a slice whose top-n candidates overflowed sends the row to the exact path
         const bool ovf = ntop && ballot(mine && ((uint32_t)(h0 >> 48) & rec::kFlagCandOverflow));
         const uint32_t na = wave_sum_u(mine ? (uint32_t)h4 : 0u);
@@ -573,10 +572,10 @@ __global__ __launch_bounds__(NT) void nuc_stats_fin(SampleArgs a) {
             nr->list_n = 0u;
         }
     } else if (wv == 1 && want_lp) {
-        const uint64_t h0 = ld_dev_u64(my + 0), h1 = ld_dev_u64(my + 1);
+        const uint64_t h0 = my[0], h1 = my[1];
         uint64_t tk[kTopMax];
 #pragma unroll
-        for (int j = 0; j < (int)kTopMax; ++j) tk[j] = (uint32_t)j < ntop ? ld_dev_u64(my + nrec::kTop + j) : ~0ull;
+        for (int j = 0; j < (int)kTopMax; ++j) tk[j] = (uint32_t)j < ntop ? my[nrec::kTop + j] : ~0ull;
         const float m_raw = mine ? __uint_as_float((uint32_t)h0) : NEG;
         const uint32_t nts = mine ? (uint32_t)(h0 >> 32) & 0xffffu : 0u;
         const uint32_t flags = mine ? (uint32_t)(h0 >> 48) : 0u;
@@ -691,8 +690,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     uint32_t* gc = a.nh_cnt + ((uint64_t)wrow * kMaxSlices + slice) * kNucBins;
     double* gm = a.nh_mass + ((uint64_t)wrow * kMaxSlices + slice) * kNucBins;
     for (uint32_t b = tid; b < kNucBins; b += NT) {
-        st_dev(gc + b, sm.u.h.cnt[b]);
-        st_dev_d(gm + b, sm.u.h.mass[b]);
+        gc[b] = sm.u.h.cnt[b];
+        gm[b] = sm.u.h.mass[b];
     }
 }
 
@@ -734,8 +733,8 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
 #pragma unroll
                 for (uint32_t k = 0; k < BPT; ++k) {
                     const uint32_t b = tid * BPT + k;
-                    cc[i][k] = ld_dev(rc + (uint64_t)ss * kNucBins + b);
-                    mm[i][k] = ld_dev_d(rm + (uint64_t)ss * kNucBins + b);
+                    cc[i][k] = rc[(uint64_t)ss * kNucBins + b];
+                    mm[i][k] = rm[(uint64_t)ss * kNucBins + b];
                 }
             }
 #pragma unroll
@@ -901,7 +900,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     const float inv_t = fdiv(1.0f, P.temperature);
     const uint64_t* list = a.nlist + (uint64_t)wrow * kNucList;
     // =========== row finalize: exact decisions over the compacted ranges ===
-    const uint32_t n_all = ld_dev(&nr->list_n);
+    const uint32_t n_all = nr->list_n;
     const uint32_t n = min(n_all, kNucList);
     NucRange rg[kNucRanges];
 #pragma unroll
@@ -936,7 +935,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     };
     for (uint32_t i = tid; i < n; i += NT) {
         uint32_t k, s;
-        const float x = locate(ld_dev_u64(list + i), k, s);
+        const float x = locate(list[i], k, s);
         if (k < kNucRanges) {
             atomicAdd(&sm.u.fc.scnt[k][s], 1u);
             atomicAdd(&sm.u.fc.smass[k][s], exp_f64((double)x));
@@ -999,7 +998,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
         if (tid == 0) sm.l.ng = 0u;
         __syncthreads();
         for (uint32_t i = tid; i < n; i += NT) {
-            const uint64_t key = ld_dev_u64(list + i);
+            const uint64_t key = list[i];
             uint32_t kk, s;
             locate(key, kk, s);
             if (kk == k && s >= s0 && s <= s1) {
@@ -1143,7 +1142,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
             double ms = 0.0;
             uint64_t kl = 0ull;
             for (uint32_t i = tid; i < n; i += NT) {
-                const uint64_t key = ld_dev_u64(list + i);
+                const uint64_t key = list[i];
                 uint32_t kk, s;
                 const float x = locate(key, kk, s);
                 const double w = kk == km ? exp_f64((double)x) : 0.0;
@@ -1325,14 +1324,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         const uint32_t n = min(tot, kNucStage);
         uint64_t* list = a.nlist + (uint64_t)wrow * kNucList;
         for (uint32_t i = tid; i < n; i += NT) {
-            if (base + i < kNucList) st_dev_u64(list + base + i, sm.u.lkeys[i]);
+            if (base + i < kNucList) list[base + i] = sm.u.lkeys[i];
         }
         if (pos > kNucStage) {
             uint32_t p = pos0;
 #pragma unroll
             for (int q = 0; q < kSliceElems; ++q) {
                 if ((sel >> q) & 1u) {
-                    if (p >= kNucStage && base + p < kNucList) st_dev_u64(list + base + p, rank_key(in.v[q], in.eid(q)));
+                    if (p >= kNucStage && base + p < kNucList) list[base + p] = rank_key(in.v[q], in.eid(q));
                     ++p;
                 }
             }
