@@ -13,8 +13,9 @@
 //   A  nuc_stats:  penalties and the constraint (sampling.cpp:16-41, 70-86);
 //                  the raw max, log-normaliser and top-n (logprobs_from,
 //                  sampling.cpp:150-190); the penalised candidate max (the
-//                  reference's maxl) and min. The row's finalize writes the
-//                  row state and the top-n logprobs (nuc_stats_fin).
+//                  reference's maxl) and min. Pass B's workgroups derive
+//                  the row state from these records; its finalize writes
+//                  the top-n logprobs.
 //   B  nuc_hist:   the reference's weights exp((double)((p - maxl) * inv_t))
 //                  (sampling.cpp:101-109) binned by the tempered offset into
 //                  kNucBins bins (counts, f64 masses). The row's finalize
@@ -71,6 +72,9 @@ struct NucLocal {
     uint32_t ng;               // group size
     uint32_t out_flag;
     double out_m;              // kept mass at the top-p crossing
+    // the row state pass B's workgroups derive from pass A's records
+    float st_maxl, st_sx;
+    uint32_t st_use_mask, st_fallback;
     SampleArgs args;           // for the exact fallback
 };
 struct NucFinC {
@@ -87,8 +91,8 @@ struct NucSmem {
         struct {
             uint32_t cnt[kNucBins];
             double mass[kNucBins];
+            uint64_t top[kMaxSlices * kTopMax];   // top-n merge (pass B finalize, wave 1)
         } h;                              // histogram (pass B)
-        uint64_t top[kMaxSlices * kTopMax];   // top-n merge (pass A finalize)
         uint64_t lkeys[kNucStage];        // the slice's selections (pass C), thread order
         NucFinC fc;                       // select finalize
         ExactSmem<kSliceThreads, kFbBins, kFbCap, kFbHistCap> ex;
@@ -518,95 +522,100 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     }
 }
 
-// The row state and top-n logprobs from pass A's records (one workgroup per
-// row; the kernel boundary orders the records before these reads).
-template <int G>
-__global__ __launch_bounds__(NT) void nuc_stats_fin(SampleArgs a) {
-    NucSmem& sm = g_nuc;
-    uint32_t row;
-    lcs_params P;
-    bool masked;
-    if (!nuc_fin_row(a, row, P, masked)) return;
-    const uint32_t tid = tid_x(), S = a.slices;
-    const int lane = lane_id(), wv = (int)(tid / kWave);
-    const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
-    const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
+// The row state from pass A's records (wave 0 of the calling workgroup; lane
+// s reads slice s's header): the penalised candidate max (over the allowed
+// ids when the mask allows any) and its first index, the candidate count,
+// whether the mask is used (a mask that allows nothing falls back to all
+// ids, sampling.cpp:83-85), the bin scale sx, and whether a slice's top-n
+// candidates overflowed (the row then goes to the exact path). Every pass-B
+// workgroup of the row derives the same state from the same records.
+struct NucState {
+    float maxl, sx;
+    uint32_t maxi, n_cand;
+    bool use_mask, fallback;
+};
+__device__ __forceinline__ NucState nuc_row_state(const SampleArgs& a, uint32_t row, const lcs_params& P,
+                                                  bool masked, uint32_t ntop) {
+    const uint32_t S = a.slices;
+    const int lane = lane_id();
     const float NEG = -__builtin_huge_valf();
-    (void)tid;
-
-    // ---- the row's state (wave 0) and logprobs (wave 1) ----
     const uint64_t* recs = reinterpret_cast<const uint64_t*>(a.recs) + (uint64_t)row * S * rec::kWords64;
     const bool mine = (uint32_t)lane < S;
     const uint64_t* my = recs + (mine ? lane : 0) * rec::kWords64;
-    NucRow* nr = a.nrow + (row - a.nuc_row0);
-    if (wv == 0) {
-        const uint64_t h0 = my[0], h2 = my[2], h3 = my[3], h4 = my[4], h5 = my[5];
-        // a slice whose top-n candidates overflowed sends the row to the exact path
-        const bool ovf = ntop && ballot(mine && ((uint32_t)(h0 >> 48) & rec::kFlagCandOverflow));
-        const uint32_t na = wave_sum_u(mine ? (uint32_t)h4 : 0u);
-        const bool use_mask = masked && na > 0;
-        const uint64_t hb = use_mask ? h3 : h2;
-        float mx = mine ? __uint_as_float((uint32_t)hb) : NEG;
-        uint32_t mi = mine ? (uint32_t)(hb >> 32) : 0xfffffffeu;
-        wave_argmax(mx, mi);
-        const float mn = wave_min(mine ? __uint_as_float(use_mask ? (uint32_t)(h5 >> 32) : (uint32_t)h5)
-                                       : __builtin_huge_valf());
-        if (lane == 0) {
-            const float inv_t = fdiv(1.0f, P.temperature);
-            float x_lo = (mx == NEG) ? 0.0f : tempered(mn, mx, inv_t);
-            if (!(x_lo >= kNucXFloor)) x_lo = kNucXFloor;   // also NaN
-            nr->maxl = mx;
-            nr->maxi = mi;
-            // bins per unit offset: the largest power of two in [4, 2^20]
-            // with kNucBins / sx >= -x_lo
-            float sxv = 1048576.0f;
-            if (x_lo < 0.0f) {
-                const float q = fdiv((float)kNucBins, -x_lo);
-                sxv = fminf(__uint_as_float(__float_as_uint(q) & 0xff800000u), 1048576.0f);
-            }
-            nr->sx = sxv;
-            nr->n_cand = use_mask ? na : a.vocab;
-            nr->use_mask = use_mask ? 1u : 0u;
-            nr->flags = ovf ? kNucFallback : 0u;
-            nr->nr = 0u;
-            nr->list_n = 0u;
+    const uint64_t h0 = my[0], h2 = my[2], h3 = my[3], h4 = my[4], h5 = my[5];
+    const bool ovf = ntop && ballot(mine && ((uint32_t)(h0 >> 48) & rec::kFlagCandOverflow));
+    const uint32_t na = wave_sum_u(mine ? (uint32_t)h4 : 0u);
+    const bool use_mask = masked && na > 0;
+    const uint64_t hb = use_mask ? h3 : h2;
+    float mx = mine ? __uint_as_float((uint32_t)hb) : NEG;
+    uint32_t mi = mine ? (uint32_t)(hb >> 32) : 0xfffffffeu;
+    wave_argmax(mx, mi);
+    const float mn = wave_min(mine ? __uint_as_float(use_mask ? (uint32_t)(h5 >> 32) : (uint32_t)h5)
+                                   : __builtin_huge_valf());
+    const float inv_t = fdiv(1.0f, P.temperature);
+    float x_lo = (mx == NEG) ? 0.0f : tempered(mn, mx, inv_t);
+    if (!(x_lo >= kNucXFloor)) x_lo = kNucXFloor;   // also NaN
+    // bins per unit offset: the largest power of two in [4, 2^20] with
+    // kNucBins / sx >= -x_lo
+    float sxv = 1048576.0f;
+    if (x_lo < 0.0f) {
+        const float q = fdiv((float)kNucBins, -x_lo);
+        sxv = fminf(__uint_as_float(__float_as_uint(q) & 0xff800000u), 1048576.0f);
+    }
+    NucState st;
+    st.maxl = mx;
+    st.maxi = mi;
+    st.sx = sxv;
+    st.n_cand = use_mask ? na : a.vocab;
+    st.use_mask = use_mask;
+    st.fallback = ovf;
+    return st;
+}
+
+// The raw log-normaliser and the top-n logprobs from pass A's records (one
+// wave; lane s reads slice s's record).
+__device__ __forceinline__ void nuc_logprobs(const SampleArgs& a, uint32_t row, uint32_t ntop, NucRow* nr,
+                                             uint64_t* top) {
+    const uint32_t S = a.slices;
+    const int lane = lane_id();
+    const float NEG = -__builtin_huge_valf();
+    const uint64_t* recs = reinterpret_cast<const uint64_t*>(a.recs) + (uint64_t)row * S * rec::kWords64;
+    const bool mine = (uint32_t)lane < S;
+    const uint64_t* my = recs + (mine ? lane : 0) * rec::kWords64;
+    const uint64_t h0 = my[0], h1 = my[1];
+    uint64_t tk[kTopMax];
+#pragma unroll
+    for (int j = 0; j < (int)kTopMax; ++j) tk[j] = (uint32_t)j < ntop ? my[nrec::kTop + j] : ~0ull;
+    const float m_raw = mine ? __uint_as_float((uint32_t)h0) : NEG;
+    const uint32_t nts = mine ? (uint32_t)(h0 >> 32) & 0xffffu : 0u;
+    const uint32_t flags = mine ? (uint32_t)(h0 >> 48) : 0u;
+    const double s_raw = mine ? bits_d(h1) : 0.0;
+    const float M = wave_max(m_raw);
+    const double z = wave_sum(mine && m_raw != NEG ? s_raw * exp_f64((double)m_raw - (double)M) : 0.0);
+    const double log_z = log(z) + (double)M;
+    if (lane == 0) nr->log_z = log_z;
+    if (ntop && !ballot(mine && (flags & rec::kFlagCandOverflow))) {
+#pragma unroll
+        for (int j = 0; j < (int)kTopMax; ++j) {
+            if (mine && (uint32_t)j < ntop) top[lane * kTopMax + j] = (uint32_t)j < nts ? tk[j] : ~0ull;
         }
-    } else if (wv == 1 && want_lp) {
-        const uint64_t h0 = my[0], h1 = my[1];
-        uint64_t tk[kTopMax];
-#pragma unroll
-        for (int j = 0; j < (int)kTopMax; ++j) tk[j] = (uint32_t)j < ntop ? my[nrec::kTop + j] : ~0ull;
-        const float m_raw = mine ? __uint_as_float((uint32_t)h0) : NEG;
-        const uint32_t nts = mine ? (uint32_t)(h0 >> 32) & 0xffffu : 0u;
-        const uint32_t flags = mine ? (uint32_t)(h0 >> 48) : 0u;
-        const double s_raw = mine ? bits_d(h1) : 0.0;
-        const float M = wave_max(m_raw);
-        const double z = wave_sum(mine && m_raw != NEG ? s_raw * exp_f64((double)m_raw - (double)M) : 0.0);
-        const double log_z = log(z) + (double)M;
-        if (lane == 0) nr->log_z = log_z;
-        if (ntop && !ballot(mine && (flags & rec::kFlagCandOverflow))) {
-#pragma unroll
-            for (int j = 0; j < (int)kTopMax; ++j) {
-                if (mine && (uint32_t)j < ntop) sm.u.top[lane * kTopMax + j] = (uint32_t)j < nts ? tk[j] : ~0ull;
-            }
-            wave_sync();
-            uint32_t p = 0;
-            uint64_t myk = ~0ull;
-            for (uint32_t r = 0; r < ntop; ++r) {
-                const uint64_t head = mine && p < nts ? sm.u.top[lane * kTopMax + p] : ~0ull;
-                const uint32_t hk = (uint32_t)(head >> 32);
-                const uint32_t mk = wave_min_u(hk);
-                const uint64_t hit = ballot(head != ~0ull && hk == mk);
-                if (!hit) break;
-                const int wl = __builtin_ctzll(hit);
-                const uint64_t best = readlane_u64(head, wl);
-                if (lane == wl) ++p;
-                if ((uint32_t)lane == r) myk = best;
-            }
-            if ((uint32_t)lane < ntop) {
-                a.top_ids[(uint64_t)row * a.n_top + lane] = (int32_t)rank_idx(myk);
-                a.top_lp[(uint64_t)row * a.n_top + lane] = (float)((double)rank_val(myk) - log_z);
-            }
+        wave_sync();
+        uint32_t p = 0;
+        uint64_t myk = ~0ull;
+        for (uint32_t r = 0; r < ntop; ++r) {
+            const uint64_t head = mine && p < nts ? top[lane * kTopMax + p] : ~0ull;
+            const uint32_t hk = (uint32_t)(head >> 32);
+            const uint32_t mk = wave_min_u(hk);
+            const uint64_t hit = ballot(head != ~0ull && hk == mk);
+            if (!hit) break;
+            const int wl = __builtin_ctzll(hit);
+            const uint64_t best = readlane_u64(head, wl);
+            if (lane == wl) ++p;
+            if ((uint32_t)lane == r) myk = best;
+        }
+        if ((uint32_t)lane < ntop) {
+            a.top_ids[(uint64_t)row * a.n_top + lane] = (int32_t)rank_idx(myk);
+            a.top_lp[(uint64_t)row * a.n_top + lane] = (float)((double)rank_val(myk) - log_z);
         }
     }
 }
@@ -624,19 +633,44 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         wait_all_memory();   // (loads issued only when the host's parameter copy disagreed)
         return;
     }
-    const uint32_t tid = tid_x(), S = a.slices;
+    const uint32_t tid = tid_x();
     const uint32_t wrow = row - a.nuc_row0;
     NucRow* nr = a.nrow + wrow;
-    if (scalar_load(&nr->flags) & kNucFallback) return;   // resolved by the exact path
-    const float maxl = scalar_load(&nr->maxl);
-    const float sx = scalar_load(&nr->sx);
-    const bool use_mask = scalar_load(&nr->use_mask) != 0u;
     SliceIn<G> in;
     in.start(a, row, slice, P, masked, early ? pre : nullptr);
-    if (use_mask) in.load_mask();   // (its loads arrive with the logits')
+    if (masked) in.load_mask();   // (its loads arrive with the logits'; used when the mask allows any id)
+    if (tid < kWave) {
+        // the row state from pass A's records (slice 0 publishes it for the
+        // kernels that follow)
+        const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
+        const NucState st = nuc_row_state(a, row, P, masked, want_lp ? min(a.n_top, kTopMax) : 0u);
+        if (tid == 0) {
+            sm.l.st_maxl = st.maxl;
+            sm.l.st_sx = st.sx;
+            sm.l.st_use_mask = st.use_mask ? 1u : 0u;
+            sm.l.st_fallback = st.fallback ? 1u : 0u;
+            if (slice == 0) {
+                nr->maxl = st.maxl;
+                nr->maxi = st.maxi;
+                nr->sx = st.sx;
+                nr->n_cand = st.n_cand;
+                nr->use_mask = st.use_mask ? 1u : 0u;
+                nr->flags = st.fallback ? kNucFallback : 0u;
+                nr->nr = 0u;
+                nr->list_n = 0u;
+            }
+        }
+    }
     in.penalise(sm, P);   // (ends on a barrier when it used the LDS)
     for (uint32_t b = tid; b < kNucBins; b += NT) { sm.u.h.cnt[b] = 0u; sm.u.h.mass[b] = 0.0; }
     __syncthreads();
+    if (sm.l.st_fallback) {   // resolved by the exact path
+        wait_all_memory();
+        return;
+    }
+    const float maxl = sm.l.st_maxl;
+    const float sx = sm.l.st_sx;
+    const bool use_mask = sm.l.st_use_mask != 0u;
     const float inv_t = fdiv(1.0f, P.temperature);
     // Bin b holds sum exp(d), d = x + (b + 1/2) / sx, |d| <= 1 / (2 sx); the
     // finalize scales it by exp(-(b + 1/2) / sx). exp(d) is a Taylor
@@ -770,7 +804,12 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
         }
         __syncthreads();
     }
-    if (tid >= kWave) return;
+    if (tid >= kWave) {
+        // wave 1: the raw log-normaliser and the top-n logprobs
+        if (tid < 2 * kWave && (a.flags & LCS_WANT_LOGPROBS) != 0)
+            nuc_logprobs(a, row, min(a.n_top, kTopMax), nr, sm.u.h.top);
+        return;
+    }
     // ---- plan (wave 0, every lane computes the same plan): the bin ranges
     // each decision can need ----
     const int lane = lane_id();
@@ -1365,7 +1404,6 @@ static void launch_passes(const SampleArgs& a, uint32_t nrows, hipStream_t st) {
     const dim3 grid(nrows * a.slices), block(NT), rgrid(nrows);
     hipLaunchKernelGGL(nuc_stats<G>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
                        a.vocab, a.nuc_row0, a.all_nucleus, a);
-    hipLaunchKernelGGL(nuc_stats_fin<G>, rgrid, block, 0, st, a);
     hipLaunchKernelGGL(nuc_hist<G>, grid, block, 0, st, a.logits, a.row_stride, a.rows, a.slices, a.slice_len,
                        a.vocab, a.nuc_row0, a.all_nucleus, a);
     hipLaunchKernelGGL(nuc_hist_fin<G>, rgrid, block, 0, st, a);
