@@ -101,6 +101,30 @@ struct NucSmem {
 };
 __shared__ NucSmem g_nuc;
 
+// The select finalize's code of each compacted candidate: range k and
+// sub-bin s as k * kNucSub + s, kNoCode outside the planned ranges. Only
+// that kernel references it, so only it allocates the LDS.
+constexpr uint16_t kNoCode = 0xffffu;
+__shared__ uint16_t g_code[kNucList];
+
+#ifdef LCS_PROFILE
+// Phase timestamps (wall clock, 100 MHz) of the per-row finalize kernels for
+// performance work: slot k of row r at g_nprof[r * 32 + k] (hist finalize
+// slots 0-7, select finalize slots 8-31); lane 0 of wave 0 writes.
+__device__ uint64_t g_nprof[4096 * 32];
+#define NPROF(r, k)                                                                     \
+    do {                                                                                \
+        if (tid_x() == 0 && (r) < 4096) g_nprof[(uint64_t)(r) * 32 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+extern "C" int lcs_nprof_read(uint64_t* out, uint32_t n) {
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_nprof), (size_t)n * 8, 0, hipMemcpyDeviceToHost);
+}
+#else
+#define NPROF(r, k) \
+    do {            \
+    } while (0)
+#endif
+
 // ---------------------------------------------------- one slice of a row ----
 // The slice's logits (penalised in place once apply() ran), its mask words
 // and the penalty bookkeeping, for one thread.
@@ -741,10 +765,12 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
     const uint32_t tid = tid_x(), S = a.slices;
     const uint32_t wrow = row - a.nuc_row0;
     NucRow* nr = a.nrow + wrow;
+    const double u = a.u[row];   // (requested now: the plan needs it behind the merge)
     if (nr->flags & kNucFallback) return;   // resolved by the exact path
     const float sx = nr->sx;
     const double inv_sx = 1.0 / (double)sx;
 
+    NPROF(row, 0);
     // ---- the row's histogram: merged, then inclusive prefix sums ----
     constexpr uint32_t BPT = kNucBins / NT;   // bins per thread
     static_assert(kNucBins % NT == 0, "bins per thread");
@@ -782,6 +808,7 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
     }
 #pragma unroll
     for (uint32_t k = 0; k < BPT; ++k) m[k] *= exp_f64(-((double)(tid * BPT + k) + 0.5) * inv_sx);
+    NPROF(row, 1);
     {
         uint32_t cs = 0;
         double ms = 0.0;
@@ -810,6 +837,7 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
             nuc_logprobs(a, row, min(a.n_top, kTopMax), nr, sm.u.h.top);
         return;
     }
+    NPROF(row, 2);
     // ---- plan (wave 0, every lane computes the same plan): the bin ranges
     // each decision can need ----
     const int lane = lane_id();
@@ -874,7 +902,6 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
     }
     const uint32_t keep_lo = max(1u, min(kp_lo, km_lo)), keep_hi = max(1u, min(kp_hi, km_hi));
     const double K_lo = mb(first_count(keep_lo)), K_hi = hm[first_count(keep_hi)];
-    const double u = a.u[row];
     const int kb = first_count(keep_hi);
     const int d0 = min(first_mass(u * K_lo * (1.0 - kGuard)), kb);
     const int d1 = min(first_mass(u * K_hi * (1.0 + kGuard)), kb);
@@ -912,6 +939,7 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
         nr->r[i] = g;
     }
     nr->list_n = 0u;
+    NPROF(row, 3);
     if (total > kNucList || nm_ > (int)kNucRanges || ncand != scalar_load(&nr->n_cand)) nr->flags |= kNucFallback;
 }
 
@@ -936,6 +964,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     const float maxl = nr->maxl;
     const float sx = nr->sx;
     const uint32_t nrg = nr->nr;
+    const double u_row = a.u[row];   // (requested now: the draw needs it last)
     const float inv_t = fdiv(1.0f, P.temperature);
     const uint64_t* list = a.nlist + (uint64_t)wrow * kNucList;
     // =========== row finalize: exact decisions over the compacted ranges ===
@@ -949,6 +978,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     }
     const double Stot = nr->S;
     const uint32_t ncand = nr->n_cand;
+    NPROF(row, 8);
     // sub-bin tables
     for (uint32_t i = tid; i < kNucRanges * kNucSub; i += NT) {
         sm.u.fc.scnt[i / kNucSub][i % kNucSub] = 0u;
@@ -975,12 +1005,14 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     for (uint32_t i = tid; i < n; i += NT) {
         uint32_t k, s;
         const float x = locate(list[i], k, s);
+        g_code[i] = k < kNucRanges ? (uint16_t)(k * kNucSub + s) : kNoCode;
         if (k < kNucRanges) {
             atomicAdd(&sm.u.fc.scnt[k][s], 1u);
             atomicAdd(&sm.u.fc.smass[k][s], exp_f64((double)x));
         }
     }
     __syncthreads();
+    NPROF(row, 9);
     // inclusive sub-bin prefix sums, one wave per range (kNucSub = 2 per lane)
     static_assert(kNucRanges == kNW && kNucSub == 2 * kWave, "one wave per range");
     {
@@ -1036,13 +1068,13 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     auto gather = [&](uint32_t k, uint32_t s0, uint32_t s1) -> uint32_t {
         if (tid == 0) sm.l.ng = 0u;
         __syncthreads();
+        // (the codes in LDS select the group; only its keys are read again)
+        const uint32_t c0 = k * kNucSub + s0, c1 = k * kNucSub + s1;
         for (uint32_t i = tid; i < n; i += NT) {
-            const uint64_t key = list[i];
-            uint32_t kk, s;
-            locate(key, kk, s);
-            if (kk == k && s >= s0 && s <= s1) {
+            const uint32_t c = g_code[i];
+            if (c >= c0 && c <= c1) {
                 const uint32_t slot = atomicAdd(&sm.l.ng, 1u);
-                if (slot < kGroupMax) sm.u.fc.gkey[slot] = key;
+                if (slot < kGroupMax) sm.u.fc.gkey[slot] = list[i];
             }
         }
         __syncthreads();
@@ -1104,6 +1136,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
         return pos;
     };
 
+    NPROF(row, 10);
     // ---- decisions; `fail` sends the row to the exact path ----
     bool fail = sm.l.out_flag != 0u;
     uint32_t keep = ncand;
@@ -1131,6 +1164,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
             }
         }
     }
+    NPROF(row, 11);
     // top-p (sampling.cpp:113-123): first position with cum = prefix / SK >= top_p
     uint32_t keep_p = K;
     double mass_p = SK;
@@ -1161,6 +1195,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
             }
         }
     }
+    NPROF(row, 12);
     // min-p (sampling.cpp:125-133): survivors are the leading candidates with
     // w / S >= min_p * (w_0 / S); w is non-increasing in rank order, so the
     // survivors of the deciding range are counted without ordering them
@@ -1181,14 +1216,15 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
             double ms = 0.0;
             uint64_t kl = 0ull;
             for (uint32_t i = tid; i < n; i += NT) {
-                const uint64_t key = list[i];
-                uint32_t kk, s;
-                const float x = locate(key, kk, s);
-                const double w = kk == km ? exp_f64((double)x) : 0.0;
-                if (kk == km && w / SK >= thresh) {
-                    ++cnt;
-                    ms += w;
-                    kl = key > kl ? key : kl;
+                const uint32_t c = g_code[i];
+                if (c != kNoCode && c / kNucSub == km) {
+                    const uint64_t key = list[i];
+                    const double w = exp_f64((double)tempered(rank_val(key), maxl, inv_t));
+                    if (w / SK >= thresh) {
+                        ++cnt;
+                        ms += w;
+                        kl = key > kl ? key : kl;
+                    }
                 }
             }
             const uint32_t tc = block_sum_u<NT>(cnt, sm.l.nall);
@@ -1211,11 +1247,12 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
             keep = K; kept_sum = SK; last_key = key_k;   // ~0 when no top-k cut
         }
     }
+    NPROF(row, 13);
     // draw (sampling.cpp:135-147): r = u * kept_sum; the first kept candidate
     // whose inclusive prefix reaches r, else the last kept one
     int32_t chosen = -1;
     if (!fail) {
-        const double r0 = a.u[row] * (kept_sum - 0.0) + 0.0;
+        const double r0 = u_row * (kept_sum - 0.0) + 0.0;
         uint32_t k0, s0, k1, s1;
         const bool f0 = find_mass(r0 * (1.0 - kGuard), k0, s0);
         bool f1 = find_mass(r0 * (1.0 + kGuard), k1, s1);
@@ -1244,6 +1281,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
             }
         }
     }
+    NPROF(row, 14);
     if (fail) {
         // every thread agrees (all decisions above are block-uniform)
         exact_row<kSliceThreads, kFbBins, kFbCap, kFbHistCap, G>(sm.l.args, row, sm.u.ex);
@@ -1270,6 +1308,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
             a.diag[row] = dg;
         }
     }
+    NPROF(row, 16);
 }
 
 
@@ -1390,6 +1429,7 @@ __global__ __launch_bounds__(NT) void nuc_select_fin_kernel(SampleArgs a) {
     lcs_params P;
     bool masked;
     if (!nuc_fin_row(a, row, P, masked)) return;
+    NPROF(row, 15);
     const bool exact = (a.nrow[row - a.nuc_row0].flags & kNucFallback) != 0u;
     if (tid_x() == 0) stash_args(&sm.l.args, a);
     __syncthreads();
