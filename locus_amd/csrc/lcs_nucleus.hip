@@ -75,6 +75,7 @@ struct NucLocal {
     // the row state pass B's workgroups derive from pass A's records
     float st_maxl, st_sx;
     uint32_t st_use_mask, st_fallback;
+    NucRange rgl[kNucRanges];  // the planned ranges, for lookups by a computed index (select finalize)
     SampleArgs args;           // for the exact fallback
 };
 struct NucFinC {
@@ -766,6 +767,7 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
     const uint32_t wrow = row - a.nuc_row0;
     NucRow* nr = a.nrow + wrow;
     const double u = a.u[row];   // (requested now: the plan needs it behind the merge)
+    const uint32_t ncand_row = nr->n_cand;
     if (nr->flags & kNucFallback) return;   // resolved by the exact path
     const float sx = nr->sx;
     const double inv_sx = 1.0 / (double)sx;
@@ -867,9 +869,9 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
     auto first_count = [&](uint32_t n) -> int {   // bin holding candidate position n - 1
         return first_of([&](int j) { return lc[j] >= n; });
     };
-    int ivl[kNucRanges + 3][2];
-    int niv = 0;
-    auto add = [&](int b0, int b1) { ivl[niv][0] = b0; ivl[niv][1] = b1; ++niv; };
+    // the decisions' bin intervals in fixed slots (0 top-k, 1 top-p, 2 min-p,
+    // 3 draw; an unused slot starts at NB), so that they stay in registers
+    int ib[4] = {NB, NB, NB, NB}, ie[4] = {0, 0, 0, 0};
     // top-k (sampling.cpp:87-97): the first K candidates survive and their
     // mass S_K, which lies in [mass before bin bK, mass through bin bK] for
     // the bin bK holding position K - 1, is the normaliser of what follows
@@ -880,14 +882,16 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
         bK = first_count(K);
         SK_lo = mb(bK);
         SK_hi = hm[bK];
-        add(bK, bK);
+        ib[0] = bK;
+        ie[0] = bK;
     }
     uint32_t kp_lo = K, kp_hi = K, km_lo = K, km_hi = K;
     if (P.top_p < 1.0f) {
         const double tp = (double)P.top_p;
         const int b0 = min(first_mass(tp * SK_lo * (1.0 - kGuard)), bK);
         const int b1 = min(first_mass(tp * SK_hi * (1.0 + kGuard)), bK);
-        add(b0, b1);
+        ib[1] = b0;
+        ie[1] = b1;
         kp_lo = min(cb(b0) + 1u, K);
         kp_hi = min(hc[b1], K);
     }
@@ -896,7 +900,8 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
         const float xm = (float)log((double)P.min_p);
         const float d = 1e-4f * fmaxf(1.0f, fabsf(xm));
         const int b0 = (int)nuc_bin(nuc_f(xm + d, sx)), b1 = (int)nuc_bin(nuc_f(xm - d, sx));
-        add(b0, b1);
+        ib[2] = b0;
+        ie[2] = b1;
         km_lo = min(max(1u, cb(b0)), K);
         km_hi = min(max(1u, hc[b1]), K);
     }
@@ -905,42 +910,52 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
     const int kb = first_count(keep_hi);
     const int d0 = min(first_mass(u * K_lo * (1.0 - kGuard)), kb);
     const int d1 = min(first_mass(u * K_hi * (1.0 + kGuard)), kb);
-    add(d0, d1);
-    // merge overlapping or adjacent intervals (insertion sort by start)
-    for (int i = 1; i < niv; ++i) {
-        for (int j = i; j > 0 && ivl[j][0] < ivl[j - 1][0]; --j) {
-            const int t0 = ivl[j][0], t1 = ivl[j][1];
-            ivl[j][0] = ivl[j - 1][0]; ivl[j][1] = ivl[j - 1][1];
-            ivl[j - 1][0] = t0; ivl[j - 1][1] = t1;
+    ib[3] = d0;
+    ie[3] = d1;
+    // sort the slots by start (a five-exchange network), then merge
+    // overlapping or adjacent intervals in order, writing each merged range
+    // as it closes
+    auto cx = [&](int i, int j) {
+        if (ib[j] < ib[i]) {
+            const int t0 = ib[i], t1 = ie[i];
+            ib[i] = ib[j]; ie[i] = ie[j];
+            ib[j] = t0; ie[j] = t1;
+        }
+    };
+    cx(0, 1); cx(2, 3); cx(0, 2); cx(1, 3); cx(1, 2);
+    uint32_t total = 0, nm_ = 0;
+    int cur_b = NB, cur_e = 0;
+    auto close = [&]() {
+        NucRange g;
+        g.b0 = (uint32_t)cur_b;
+        g.b1 = (uint32_t)cur_e;
+        g.c0 = cb(cur_b);
+        g.cnt = hc[cur_e] - g.c0;
+        g.m0 = mb(cur_b);
+        g.m = hm[cur_e] - g.m0;
+        total += g.cnt;
+        if (lane == 0) nr->r[nm_] = g;   // (at most four merged ranges)
+        ++nm_;
+    };
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (ib[i] < NB) {
+            if (cur_b < NB && ib[i] <= cur_e + 1) {
+                cur_e = max(cur_e, ie[i]);
+            } else {
+                if (cur_b < NB) close();
+                cur_b = ib[i];
+                cur_e = ie[i];
+            }
         }
     }
-    int nm_ = 0;
-    for (int i = 0; i < niv; ++i) {
-        if (nm_ > 0 && ivl[i][0] <= ivl[nm_ - 1][1] + 1) {
-            ivl[nm_ - 1][1] = max(ivl[nm_ - 1][1], ivl[i][1]);
-        } else {
-            ivl[nm_][0] = ivl[i][0]; ivl[nm_][1] = ivl[i][1];
-            ++nm_;
-        }
-    }
-    uint32_t total = 0;
-    for (int i = 0; i < nm_; ++i) total += hc[ivl[i][1]] - cb(ivl[i][0]);
+    if (cur_b < NB) close();
     if (lane != 0) return;
     nr->S = Stot;
-    nr->nr = (uint32_t)nm_;
-    for (int i = 0; i < nm_ && i < (int)kNucRanges; ++i) {
-        NucRange g;
-        g.b0 = (uint32_t)ivl[i][0];
-        g.b1 = (uint32_t)ivl[i][1];
-        g.c0 = cb(ivl[i][0]);
-        g.cnt = hc[ivl[i][1]] - g.c0;
-        g.m0 = mb(ivl[i][0]);
-        g.m = hm[ivl[i][1]] - g.m0;
-        nr->r[i] = g;
-    }
+    nr->nr = nm_;
     nr->list_n = 0u;
     NPROF(row, 3);
-    if (total > kNucList || nm_ > (int)kNucRanges || ncand != scalar_load(&nr->n_cand)) nr->flags |= kNucFallback;
+    if (total > kNucList || ncand != ncand_row) nr->flags |= kNucFallback;
 }
 
 // ========================================================= C: nuc_select ==
@@ -985,7 +1000,17 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
         sm.u.fc.smass[i / kNucSub][i % kNucSub] = 0.0;
     }
     if (tid == 0) sm.l.out_flag = n_all > kNucList ? 1u : 0u;
+    if (tid < kNucRanges) {
+        if (tid < nrg) {
+            sm.l.rgl[tid] = nr->r[tid];
+        } else {
+            NucRange e;
+            e.b0 = 1; e.b1 = 0; e.c0 = 0; e.cnt = 0; e.m0 = 0.0; e.m = 0.0;
+            sm.l.rgl[tid] = e;
+        }
+    }
     __syncthreads();
+    const NucRange* rgl = sm.l.rgl;   // (rg in registers for the hot loops, rgl for computed indices)
     // range and sub-bin of a compacted candidate; its weight as the reference's
     auto locate = [&](uint64_t key, uint32_t& k, uint32_t& s) -> float {
         const float x = tempered(rank_val(key), maxl, inv_t);
@@ -1028,13 +1053,13 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     }
     __syncthreads();
     // count / mass before sub-bin s of range k (row-level)
-    auto c_before = [&](uint32_t k, uint32_t s) -> uint32_t { return rg[k].c0 + (s > 0 ? sm.u.fc.scnt[k][s - 1] : 0u); };
-    auto m_before = [&](uint32_t k, uint32_t s) -> double { return rg[k].m0 + (s > 0 ? sm.u.fc.smass[k][s - 1] : 0.0); };
-    auto m_incl = [&](uint32_t k, uint32_t s) -> double { return rg[k].m0 + sm.u.fc.smass[k][s]; };
+    auto c_before = [&](uint32_t k, uint32_t s) -> uint32_t { return rgl[k].c0 + (s > 0 ? sm.u.fc.scnt[k][s - 1] : 0u); };
+    auto m_before = [&](uint32_t k, uint32_t s) -> double { return rgl[k].m0 + (s > 0 ? sm.u.fc.smass[k][s - 1] : 0.0); };
+    auto m_incl = [&](uint32_t k, uint32_t s) -> double { return rgl[k].m0 + sm.u.fc.smass[k][s]; };
     // first (range, sub-bin) whose inclusive mass reaches t (by rank order)
     auto find_mass = [&](double t, uint32_t& k, uint32_t& s) -> bool {
         for (uint32_t j = 0; j < nrg && j < kNucRanges; ++j) {
-            if (rg[j].m0 + rg[j].m >= t && rg[j].m0 <= t * (1.0 + kGuard)) {
+            if (rgl[j].m0 + rgl[j].m >= t && rgl[j].m0 <= t * (1.0 + kGuard)) {
                 int lo = 0, hi = (int)kNucSub - 1;
                 while (lo < hi) {
                     const int mid = (lo + hi) >> 1;
@@ -1050,11 +1075,11 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     // (range, sub-bin) holding candidate position n - 1 (rank order)
     auto find_count = [&](uint32_t n, uint32_t& k, uint32_t& s) -> bool {
         for (uint32_t j = 0; j < nrg && j < kNucRanges; ++j) {
-            if (rg[j].c0 < n && rg[j].c0 + rg[j].cnt >= n) {
+            if (rgl[j].c0 < n && rgl[j].c0 + rgl[j].cnt >= n) {
                 int lo = 0, hi = (int)kNucSub - 1;
                 while (lo < hi) {
                     const int mid = (lo + hi) >> 1;
-                    if (rg[j].c0 + sm.u.fc.scnt[j][mid] >= n) hi = mid; else lo = mid + 1;
+                    if (rgl[j].c0 + sm.u.fc.scnt[j][mid] >= n) hi = mid; else lo = mid + 1;
                 }
                 k = j;
                 s = (uint32_t)lo;
@@ -1207,7 +1232,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
         const float xm = (float)log((double)P.min_p);
         const uint32_t bm = nuc_bin(nuc_f(xm, sx));
         uint32_t km = kNucRanges;
-        for (uint32_t j = 0; j < nrg && j < kNucRanges; ++j) if (km == kNucRanges && bm >= rg[j].b0 && bm <= rg[j].b1) km = j;
+        for (uint32_t j = 0; j < nrg && j < kNucRanges; ++j) if (km == kNucRanges && bm >= rgl[j].b0 && bm <= rgl[j].b1) km = j;
         if (km == kNucRanges) {
             fail = true;
         } else {
@@ -1230,10 +1255,10 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
             const uint32_t tc = block_sum_u<NT>(cnt, sm.l.nall);
             const double tm = block_sum<NT>(ms, sm.l.sraw);
             const uint64_t tk = ~block_min_u64<NT>(~kl, sm.l.ck);
-            keep_m = max(1u, rg[km].c0 + tc);
-            mass_m = rg[km].m0 + tm;
+            keep_m = max(1u, rgl[km].c0 + tc);
+            mass_m = rgl[km].m0 + tm;
             key_m = tc > 0 ? tk : ~0ull;
-            if (rg[km].c0 + tc == 0) fail = true;   // (w_0 always survives)
+            if (rgl[km].c0 + tc == 0) fail = true;   // (w_0 always survives)
             if (keep_m >= K) { keep_m = K; mass_m = SK; key_m = key_k; }   // top-k cut first
         }
     }
