@@ -69,9 +69,10 @@ struct NucLocal {
     uint32_t ipen[kNW], imsk[kNW], nall[kNW];
     uint64_t ck[kNucCand];
     // select-pass finalize
-    uint32_t ng;               // group size
+    uint32_t ngc[2];           // group sizes of alternate gathers (each reset one gather ahead)
+    uint32_t fp_pos;           // first_prefix's position and prefix mass
+    double fp_m;
     uint32_t out_flag;
-    double out_m;              // kept mass at the top-p crossing
     // the row state pass B's workgroups derive from pass A's records
     float st_maxl, st_sx;
     uint32_t st_use_mask, st_fallback;
@@ -999,7 +1000,10 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
         sm.u.fc.scnt[i / kNucSub][i % kNucSub] = 0u;
         sm.u.fc.smass[i / kNucSub][i % kNucSub] = 0.0;
     }
-    if (tid == 0) sm.l.out_flag = n_all > kNucList ? 1u : 0u;
+    if (tid == 0) {
+        sm.l.out_flag = n_all > kNucList ? 1u : 0u;
+        sm.l.ngc[0] = 0u;
+    }
     if (tid < kNucRanges) {
         if (tid < nrg) {
             sm.l.rgl[tid] = nr->r[tid];
@@ -1090,20 +1094,24 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     };
     // Gathers the candidates of range k's sub-bins [s0, s1] into gkey and ranks
     // them (wave 0) into gsorted with weights gw. Every thread calls it.
+    // (gather i counts into ngc[i & 1], which was cleared during gather i - 1,
+    // after every thread had read it in gather i - 2)
+    uint32_t gidx = 0;
     auto gather = [&](uint32_t k, uint32_t s0, uint32_t s1) -> uint32_t {
-        if (tid == 0) sm.l.ng = 0u;
-        __syncthreads();
+        uint32_t* cnt = &sm.l.ngc[gidx & 1u];
+        if (tid == 0) sm.l.ngc[(gidx + 1u) & 1u] = 0u;
+        ++gidx;
         // (the codes in LDS select the group; only its keys are read again)
         const uint32_t c0 = k * kNucSub + s0, c1 = k * kNucSub + s1;
         for (uint32_t i = tid; i < n; i += NT) {
             const uint32_t c = g_code[i];
             if (c >= c0 && c <= c1) {
-                const uint32_t slot = atomicAdd(&sm.l.ng, 1u);
+                const uint32_t slot = atomicAdd(cnt, 1u);
                 if (slot < kGroupMax) sm.u.fc.gkey[slot] = list[i];
             }
         }
         __syncthreads();
-        const uint32_t ng = sm.l.ng;
+        const uint32_t ng = *cnt;
         if (ng <= kGroupMax && wv == 0) {
             uint64_t kk[4];
             uint32_t rk[4];
@@ -1150,15 +1158,15 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
                 double pa = 0.0;
 #pragma unroll
                 for (int c = 0; c < 4; ++c) pa = (uint32_t)c == first ? base + pre[c] : pa;
-                g_nuc.l.ng = bal ? 4u * (uint32_t)L + first : kNone;
-                g_nuc.l.out_m = pa;
+                g_nuc.l.fp_pos = bal ? 4u * (uint32_t)L + first : kNone;
+                g_nuc.l.fp_m = pa;
             }
         }
         __syncthreads();
-        const uint32_t pos = g_nuc.l.ng;
-        p_at = g_nuc.l.out_m;
-        __syncthreads();
-        return pos;
+        // (the next writer of fp_pos / fp_m is a later first_prefix, after
+        // a gather's barriers)
+        p_at = g_nuc.l.fp_m;
+        return g_nuc.l.fp_pos;
     };
 
     NPROF(row, 10);
