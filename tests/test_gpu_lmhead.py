@@ -8,8 +8,8 @@ Two gates, as for every kernel here:
 - the epilogue's statistics against the kernel's own written logits: argmax
   bit-exact with the first-index rule (llama.cpp:1237-1245), the draft
   logprob and acceptance length against the oracle's verify
-  (sampling.cpp:150-170, engine.cpp:357-383), log_z within 1e-5 of the
-  float64 log-sum-exp.
+  (sampling.cpp:150-170, engine.cpp:357-383), log_z (returned in f32)
+  within 1e-5 plus half an f32 spacing of the float64 log-sum-exp.
 """
 import sys
 from types import SimpleNamespace
