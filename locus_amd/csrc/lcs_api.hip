@@ -20,6 +20,7 @@ hipError_t launch_nucleus(const SampleArgs& a, hipStream_t st);
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t st);
 hipError_t launch_draft(const DraftArgs& a, hipStream_t st);
 hipError_t launch_lmhead(const LmArgs& a, hipStream_t st);
+uint32_t lmhead_cols(uint32_t vocab, uint32_t cus);
 }  // namespace lcs
 
 struct lcs_ctx {
@@ -32,7 +33,8 @@ struct lcs_ctx {
     float* d_raw = nullptr;
     float* d_pen = nullptr;
     uint32_t* status = nullptr;
-    lcs::LmRec* lmrecs = nullptr;   // lm-head epilogue records: max_rows x blocks of kLmCols
+    lcs::LmRec* lmrecs = nullptr;   // lm-head epilogue records: max_rows x blocks of >= kLmColsMin columns
+    uint32_t cus = 0;               // compute units of the device (the lm-head's block shape)
     // nucleus path workspace (kNucRows rows at a time)
     lcs::NucRow* nrow = nullptr;
     uint32_t* nh_cnt = nullptr;
@@ -115,6 +117,9 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t 
     }
     DeviceGuard g(device);
     c->device = device;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+        c->cus = (uint32_t)cus;
     c->max_rows = max_rows;
     c->max_vocab = max_vocab;
     c->max_hist = max_hist > 0 ? max_hist : 1;
@@ -132,7 +137,7 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t 
         (e = hipMalloc(&c->d_raw, d_elems * 4)) != hipSuccess ||
         (e = hipMalloc(&c->d_pen, d_elems * 4)) != hipSuccess ||
         (e = hipMalloc(&c->status, 4)) != hipSuccess ||
-        (e = hipMalloc(&c->lmrecs, (size_t)max_rows * ((max_vocab + lcs::kLmCols - 1) / lcs::kLmCols) *
+        (e = hipMalloc(&c->lmrecs, (size_t)max_rows * ((max_vocab + lcs::kLmColsMin - 1) / lcs::kLmColsMin) *
                                        sizeof(lcs::LmRec))) != hipSuccess ||
         (e = hipMalloc(&c->nrow, nuc_rows * sizeof(lcs::NucRow))) != hipSuccess ||
         (e = hipMalloc(&c->nh_cnt, nh_elems * 4)) != hipSuccess ||
@@ -473,7 +478,8 @@ int lcs_lmhead(lcs_ctx* c, const lcs_lmhead_batch* b, const lcs_lmhead_out* o, v
     a.rows = b->rows;
     a.vocab = b->vocab;
     a.hidden = b->hidden;
-    a.nblocks = (b->vocab + lcs::kLmCols - 1) / lcs::kLmCols;
+    a.cols = lcs::lmhead_cols(b->vocab, c->cus);
+    a.nblocks = (b->vocab + a.cols - 1) / a.cols;
     a.rows_per_seq = b->rows_per_seq;
     a.ld_logits = o->ld_logits;
     a.draft = b->draft;

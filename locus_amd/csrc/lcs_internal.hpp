@@ -172,9 +172,8 @@ struct DraftArgs {
 
 // lm-head product with the first statistics in its epilogue (lcs_lmhead.hip)
 constexpr uint32_t kLmRows = 64;    // rows per product launch (4 MFMA row tiles)
-constexpr uint32_t kLmWaveTiles = 4;                // 16-column MFMA tiles per wave
-constexpr uint32_t kLmCols = 4 * 16 * kLmWaveTiles;  // vocabulary columns per workgroup: one record block
-struct LmRec {                      // per (row, block of kLmCols columns)
+constexpr uint32_t kLmColsMin = 256;  // vocabulary columns per workgroup (one record block): 256 or 320
+struct LmRec {                      // per (row, block of columns)
     float max;                      // the block's largest logit
     uint32_t idx;                   // its first column; bit 31: the block holds the row's draft token
     float sum;                      // sum of exp(logit - max) over the block
@@ -185,6 +184,7 @@ struct LmArgs {
     const uint16_t* x;              // rows x hidden bf16
     const uint16_t* w;              // vocab x hidden bf16
     uint32_t rows, vocab, hidden, m0, nblocks, rows_per_seq;
+    uint32_t cols;                  // columns per block (lmhead_cols)
     uint64_t ld_logits;             // elements between logits rows
     const int32_t* draft;
     float* logits;

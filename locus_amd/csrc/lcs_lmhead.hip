@@ -42,7 +42,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kLmThreads = 256;
 constexpr float kL2E = 1.4426950408889634f;
-constexpr int kDepth = 3;   // weight k-steps in flight ahead of the product
 constexpr int kKC = 2;      // 32-wide k chunks per step: 128 bytes of each weight row
 
 __device__ __forceinline__ bf16x8 ld_frag(const uint16_t* p) {
@@ -67,7 +66,10 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 }  // namespace
 
-// a.m0: first row of this launch's chunk (<= kLmRows rows)
+// a.m0: first row of this launch's chunk (<= kLmRows rows). WC: 16-column
+// MFMA tiles per wave (the workgroup's block is 64 WC columns); kDepth:
+// weight k-steps in flight ahead of the product.
+template <int WC, int kDepth>
 __global__ __launch_bounds__(kLmThreads, 2) void lmhead_kernel(LmArgs a) {
     __shared__ uint64_t pkey[kLmThreads / kWave][kLmRows];   // per wave: row's best (rank key)
     __shared__ float psum[kLmThreads / kWave][kLmRows];
@@ -78,8 +80,8 @@ __global__ __launch_bounds__(kLmThreads, 2) void lmhead_kernel(LmArgs a) {
     const uint32_t nb = wg_x();
     const uint32_t K = a.hidden, V = a.vocab;
     const uint32_t m0 = a.m0, mrows = min((uint32_t)kLmRows, a.rows - m0);
-    constexpr int WC = (int)kLmWaveTiles;
-    const uint32_t nw = nb * (uint32_t)kLmCols + (uint32_t)wv * (16u * WC);   // this wave's first column
+    constexpr uint32_t kCols = 4u * 16u * WC;
+    const uint32_t nw = nb * kCols + (uint32_t)wv * (16u * WC);   // this wave's first column
     const uint32_t lr = (uint32_t)lane & 15u, kq = (uint32_t)lane >> 4;
     // fragment rows: A rows past the chunk and B columns past the vocabulary
     // read row 0 / column 0 (in bounds) and are masked in the epilogue
@@ -311,11 +313,25 @@ __global__ __launch_bounds__(kLmThreads) void lmhead_fin(LmArgs a) {
     }
 }
 
+// The block shape per launch: 256 columns three k-steps deep, or 320
+// columns two k-steps deep (the register budget of two workgroups per CU)
+// when that fits the blocks in one round of resident workgroups and 256
+// does not (a vocabulary just above 512 blocks of 256 would pay a second,
+// mostly idle round).
+uint32_t lmhead_cols(uint32_t vocab, uint32_t cus) {
+    const uint32_t slots = 2u * (cus ? cus : 256u);
+    const uint32_t n4 = (vocab + 255u) / 256u, n5 = (vocab + 319u) / 320u;
+    const uint32_t r4 = (n4 + slots - 1u) / slots, r5 = (n5 + slots - 1u) / slots;
+    return r5 < r4 ? 320u : 256u;
+}
+
 hipError_t launch_lmhead(const LmArgs& a0, hipStream_t st) {
     LmArgs a = a0;
+    const bool wide = a0.cols == 320u;
     for (uint32_t m0 = 0; m0 < a0.rows; m0 += kLmRows) {
         a.m0 = m0;
-        hipLaunchKernelGGL(lmhead_kernel, dim3(a.nblocks), dim3(kLmThreads), 0, st, a);
+        if (wide) hipLaunchKernelGGL((lmhead_kernel<5, 2>), dim3(a.nblocks), dim3(kLmThreads), 0, st, a);
+        else hipLaunchKernelGGL((lmhead_kernel<4, 3>), dim3(a.nblocks), dim3(kLmThreads), 0, st, a);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
