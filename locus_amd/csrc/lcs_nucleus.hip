@@ -758,7 +758,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
 // Pass B's histograms merged per row and the plan of bin ranges (one
 // workgroup per row, after the kernel boundary).
 template <int G>
-__global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void nuc_hist_fin(SampleArgs a) {
     NucSmem& sm = g_nuc;
     uint32_t row;
     lcs_params P;
@@ -784,9 +784,9 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
     const uint32_t* rc = a.nh_cnt + (uint64_t)wrow * kMaxSlices * kNucBins;
     const double* rm = a.nh_mass + (uint64_t)wrow * kMaxSlices * kNucBins;
     {
-        // slices in chunks of 10: a chunk's words are all issued before any is
+        // slices in chunks of 20: a chunk's words are all issued before any is
         // summed; sums run in slice order (deterministic)
-        constexpr uint32_t CH = 10;
+        constexpr uint32_t CH = 20;
         for (uint32_t s0 = 0; s0 < S; s0 += CH) {
             uint32_t cc[CH][BPT];
             double mm[CH][BPT];
@@ -804,7 +804,11 @@ __global__ __launch_bounds__(NT) void nuc_hist_fin(SampleArgs a) {
             for (uint32_t i = 0; i < CH; ++i) {
 #pragma unroll
                 for (uint32_t k = 0; k < BPT; ++k) {
-                    if (s0 + i < S) { c[k] += cc[i][k]; m[k] += mm[i][k]; }
+                    // (selects, not a branch: a branch would let the
+                    // compiler sink each load into it, one round trip each)
+                    const bool in = s0 + i < S;
+                    c[k] += in ? cc[i][k] : 0u;
+                    m[k] += in ? mm[i][k] : 0.0;
                 }
             }
         }
