@@ -242,6 +242,11 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
     LCS_WAVE_REDUCE_64(v, ~0ull, u64_min);
     return v;
 }
+__device__ __forceinline__ uint64_t u64_max(uint64_t a, uint64_t b) { return b > a ? b : a; }
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    LCS_WAVE_REDUCE_64(v, 0ull, u64_max);
+    return v;
+}
 __device__ __forceinline__ double wave_sum(double v) {
     uint64_t b = (uint64_t)__double_as_longlong(v);
     LCS_WAVE_REDUCE_64(b, 0ull, d_add_bits);  // +0.0 identity

@@ -872,7 +872,7 @@ struct FinSmem {
     uint32_t fin_fb, fin_L0;
     uint32_t tk_ns[kSsMaxSlices];                    // top-k rows: entries of each slice's list,
     uint32_t tk_cs[kSsMaxSlices], tk_base[kSsMaxSlices];   // its candidates (keys <= U), their offset
-    uint32_t tk_ke, tk_nc;
+    uint64_t tk_u[4];                                // top-k rows: each wave's bound
     uint32_t tn_ns[kSsMaxSlices];                    // top-n list lengths (logprobs)
     SampleArgs args;   // the kernel arguments (exact_row reads them from here)
 };
@@ -1087,125 +1087,138 @@ __device__ __forceinline__ bool fin_window(const uint64_t (&hd)[rec::kHdr], cons
     return false;
 }
 
-// Top-k rows: waves 2-3 copy the slices' rank-ordered top-k lists into LDS
-// (slot i: entry i % K of slice i / K), all loads issued before any store.
-__device__ __forceinline__ void fin_fetch_topk(const uint64_t* recs, uint32_t S, uint32_t K, FinSmem& sm) {
-    constexpr uint32_t NF = 2 * kWave;                  // fetching threads
-    constexpr uint32_t SL = kSsTopKMerge / NF;          // slots per thread
-    const uint32_t t = tid_x() - 2 * kWave;
-    uint64_t kk[SL];
-    uint32_t rr[SL];
+// Top-k rows: wave w holds the rank-ordered top-k lists of slices 4i + w in
+// registers, entry = lane (plain loads; the lists are kTopKMax <= kWinCap
+// entries apart, past a list's length the entries are unused). The loads are
+// unconditional (slices past S read slice 0, and every use checks s < S), so
+// none of them waits for another.
+constexpr uint32_t kTkPer = kSsMaxSlices / 4;   // lists a wave holds
+__device__ __forceinline__ void fin_load_topk(const uint64_t* recs, uint32_t S, int wv, uint64_t (&kk)[kTkPer],
+                                              float (&rr)[kTkPer]) {
+    const uint32_t lane = (uint32_t)lane_id();
 #pragma unroll
-    for (uint32_t c = 0; c < SL; ++c) {
-        const uint32_t i = t + c * NF, s = i / K, j = i - s * K;
-        kk[c] = ~0ull;
-        rr[c] = 0u;
-        if (s < S) {
-            const uint64_t* r = recs + (uint64_t)s * rec::kWords64;
-            kk[c] = r[rec::kWin + j];
-            rr[c] = (uint32_t)r[rec::kWinRaw + j];
-        }
+    for (uint32_t i = 0; i < kTkPer; ++i) {
+        const uint32_t s = 4 * i + (uint32_t)wv;
+        const uint64_t* r = recs + (uint64_t)(s < S ? s : 0u) * rec::kWords64;
+        kk[i] = r[rec::kWin + lane];
+        rr[i] = reinterpret_cast<const float*>(r + rec::kWinRaw + lane)[0];   // (the low half)
     }
-#pragma unroll
-    for (uint32_t c = 0; c < SL; ++c) {
-        const uint32_t i = t + c * NF;
-        if (i < S * K) {
-            sm.u.f.tkey[i] = kk[c];
-            sm.u.f.traw[i] = __uint_as_float(rr[c]);
-        }
-    }
-}
-
-// Top-k rows, wave 0 before the merge: each slice's list length into LDS (h0:
-// this lane's slice header word 0). Returns true when a slice could not rank
-// its list.
-__device__ __forceinline__ bool fin_topk_lengths(uint32_t S, uint32_t K, FinSmem& sm, uint64_t h0) {
-    const int lane = lane_id();
-    const bool mine = (uint32_t)lane < S;
-    const uint32_t flags = mine ? (uint32_t)(h0 >> 48) : 0u;
-    if (mine) sm.tk_ns[lane] = min((uint32_t)(h0 >> 32) & 0xffffu, K);
-    return ballot(mine && (flags & rec::kFlagWinLost)) != 0;
 }
 
 // Top-k rows (sampling.cpp:87-97): the merge of the slices' top-k lists (each
 // in ascending rank-key order), then the exact normaliser over those k.
-// Called by every thread after the barrier that follows the fetch.
-//   1. (wave 0, lane t for list t) A bound U: with m = ceil(Ke / S), the
-//      first m keys of every list hold at least Ke keys, so the Ke-th smallest
-//      key overall is at most the largest of the lists' m-th keys; only keys
-//      <= U can rank below Ke. Each list's keys <= U are a prefix; its length
-//      and offset go to LDS.
-//   2. (every thread) A candidate's rank is the count of keys below it. Every
-//      key below a candidate x <= U is itself <= U, so it is a candidate too:
-//      with at most kRowWin candidates, they are copied together and each is
-//      ranked against the others with LDS broadcast reads. With more, the
-//      count runs over the lists: branch-free lower bounds, 7 halving steps
-//      over 16 lists at a time in lockstep (loads always in bounds). Rank keys
-//      are unique, so ranks below Ke are distinct.
-__device__ __forceinline__ void fin_merge_topk(uint32_t S, uint32_t K, FinSmem& sm, float inv_t) {
+// Called by every thread with the lists from fin_load_topk; every wave holds
+// the slice headers (lane s: slice s), so the list lengths need no exchange.
+//   1. A bound U: with m = ceil(Ke / S), the first m keys of every list hold
+//      at least Ke keys, so the Ke-th smallest key overall is at most the
+//      largest of the lists' m-th keys; only keys <= U can rank below Ke. Each
+//      wave takes the largest over its lists, U is the largest of the four.
+//   2. Each list's keys <= U are a prefix; the owning wave counts it with a
+//      ballot, every wave scans the counts into offsets, and the prefixes are
+//      copied together from registers.
+//   3. A candidate's rank is the count of keys below it. Every key below a
+//      candidate x <= U is itself <= U, so it is a candidate too: with at most
+//      kRowWin candidates each is ranked against the others with LDS
+//      broadcast reads. With more, the count runs over the lists (staged in
+//      LDS, kTopKMax apart): branch-free lower bounds, 7 halving steps over 16
+//      lists at a time in lockstep (loads always in bounds). Rank keys are
+//      unique, so ranks below Ke are distinct.
+// The row's exact-path flag sm.fin_fb, set before the call, is read after the
+// first barrier; the function returns early (uniformly) when it is set.
+__device__ __forceinline__ void fin_merge_topk(uint64_t h0, const uint64_t (&kk)[kTkPer], const float (&rr)[kTkPer],
+                                               uint32_t S, uint32_t K, FinSmem& sm, float inv_t) {
     const uint32_t tid = tid_x();
     const int lane = lane_id();
-    static_assert(kSsTopKMerge <= 8 * kFinThreads && kTopKMax <= 64 && kSsMaxSlices <= kWave, "merge shape");
-    if (tid < kWave) {
-        const bool mine = (uint32_t)lane < S;
-        const uint32_t t = mine ? (uint32_t)lane : 0u;
-        const uint32_t n = mine ? sm.tk_ns[t] : 0u;
-        const uint32_t Ke = min(K, wave_sum_u(n));
-        const uint32_t m = (Ke + S - 1) / S;
-        const uint32_t c = min(m, n);
-        const uint32_t sub = wave_sum_u(c);
-        const uint64_t kv = c > 0u ? sm.u.f.tkey[t * K + c - 1] : 0ull;
-        uint64_t U = 0;
-        for (uint32_t l = 0; l < S; ++l) {
-            const uint64_t v = readlane_u64(kv, (int)l);
-            U = v > U ? v : U;
-        }
-        if (sub < Ke) U = ~0ull;
-        uint32_t cs = 0;   // keys <= U in this list
+    const int wv = __builtin_amdgcn_readfirstlane((int)(tid / kWave));
+    static_assert(kSsTopKMerge == kSsMaxSlices * kTopKMax && kTopKMax == kWave && kSsMaxSlices <= kWave &&
+                      kFinThreads == 4 * kWave,
+                  "merge shape");
+    const bool mine = (uint32_t)lane < S;
+    const uint32_t n = mine ? min((uint32_t)(h0 >> 32) & 0xffffu, K) : 0u;   // lane s: list s's length
+    const uint32_t Ke = min(K, wave_sum_u(n));
+    const uint32_t m = (Ke + S - 1) / S;
+    const uint32_t c = min(m, n);
+    const uint32_t sub = wave_sum_u(c);
+    uint64_t um = 0;
 #pragma unroll
-        for (uint32_t step = 64; step >= 1; step >>= 1) {
-            const uint32_t q = cs + step;
-            const uint32_t qq = q < n ? q : n;
-            const uint64_t v = sm.u.f.tkey[t * K + (qq > 0u ? qq - 1u : 0u)];
-            cs = (q <= n && v <= U) ? q : cs;
+    for (uint32_t i = 0; i < kTkPer; ++i) {
+        const uint32_t s = 4 * i + (uint32_t)wv;
+        if (s < S) {   // (uniform)
+            const uint32_t cs = (uint32_t)__builtin_amdgcn_readlane((int)c, (int)s);
+            um = (lane + 1 == (int)cs && kk[i] > um) ? kk[i] : um;
+            sm.u.f.tkey[s * kTopKMax + lane] = kk[i];   // for the count over lists
+            sm.u.f.traw[s * kTopKMax + lane] = rr[i];
         }
-        const uint32_t incl = wave_scan_incl_u(cs);
-        const uint32_t nc = wave_sum_u(cs);   // (a whole-wave reduction: outside the lane-0 branch)
-        if (mine) { sm.tk_cs[t] = cs; sm.tk_base[t] = incl - cs; }
-        if (lane == 0) { sm.tk_ke = Ke; sm.tk_nc = nc; }
+    }
+    um = wave_max_u64(um);
+    if (lane == 0) sm.tk_u[wv] = um;
+    __syncthreads();
+    if (sm.fin_fb) return;
+    uint64_t U = sm.tk_u[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) U = sm.tk_u[w] > U ? sm.tk_u[w] : U;
+    if (sub < Ke) U = ~0ull;
+#pragma unroll
+    for (uint32_t i = 0; i < kTkPer; ++i) {
+        const uint32_t s = 4 * i + (uint32_t)wv;
+        if (s < S) {
+            const uint32_t ns = (uint32_t)__builtin_amdgcn_readlane((int)n, (int)s);
+            const uint32_t cnt = (uint32_t)__builtin_popcountll(ballot((uint32_t)lane < ns && kk[i] <= U));
+            if (lane == 0) sm.tk_cs[s] = cnt;
+        }
     }
     __syncthreads();
-    const uint32_t Ke = sm.tk_ke, ncand = sm.tk_nc;
-    auto cand_index = [&](uint32_t k) -> uint32_t {   // k-th candidate's place in tkey
-        uint32_t s = 0;
-        for (uint32_t t = 1; t < S; ++t) s = k >= sm.tk_base[t] ? t : s;   // bases ascend
-        return s * K + (k - sm.tk_base[s]);
-    };
+    const uint32_t cs = mine ? sm.tk_cs[lane] : 0u;
+    const uint32_t incl = wave_scan_incl_u(cs);
+    const uint32_t ncand = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
     if (ncand <= kRowWin) {   // uniform
-        if (tid < ncand) {
-            const uint32_t i = cand_index(tid);
-            sm.u.f.ent[tid] = sm.u.f.tkey[i];
-            sm.u.f.entraw[tid] = sm.u.f.traw[i];
+#pragma unroll
+        for (uint32_t i = 0; i < kTkPer; ++i) {
+            const uint32_t s = 4 * i + (uint32_t)wv;
+            if (s < S) {
+                const uint32_t cl = (uint32_t)__builtin_amdgcn_readlane((int)cs, (int)s);
+                const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)(incl - cs), (int)s);
+                if ((uint32_t)lane < cl) {
+                    sm.u.f.ent[b + lane] = kk[i];
+                    sm.u.f.entraw[b + lane] = rr[i];
+                }
+            }
         }
-        __syncthreads();
-        if (tid < ncand) {
-            const uint64_t x = sm.u.f.ent[tid];
-            uint32_t rank = 0;
-            for (uint32_t j0 = 0; j0 < ncand; j0 += 8) {   // 8 broadcast reads per LDS round trip
-                uint64_t e[8];
+        // keys past the candidates read as the largest key (no candidate is
+        // below it), up to the next multiple of 32 the ranking may read
+        if (wv == 0 && ncand + (uint32_t)lane < kRowWin && (uint32_t)lane < 32u) sm.u.f.ent[ncand + lane] = ~0ull;
+    } else if (wv == 0 && mine) {
+        sm.tk_ns[lane] = n;
+        sm.tk_base[lane] = incl - cs;
+    }
+    __syncthreads();
+    if (ncand <= kRowWin) {   // uniform
+        // P adjacent threads rank one candidate, each against the keys
+        // j = p (mod P); a quad DPP sum joins their counts. Reads stay below
+        // the next multiple of 8P of ncand, which is at most kRowWin.
+        const uint32_t P = ncand <= kWave ? 4u : ncand <= 2 * kWave ? 2u : 1u;
+        const uint32_t k = min(tid / P, ncand > 0u ? ncand - 1u : 0u), p = tid % P;
+        const uint64_t x = sm.u.f.ent[k];
+        const uint32_t nj = (ncand + P - 1) / P;
+        uint32_t rank = 0;
+        for (uint32_t i0 = 0; i0 < nj; i0 += 8) {   // 8 broadcast reads per LDS round trip
+            uint64_t e[8];
 #pragma unroll
-                for (uint32_t u = 0; u < 8; ++u) e[u] = sm.u.f.ent[min(j0 + u, kRowWin - 1)];
+            for (uint32_t u = 0; u < 8; ++u) e[u] = sm.u.f.ent[p + P * (i0 + u)];
 #pragma unroll
-                for (uint32_t u = 0; u < 8; ++u) rank += (j0 + u < ncand && e[u] < x) ? 1u : 0u;
-            }
-            if (rank < Ke) {
-                sm.u.f.sorted[rank] = x;
-                sm.u.f.sortedraw[rank] = sm.u.f.entraw[tid];
-            }
+            for (uint32_t u = 0; u < 8; ++u) rank += e[u] < x ? 1u : 0u;
+        }
+        if (P >= 2) rank += (uint32_t)dpp_i<0xB1>(0, (int)rank);   // quad_perm [1,0,3,2]
+        if (P == 4) rank += (uint32_t)dpp_i<0x4E>(0, (int)rank);   // quad_perm [2,3,0,1]
+        if (p == 0 && tid / P < ncand && rank < Ke) {
+            sm.u.f.sorted[rank] = x;
+            sm.u.f.sortedraw[rank] = sm.u.f.entraw[k];
         }
     }
     for (uint32_t k = tid; ncand > kRowWin && k < ncand; k += kFinThreads) {
-        const uint32_t i = cand_index(k);
+        uint32_t ls = 0;   // the list of the k-th candidate (offsets ascend)
+        for (uint32_t t = 1; t < S; ++t) ls = k >= sm.tk_base[t] ? t : ls;
+        const uint32_t i = ls * kTopKMax + (k - sm.tk_base[ls]);
         const uint64_t x = sm.u.f.tkey[i];
         uint32_t rank = 0;
         for (uint32_t t0 = 0; t0 < S; t0 += 16) {   // uniform
@@ -1222,7 +1235,7 @@ __device__ __forceinline__ void fin_merge_topk(uint32_t S, uint32_t K, FinSmem& 
                     const uint32_t q = lo[u] + step;
                     const uint32_t qq = q < ns[u] ? q : ns[u];
                     const uint32_t t = t0 + u < S ? t0 + u : 0u;
-                    const uint64_t v = sm.u.f.tkey[t * K + (qq > 0u ? qq - 1u : 0u)];
+                    const uint64_t v = sm.u.f.tkey[t * kTopKMax + (qq > 0u ? qq - 1u : 0u)];
                     lo[u] = (q <= ns[u] && v < x) ? q : lo[u];
                 }
             }
@@ -1347,7 +1360,7 @@ __device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, Fi
 // into SGPRs at wave launch, so each wave's record loads go out at once,
 // before the row's parameters arrive (a row of another path reads a stale
 // record, unused, and returns).
-template <int G>
+template <int G, bool TK>
 __global__ __launch_bounds__(kFinThreads) void row_fin(const lcs_params* params, const uint64_t* srecs, uint32_t rows,
                                                        uint32_t vocab, uint32_t flags, uint32_t slices, uint32_t n_top,
                                                        SampleArgs a) {
@@ -1368,16 +1381,24 @@ __global__ __launch_bounds__(kFinThreads) void row_fin(const lcs_params* params,
     for (int w = 0; w < (int)rec::kHdr; ++w) hd[w] = my[w];
     uint64_t wk[kSpecWin], tk[kTopMax];
     uint32_t wr[kSpecWin];
-    if (wv == 0) {
+    auto load_window = [&]() {
 #pragma unroll
         for (int j = 0; j < (int)kSpecWin; ++j) {
             wk[j] = my[rec::kWin + j];
             wr[j] = (uint32_t)my[rec::kWinRaw + j];
         }
+    };
+    if (wv == 0 && !TK) {   // (with TK, a window row loads it once its mode is known)
+        load_window();
     } else if (wv == 1) {
 #pragma unroll
         for (int j = 0; j < (int)kTopMax; ++j) tk[j] = (uint32_t)j < ntop ? my[rec::kTop + j] : ~0ull;
     }
+    // top-k rows: the slices' lists, requested at launch when the host saw
+    // top-k rows in the batch (TK)
+    uint64_t tkk[kTkPer];
+    float tkr[kTkPer];
+    if (TK) fin_load_topk(recs, S, wv, tkk, tkr);
     const lcs_params P = scalar_load(params + row);
     const bool masked = a.mask != nullptr && (a.has_mask == nullptr || scalar_load_u8(a.has_mask + row) != 0);
     const uint32_t mode = row_mode(P, masked, vocab);
@@ -1399,17 +1420,14 @@ __global__ __launch_bounds__(kFinThreads) void row_fin(const lcs_params* params,
     PROF_AT(kProfFin + row, 4 + wv);
     bool fb = false;
     if (topk) {
-        if (wv == 0) {
-            fb = fin_topk_lengths(S, P.top_k, sm, hd[0]);
-        } else if (wv == 1) {
-            if (want_lp) fb = fin_logz(hd, tk, S, ntop, sm);
-        } else {
-            fin_fetch_topk(recs, S, P.top_k, sm);
-        }
+        if (!TK) fin_load_topk(recs, S, wv, tkk, tkr);
+        if (wv == 1 && want_lp) fb = fin_logz(hd, tk, S, ntop, sm);
+        // a slice that could not rank its list sends the row to the exact path
+        if (wv == 0) fb = ballot((uint32_t)lane < S && ((uint32_t)(hd[0] >> 48) & rec::kFlagWinLost)) != 0;
         if (fb && lane == 0) sm.fin_fb = 1u;
-        __syncthreads();
-        if (!sm.fin_fb) fin_merge_topk(S, P.top_k, sm, inv_t);
+        fin_merge_topk(hd[0], tkk, tkr, S, P.top_k, sm, inv_t);
     } else if (wv == 0) {
+        if (stoch && TK) load_window();
         if (stoch) fb = fin_window(hd, wk, wr, my, S, P, sm, inv_t);
         else fin_greedy(a, hd, S, vocab, row, masked, sm);
     } else if (wv == 1) {
@@ -1486,13 +1504,13 @@ hipError_t launch_slice(const SampleArgs& a, hipStream_t st) {
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (a.dtype == LCS_BF16) {
-        hipLaunchKernelGGL(row_fin<8>, dim3(a.rows), dim3(kFinThreads), 0, st, a.params, a.srecs, a.rows, a.vocab,
-                           a.flags, a.ss_slices, a.n_top, a);
-    } else {
-        hipLaunchKernelGGL(row_fin<4>, dim3(a.rows), dim3(kFinThreads), 0, st, a.params, a.srecs, a.rows, a.vocab,
-                           a.flags, a.ss_slices, a.n_top, a);
-    }
+    // (an instantiation that requests the top-k lists at launch, for batches
+    // the host saw holding top-k rows)
+    const bool tk = (a.ss_modes & kModeTopK) != 0u;
+    const auto fin = a.dtype == LCS_BF16 ? (tk ? row_fin<8, true> : row_fin<8, false>)
+                                         : (tk ? row_fin<4, true> : row_fin<4, false>);
+    hipLaunchKernelGGL(fin, dim3(a.rows), dim3(kFinThreads), 0, st, a.params, a.srecs, a.rows, a.vocab, a.flags,
+                       a.ss_slices, a.n_top, a);
     return hipGetLastError();
 }
 

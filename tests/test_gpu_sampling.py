@@ -318,6 +318,38 @@ def test_topk_rows_on_the_sliced_path(sampler):
     assert paths[ks.index(65)] == 6
 
 
+def test_topk_merge_past_the_candidate_window(sampler):
+    """Top-k rows whose slice lists leave more than 256 candidates under the
+    merge's bound: slice 0 holds one large logit, every other slice 64 large
+    ones, so the bound (the largest of the lists' m-th keys) falls in slice
+    0's noise and admits every other list whole. Those rows are ranked by the
+    count over the lists; top_k 5 stays under the bound's window."""
+    g = np.random.default_rng(20261431)
+    V, rows = 128256, 6
+    S = -(-V // 8192)
+    L = -(-V // S)
+    logits = g.standard_normal((rows, V)).astype(np.float32)
+    for r in range(rows):
+        logits[r, int(g.integers(0, L))] = 100.0
+        for s in range(1, S):
+            lo, hi = s * L, min(V, (s + 1) * L)
+            pos = g.choice(hi - lo, 64, replace=False) + lo
+            logits[r, pos] = (60.0 + 39.0 * g.random(64)).astype(np.float32)
+    p = W.default_params(rows)
+    ks = [64, 64, 40, 17, 5, 64]
+    for r in range(rows):
+        p["top_k"][r] = ks[r]
+        p["temperature"][r] = [1.0, 30.0, 10.0][r % 3]
+        p["top_p"][r] = [1.0, 0.9][r % 2]
+        p["min_p"][r] = 0.0
+    seeds = np.array([W.row_seed(20261431, r) for r in range(rows)], dtype=np.uint64)
+    hoff = np.zeros(rows + 1, dtype=np.uint32)
+    w = W.Workload("topk-many", rows, V, "f32", logits, p, seeds, W.uniforms(seeds), hoff,
+                   np.zeros(0, dtype=np.int32), None, 3, True)
+    out = run(sampler, w)
+    compare(w, out, O.sample_batch(w, threads=8), "topk-many", expect_paths={5})
+
+
 def test_nucleus_rows(sampler):
     """Stochastic rows without top_k run on the sliced nucleus path (path 6):
     top-p only, constrained rows (with and without min-p), plain temperature,
