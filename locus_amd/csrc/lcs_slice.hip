@@ -1146,8 +1146,6 @@ __device__ __forceinline__ void fin_merge_topk(uint64_t h0, const uint64_t (&kk)
         if (s < S) {   // (uniform)
             const uint32_t cs = (uint32_t)__builtin_amdgcn_readlane((int)c, (int)s);
             um = (lane + 1 == (int)cs && kk[i] > um) ? kk[i] : um;
-            sm.u.f.tkey[s * kTopKMax + lane] = kk[i];   // for the count over lists
-            sm.u.f.traw[s * kTopKMax + lane] = rr[i];
         }
     }
     um = wave_max_u64(um);
@@ -1187,30 +1185,41 @@ __device__ __forceinline__ void fin_merge_topk(uint64_t h0, const uint64_t (&kk)
         // keys past the candidates read as the largest key (no candidate is
         // below it), up to the next multiple of 32 the ranking may read
         if (wv == 0 && ncand + (uint32_t)lane < kRowWin && (uint32_t)lane < 32u) sm.u.f.ent[ncand + lane] = ~0ull;
-    } else if (wv == 0 && mine) {
-        sm.tk_ns[lane] = n;
-        sm.tk_base[lane] = incl - cs;
+    } else {   // the lists staged for the count over lists
+#pragma unroll
+        for (uint32_t i = 0; i < kTkPer; ++i) {
+            const uint32_t s = 4 * i + (uint32_t)wv;
+            if (s < S) {
+                sm.u.f.tkey[s * kTopKMax + lane] = kk[i];
+                sm.u.f.traw[s * kTopKMax + lane] = rr[i];
+            }
+        }
+        if (wv == 0 && mine) {
+            sm.tk_ns[lane] = n;
+            sm.tk_base[lane] = incl - cs;
+        }
     }
     __syncthreads();
     if (ncand <= kRowWin) {   // uniform
         // P adjacent threads rank one candidate, each against the keys
         // j = p (mod P); a quad DPP sum joins their counts. Reads stay below
         // the next multiple of 8P of ncand, which is at most kRowWin.
-        const uint32_t P = ncand <= kWave ? 4u : ncand <= 2 * kWave ? 2u : 1u;
-        const uint32_t k = min(tid / P, ncand > 0u ? ncand - 1u : 0u), p = tid % P;
+        const uint32_t lp = ncand <= kWave ? 2u : ncand <= 2 * kWave ? 1u : 0u;   // P = 2^lp
+        const uint32_t P = 1u << lp;
+        const uint32_t k = min(tid >> lp, ncand > 0u ? ncand - 1u : 0u), p = tid & (P - 1u);
         const uint64_t x = sm.u.f.ent[k];
-        const uint32_t nj = (ncand + P - 1) / P;
+        const uint32_t nj = (ncand + P - 1u) >> lp;
         uint32_t rank = 0;
         for (uint32_t i0 = 0; i0 < nj; i0 += 8) {   // 8 broadcast reads per LDS round trip
             uint64_t e[8];
 #pragma unroll
-            for (uint32_t u = 0; u < 8; ++u) e[u] = sm.u.f.ent[p + P * (i0 + u)];
+            for (uint32_t u = 0; u < 8; ++u) e[u] = sm.u.f.ent[p + ((i0 + u) << lp)];
 #pragma unroll
             for (uint32_t u = 0; u < 8; ++u) rank += e[u] < x ? 1u : 0u;
         }
-        if (P >= 2) rank += (uint32_t)dpp_i<0xB1>(0, (int)rank);   // quad_perm [1,0,3,2]
-        if (P == 4) rank += (uint32_t)dpp_i<0x4E>(0, (int)rank);   // quad_perm [2,3,0,1]
-        if (p == 0 && tid / P < ncand && rank < Ke) {
+        if (lp >= 1) rank += (uint32_t)dpp_i<0xB1>(0, (int)rank);   // quad_perm [1,0,3,2]
+        if (lp == 2) rank += (uint32_t)dpp_i<0x4E>(0, (int)rank);   // quad_perm [2,3,0,1]
+        if (p == 0 && (tid >> lp) < ncand && rank < Ke) {
             sm.u.f.sorted[rank] = x;
             sm.u.f.sortedraw[rank] = sm.u.f.entraw[k];
         }
