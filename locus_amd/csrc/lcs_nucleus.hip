@@ -50,6 +50,7 @@ constexpr int kNW = NT / kWave;
 constexpr uint32_t kNone = 0xffffffffu;
 constexpr uint32_t kNucCand = 128;     // top-n candidates one slice holds
 constexpr uint32_t kGroupMax = 4 * kWave;  // candidates one decisive group may hold
+constexpr uint32_t kNucKeyCache = 2048;     // compacted candidates the select finalize keeps in LDS
 constexpr float kL2E = 1.4426950408889634f;
 constexpr double kGuard = 1e-10;
 }  // namespace
@@ -85,6 +86,7 @@ struct NucFinC {
     uint64_t gkey[kGroupMax];             // decisive group (rank keys)
     uint64_t gsorted[kGroupMax];
     double gw[kGroupMax];                 // weights in rank order
+    uint64_t lkey[kNucKeyCache];          // the row's first compacted candidates (rank keys)
 };
 struct NucSmem {
     union {
@@ -102,12 +104,13 @@ struct NucSmem {
     NucLocal l;
 };
 __shared__ NucSmem g_nuc;
+static_assert(sizeof(NucFinC) <= sizeof(uint32_t) * kSliceMax, "the select finalize's LDS fits the union");
 
 // The select finalize's code of each compacted candidate: range k and
 // sub-bin s as k * kNucSub + s, kNoCode outside the planned ranges. Only
 // that kernel references it, so only it allocates the LDS.
 constexpr uint16_t kNoCode = 0xffffu;
-__shared__ uint16_t g_code[kNucList];
+__shared__ __align__(16) uint16_t g_code[kNucList];
 
 #ifdef LCS_PROFILE
 // Phase timestamps (wall clock, 100 MHz) of the per-row finalize kernels for
@@ -1037,7 +1040,9 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     };
     for (uint32_t i = tid; i < n; i += NT) {
         uint32_t k, s;
-        const float x = locate(list[i], k, s);
+        const uint64_t key = list[i];
+        if (i < kNucKeyCache) sm.u.fc.lkey[i] = key;
+        const float x = locate(key, k, s);
         g_code[i] = k < kNucRanges ? (uint16_t)(k * kNucSub + s) : kNoCode;
         if (k < kNucRanges) {
             atomicAdd(&sm.u.fc.scnt[k][s], 1u);
@@ -1064,17 +1069,23 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     auto c_before = [&](uint32_t k, uint32_t s) -> uint32_t { return rgl[k].c0 + (s > 0 ? sm.u.fc.scnt[k][s - 1] : 0u); };
     auto m_before = [&](uint32_t k, uint32_t s) -> double { return rgl[k].m0 + (s > 0 ? sm.u.fc.smass[k][s - 1] : 0.0); };
     auto m_incl = [&](uint32_t k, uint32_t s) -> double { return rgl[k].m0 + sm.u.fc.smass[k][s]; };
+    // compacted candidate i (the first kNucKeyCache from LDS)
+    auto key_at = [&](uint32_t i) -> uint64_t { return i < kNucKeyCache ? sm.u.fc.lkey[i] : list[i]; };
+    // first sub-bin of range j whose inclusive value v(j, s) reaches t (the
+    // values ascend with s; kNucSub - 1 when none does): lane l tests
+    // sub-bins 2l and 2l + 1, a ballot finds the first. Called by whole waves.
+    auto first_sub = [&](bool r0, bool r1) -> uint32_t {
+        const uint64_t b0 = ballot(r0), b1 = ballot(r1);
+        const uint32_t f0 = b0 ? 2u * (uint32_t)__builtin_ctzll(b0) : kNucSub;
+        const uint32_t f1 = b1 ? 2u * (uint32_t)__builtin_ctzll(b1) + 1u : kNucSub;
+        return min(min(f0, f1), kNucSub - 1u);
+    };
     // first (range, sub-bin) whose inclusive mass reaches t (by rank order)
     auto find_mass = [&](double t, uint32_t& k, uint32_t& s) -> bool {
         for (uint32_t j = 0; j < nrg && j < kNucRanges; ++j) {
             if (rgl[j].m0 + rgl[j].m >= t && rgl[j].m0 <= t * (1.0 + kGuard)) {
-                int lo = 0, hi = (int)kNucSub - 1;
-                while (lo < hi) {
-                    const int mid = (lo + hi) >> 1;
-                    if (m_incl(j, (uint32_t)mid) >= t) hi = mid; else lo = mid + 1;
-                }
                 k = j;
-                s = (uint32_t)lo;
+                s = first_sub(m_incl(j, 2u * lane) >= t, m_incl(j, 2u * lane + 1u) >= t);
                 return true;
             }
         }
@@ -1084,20 +1095,17 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     auto find_count = [&](uint32_t n, uint32_t& k, uint32_t& s) -> bool {
         for (uint32_t j = 0; j < nrg && j < kNucRanges; ++j) {
             if (rgl[j].c0 < n && rgl[j].c0 + rgl[j].cnt >= n) {
-                int lo = 0, hi = (int)kNucSub - 1;
-                while (lo < hi) {
-                    const int mid = (lo + hi) >> 1;
-                    if (rgl[j].c0 + sm.u.fc.scnt[j][mid] >= n) hi = mid; else lo = mid + 1;
-                }
                 k = j;
-                s = (uint32_t)lo;
+                s = first_sub(rgl[j].c0 + sm.u.fc.scnt[j][2u * lane] >= n, rgl[j].c0 + sm.u.fc.scnt[j][2u * lane + 1u] >= n);
                 return true;
             }
         }
         return false;
     };
     // Gathers the candidates of range k's sub-bins [s0, s1] into gkey and ranks
-    // them (wave 0) into gsorted with weights gw. Every thread calls it.
+    // them into gsorted with weights gw: P = 1, 2 or 4 adjacent threads rank
+    // one candidate, each against the keys j = p (mod P), joined by a quad
+    // DPP sum. Every thread calls it.
     // (gather i counts into ngc[i & 1], which was cleared during gather i - 1,
     // after every thread had read it in gather i - 2)
     uint32_t gidx = 0;
@@ -1106,27 +1114,47 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
         if (tid == 0) sm.l.ngc[(gidx + 1u) & 1u] = 0u;
         ++gidx;
         // (the codes in LDS select the group; only its keys are read again)
+        // (four codes per thread per LDS read; codes past n are stale and
+        // skipped, kNucList is a multiple of 4)
         const uint32_t c0 = k * kNucSub + s0, c1 = k * kNucSub + s1;
-        for (uint32_t i = tid; i < n; i += NT) {
-            const uint32_t c = g_code[i];
-            if (c >= c0 && c <= c1) {
-                const uint32_t slot = atomicAdd(cnt, 1u);
-                if (slot < kGroupMax) sm.u.fc.gkey[slot] = list[i];
+        static_assert(kNucList % 4 == 0, "code quads");
+        for (uint32_t i4 = 4 * tid; i4 < n; i4 += 4 * NT) {
+            const uint2 cq = *reinterpret_cast<const uint2*>(&g_code[i4]);
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) {
+                const uint32_t c = ((q < 2 ? cq.x : cq.y) >> (16 * (q & 1))) & 0xffffu;
+                if (i4 + q < n && c >= c0 && c <= c1) {
+                    const uint32_t slot = atomicAdd(cnt, 1u);
+                    if (slot < kGroupMax) sm.u.fc.gkey[slot] = key_at(i4 + q);
+                }
             }
         }
         __syncthreads();
         const uint32_t ng = *cnt;
-        if (ng <= kGroupMax && wv == 0) {
-            uint64_t kk[4];
-            uint32_t rk[4];
-            lds_rank4(sm.u.fc.gkey, ng, kk, rk);
+        static_assert(kGroupMax == NT, "one thread per group candidate at most");
+        if (ng <= kGroupMax) {   // uniform
+            const uint32_t lp = ng <= kWave ? 2u : ng <= 2 * kWave ? 1u : 0u;   // P = 2^lp
+            const uint32_t last = ng > 0u ? ng - 1u : 0u;
+            const uint32_t kc = tid >> lp, p = tid & ((1u << lp) - 1u);
+            const uint64_t x = sm.u.fc.gkey[min(kc, last)];
+            const uint32_t nj = (ng + (1u << lp) - 1u) >> lp;   // keys of partition p (some past ng)
+            uint32_t rank = 0;
+            for (uint32_t i0 = 0; i0 < nj; i0 += 8) {   // 8 broadcast reads per LDS round trip
+                uint64_t e[8];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
-                if (e < ng) {
-                    sm.u.fc.gsorted[rk[c]] = kk[c];
-                    sm.u.fc.gw[rk[c]] = exp_f64((double)tempered(rank_val(kk[c]), maxl, inv_t));
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t j = p + ((i0 + (uint32_t)u) << lp);
+                    e[u] = sm.u.fc.gkey[min(j, last)];
+                    e[u] = j < ng ? e[u] : ~0ull;   // (no key is below ~0)
                 }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) rank += e[u] < x ? 1u : 0u;
+            }
+            if (lp >= 1) rank += (uint32_t)dpp_i<0xB1>(0, (int)rank);   // quad_perm [1,0,3,2]
+            if (lp == 2) rank += (uint32_t)dpp_i<0x4E>(0, (int)rank);   // quad_perm [2,3,0,1]
+            if (p == 0 && kc < ng) {
+                sm.u.fc.gsorted[rank] = x;
+                sm.u.fc.gw[rank] = exp_f64((double)tempered(rank_val(x), maxl, inv_t));
             }
         }
         __syncthreads();
@@ -1255,7 +1283,7 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
             for (uint32_t i = tid; i < n; i += NT) {
                 const uint32_t c = g_code[i];
                 if (c != kNoCode && c / kNucSub == km) {
-                    const uint64_t key = list[i];
+                    const uint64_t key = key_at(i);
                     const double w = exp_f64((double)tempered(rank_val(key), maxl, inv_t));
                     if (w / SK >= thresh) {
                         ++cnt;
