@@ -155,13 +155,24 @@ def test_edge_cases_padded_stride(sampler):
         compare(w, g, O.sample_batch(w), f"edge-padded-{w.name}")
 
 
-def test_deterministic_and_host_params_optional(sampler):
+@pytest.mark.parametrize("kind", ["c2", "topk"])
+def test_deterministic_and_host_params_optional(sampler, kind):
+    """Without params_host the host cannot pick the row modes' launch shapes
+    (for top-k rows: the finalize that requests the lists at launch); the
+    results must not change."""
     w = W.make("c2", rows=16, set_index=5)
+    if kind == "topk":
+        p = w.params.copy()
+        p["top_k"] = [40, 5, 64, 1, 17, 40, 0, 40, 64, 2, 40, 8, 33, 40, 64, 40]
+        w = W.Workload("topk-hp", w.rows, w.vocab, "f32", w.logits, p, w.seeds, w.u, w.hist_off, w.hist_ids,
+                       None, w.n_top, w.want_logprobs)
     a = run(sampler, w)
     b = run(sampler, w, use_host_params=False)
     assert np.array_equal(a["ids"], b["ids"])
     assert a["diag"].tobytes() == b["diag"].tobytes()
     assert np.array_equal(a["top_lp"], b["top_lp"])
+    if kind == "topk":
+        compare(w, a, O.sample_batch(w, threads=8), "topk-hp", expect_paths={2, 3, 4, 5})
 
 
 def test_missing_u_is_rejected_before_any_launch(sampler):
