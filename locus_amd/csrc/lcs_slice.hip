@@ -1118,8 +1118,8 @@ __device__ __forceinline__ void fin_load_topk(const uint64_t* recs, uint32_t S, 
 //      copied together from registers.
 //   3. A candidate's rank is the count of keys below it. Every key below a
 //      candidate x <= U is itself <= U, so it is a candidate too: with at most
-//      kRowWin candidates each is ranked against the others with LDS
-//      broadcast reads. With more, the count runs over the lists (staged in
+//      kRowWin candidates each is ranked against the others by 1, 2 or 4
+//      threads with LDS reads. With more, the count runs over the lists (staged in
 //      LDS, kTopKMax apart): branch-free lower bounds, 7 halving steps over 16
 //      lists at a time in lockstep (loads always in bounds). Rank keys are
 //      unique, so ranks below Ke are distinct.
@@ -1210,7 +1210,7 @@ __device__ __forceinline__ void fin_merge_topk(uint64_t h0, const uint64_t (&kk)
         const uint64_t x = sm.u.f.ent[k];
         const uint32_t nj = (ncand + P - 1u) >> lp;
         uint32_t rank = 0;
-        for (uint32_t i0 = 0; i0 < nj; i0 += 8) {   // 8 broadcast reads per LDS round trip
+        for (uint32_t i0 = 0; i0 < nj; i0 += 8) {   // 8 reads per LDS round trip (P addresses each)
             uint64_t e[8];
 #pragma unroll
             for (uint32_t u = 0; u < 8; ++u) e[u] = sm.u.f.ent[p + ((i0 + u) << lp)];
