@@ -258,9 +258,10 @@ def mask_bench(budget_s: float = 5.0):
 def draft_bench(n_seq: int = 512, ctx_len: int = 4096, ngram: int = 3, max_draft: int = 7,
                 steps: int = 200, cpu_seconds: float = 3.0):
     """Batched n-gram drafts on the device (lcs_ngram_draft) for C5's 512
-    sequences, each with a 4096-token context over a 64-token alphabet
-    (matches are found near the end), against the reference's per-sequence
-    ngram_draft (speculative.cpp:7-28) on one host core."""
+    sequences, each with a 4096-token context over a 64-token alphabet (a
+    trailing 3-gram rarely recurs there, so most sequences are searched back
+    to their first token), against the reference's per-sequence ngram_draft
+    (speculative.cpp:7-28) on one host core."""
     import ctypes as C
     import torch
 

@@ -8,11 +8,13 @@
 // than ngram, or when the trailing n-gram does not occur earlier.
 //
 // The workgroup stages the trailing n-gram in LDS and tests candidate starts
-// from the most recent backwards, 256 starts per round (one per thread; a
-// start s matches when ctx[s + k] == ctx[n - ngram + k] for every k). The
-// round's largest matching start is the answer when there is one; otherwise
-// the next round tests the 256 starts before it. Each round reads the
-// context once, coalesced (thread t's window begins at position s0 + t).
+// from the most recent backwards, kDraftChunk starts per round: the round's
+// tokens (its starts and the ngram - 1 tokens after the last one) are loaded
+// into LDS at once, coalesced, all loads issued before the first is used; each
+// thread then tests 16 starts (s = lo + t + 256 j) from LDS, one pattern
+// token at a time, until no lane of its wave has a start left. The round's
+// largest matching start is the answer when there is one; otherwise the next
+// round takes the kDraftChunk starts before it.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -22,11 +24,15 @@
 namespace lcs {
 
 constexpr int kDraftThreads = 256;
+constexpr uint32_t kDraftPer = 16;                          // starts per thread per round
+constexpr uint32_t kDraftChunk = kDraftThreads * kDraftPer;  // starts per round
+constexpr uint32_t kDraftTok = kDraftChunk + kDraftMaxNgram; // tokens a round stages (rounded up below)
+constexpr uint32_t kDraftLoads = (kDraftTok + kDraftThreads - 1) / kDraftThreads;
 
 __global__ __launch_bounds__(kDraftThreads) void ngram_draft_kernel(DraftArgs a) {
     __shared__ int32_t pat[kDraftMaxNgram];
+    __shared__ int32_t tok[kDraftLoads * kDraftThreads];
     __shared__ uint32_t red[kDraftThreads / kWave];
-    __shared__ uint32_t best_s;
     const uint32_t seq = wg_x();
     if (seq >= a.n_seq) return;
     const uint32_t tid = tid_x();
@@ -39,38 +45,53 @@ __global__ __launch_bounds__(kDraftThreads) void ngram_draft_kernel(DraftArgs a)
     uint32_t len = 0;
     if (ng != 0u && md != 0u && n > ng) {
         if (tid < ng) pat[tid] = ctx[n - ng + tid];
-        if (tid == 0) best_s = kNoDraft;
-        __syncthreads();
-        // candidate starts n - ng - 1 down to 0, in rounds of kDraftThreads
-        const uint32_t last = n - ng - 1u;   // the most recent start before the trailing n-gram
-        for (uint32_t hi = last + 1u; hi > 0u;) {
-            const uint32_t lo = hi > (uint32_t)kDraftThreads ? hi - (uint32_t)kDraftThreads : 0u;
-            const uint32_t s = lo + tid;   // this thread's start, when s < hi
-            bool match = s < hi;
-            for (uint32_t k = 0; k < ng && ballot(match) != 0u; ++k) {
-                if (match) match = ctx[s + k] == pat[k];
-            }
-            // the largest matching start of the round (a wave max, then the block's)
-            // (start + 1, so that 0 stands for no match)
-            uint32_t wmax = match ? s + 1u : 0u;
+        // candidate starts n - ng - 1 down to 0, in rounds of kDraftChunk
+        uint32_t best = kNoDraft;
+        for (uint32_t hi = n - ng; hi > 0u;) {   // (uniform)
+            const uint32_t lo = hi > kDraftChunk ? hi - kDraftChunk : 0u;
+            // the round's tokens [lo, hi + ng - 1) (< n); loads clamped in bounds
+            const uint32_t end = hi + ng - 1u;
+            int32_t v[kDraftLoads];
 #pragma unroll
-            for (int sh = 32; sh >= 1; sh >>= 1) wmax = max(wmax, (uint32_t)__shfl_xor((int)wmax, sh));
-            if (lane == 0) red[wv] = wmax;
+            for (uint32_t i = 0; i < kDraftLoads; ++i) {
+                const uint32_t p = lo + tid + i * (uint32_t)kDraftThreads;
+                v[i] = ctx[p < end ? p : end - 1u];
+            }
+            __syncthreads();   // (the previous round's readers are done with tok; pat is in)
+#pragma unroll
+            for (uint32_t i = 0; i < kDraftLoads; ++i) tok[tid + i * (uint32_t)kDraftThreads] = v[i];
+            __syncthreads();
+            // bit j: start lo + tid + 256 j is in the round and still matches
+            uint32_t mm = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < kDraftPer; ++j) mm |= (lo + tid + j * (uint32_t)kDraftThreads < hi) ? 1u << j : 0u;
+            for (uint32_t k = 0; k < ng && ballot(mm != 0u) != 0u; ++k) {
+                const int32_t pk = pat[k];
+                uint32_t keep = 0;
+#pragma unroll
+                for (uint32_t j = 0; j < kDraftPer; ++j) {
+                    // (in bounds for every j: tid + 256 j + k < kDraftChunk + kDraftMaxNgram)
+                    keep |= tok[tid + j * (uint32_t)kDraftThreads + k] == pk ? 1u << j : 0u;
+                }
+                mm &= keep;
+            }
+            // the largest matching start (+1; 0: none) of the thread, the wave, the block
+            uint32_t f = mm ? lo + tid + (31u - (uint32_t)__builtin_clz(mm)) * (uint32_t)kDraftThreads + 1u : 0u;
+#pragma unroll
+            for (int sh = 32; sh >= 1; sh >>= 1) f = max(f, (uint32_t)__shfl_xor((int)f, sh));
+            if (lane == 0) red[wv] = f;
             __syncthreads();
             uint32_t found = 0u;
 #pragma unroll
             for (int w = 0; w < kDraftThreads / kWave; ++w) found = max(found, red[w]);
-            __syncthreads();   // (red is rewritten by the next round)
             if (found != 0u) {
-                if (tid == 0) best_s = found - 1u;
+                best = found - 1u;
                 break;
             }
             hi = lo;
         }
-        __syncthreads();
-        const uint32_t bs = best_s;
-        if (bs != kNoDraft) {
-            const uint32_t from = bs + ng;
+        if (best != kNoDraft) {
+            const uint32_t from = best + ng;
             len = min(md, n - from);
             for (uint32_t i = tid; i < len; i += kDraftThreads) out[i] = ctx[from + i];
         }
