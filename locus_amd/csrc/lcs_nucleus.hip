@@ -64,6 +64,7 @@ struct NucLocal {
     float t_s;
     uint32_t ncand, last, gbase;
     uint32_t bmap[kNucBins / 32];   // planned bins (select pass)
+    float piv[4];                   // or, for at most two ranges, their logit intervals (select pass)
     float mraw[kNW];
     double sraw[kNW];
     float mpen[kNW], npen[kNW], mmsk[kNW], nmsk[kNW];
@@ -1204,6 +1205,8 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     NPROF(row, 10);
     // ---- decisions; `fail` sends the row to the exact path ----
     bool fail = sm.l.out_flag != 0u;
+    // the list must hold every candidate the plan counted in its ranges
+    for (uint32_t k = 0; k < nrg && k < kNucRanges; ++k) fail = fail || sm.u.fc.scnt[k][kNucSub - 1] != rgl[k].cnt;
     uint32_t keep = ncand;
     double kept_sum = Stot;
     uint64_t last_key = ~0ull;     // the candidate at position keep - 1, when known
@@ -1407,9 +1410,49 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     in.start(a, row, slice, P, masked, early ? pre : nullptr);
     if (use_mask) in.load_mask();   // (its loads arrive with the logits')
     in.penalise(sm, P);
-    // the planned bins as a bitmap in LDS
-    if (tid < kNucBins / 32) {
-        const uint32_t nrg = scalar_load(&nr->nr);
+    const float inv_t = fdiv(1.0f, P.temperature);
+    // A logit's bin b(p) = nuc_bin(nuc_f(tempered(p))) is non-increasing in
+    // p (each step is monotone), so a range of bins [b0, b1] is an interval
+    // of logits [plo, phi]: plo the least float with b <= b1, phi the
+    // greatest with b >= b0, found by bisection over the ordered float keys
+    // (-inf .. +inf) with the same functions the histogram pass used. With at
+    // most two ranges the selection compares each logit with the intervals;
+    // with more it looks its bin up in a bitmap.
+    const uint32_t nrg = scalar_load(&nr->nr);
+    const bool iv = nrg <= 2u;
+    if (iv) {
+        // wave 2r: range r's plo, wave 2r + 1: its phi; a 64-way search, each
+        // step's 64 probes one per lane (the predicate holds on a prefix of
+        // the probes, so a ballot's count places the boundary)
+        const uint32_t r = (uint32_t)wv >> 1;
+        const bool up = ((uint32_t)wv & 1u) != 0u;
+        float bound = up ? -__builtin_huge_valf() : __builtin_huge_valf();   // empty
+        if (r < nrg) {   // (uniform in the wave)
+            const uint32_t b0 = nr->r[r].b0, b1 = nr->r[r].b1;
+            // pred(k): phi search: bin >= b0 (true from -inf up); plo search:
+            // bin > b1 (true from -inf up to just below plo)
+            auto pred = [&](uint32_t k) {
+                const uint32_t b = nuc_bin(nuc_f(tempered(key_to_f(k), maxl, inv_t), sx));
+                return up ? b >= b0 : b > b1;
+            };
+            constexpr uint32_t kMinus = 0x007fffffu, kPlus = 0xff800000u;   // keys of -inf, +inf
+            // invariant: pred(lo) holds or lo = kMinus - 1; pred(hi) fails or hi = kPlus + 1
+            uint64_t lo = up ? kMinus : (uint64_t)kMinus - 1u, hi = (uint64_t)kPlus + 1u;
+            while (hi - lo > 1u) {   // (uniform)
+                const uint64_t step = (hi - lo + 63u) / 64u;
+                const uint64_t k = lo + ((uint64_t)lane + 1u) * step;
+                const bool t = k < hi && pred((uint32_t)k);
+                const uint32_t nt = (uint32_t)__builtin_popcountll(ballot(t));
+                const uint64_t nlo = lo + (uint64_t)nt * step;
+                const uint64_t nhi = lo + ((uint64_t)nt + 1u) * step;
+                lo = nlo;
+                hi = nhi < hi ? nhi : hi;
+            }
+            // phi: the greatest key with bin >= b0; plo: the least with bin <= b1
+            bound = key_to_f((uint32_t)(up ? lo : hi));
+        }
+        if (lane == 0) sm.l.piv[wv] = bound;
+    } else if (tid < kNucBins / 32) {   // the planned bins as a bitmap
         uint32_t w = 0;
         for (uint32_t k = 0; k < nrg && k < kNucRanges; ++k) {
             const uint32_t b0 = scalar_load(&nr->r[k].b0), b1 = scalar_load(&nr->r[k].b1);
@@ -1421,15 +1464,24 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         sm.l.bmap[tid] = w;
     }
     __syncthreads();
-    const float inv_t = fdiv(1.0f, P.temperature);
     // bit q: element q is a candidate inside a planned range
     const uint32_t cm = in.cand_bits(use_mask);
     uint32_t sel = 0;
+    if (iv) {
+        const float l0 = sm.l.piv[0], h0 = sm.l.piv[1], l1 = sm.l.piv[2], h1 = sm.l.piv[3];
 #pragma unroll
-    for (int q = 0; q < kSliceElems; ++q) {
-        if ((cm >> q) & 1u) {
-            const uint32_t b = nuc_bin(nuc_f(tempered(in.v[q], maxl, inv_t), sx));
-            sel |= ((sm.l.bmap[b >> 5] >> (b & 31u)) & 1u) << q;
+        for (int q = 0; q < kSliceElems; ++q) {
+            const float p = in.v[q];
+            sel |= ((p >= l0 && p <= h0) || (p >= l1 && p <= h1)) ? 1u << q : 0u;
+        }
+        sel &= cm;
+    } else {
+#pragma unroll
+        for (int q = 0; q < kSliceElems; ++q) {
+            if ((cm >> q) & 1u) {
+                const uint32_t b = nuc_bin(nuc_f(tempered(in.v[q], maxl, inv_t), sx));
+                sel |= ((sm.l.bmap[b >> 5] >> (b & 31u)) & 1u) << q;
+            }
         }
     }
     // the workgroup's selections in thread order (one block scan) staged in
