@@ -64,6 +64,36 @@ def test_draft_random_and_long_contexts(sampler):
 
 
 @pytest.mark.gpu
+def test_draft_matches_at_round_boundaries(sampler):
+    """Contexts whose only earlier occurrence of the trailing n-gram starts at,
+    just before or just after a boundary between the kernel's rounds of 4096
+    candidate starts (the n-gram then straddles two rounds' token ranges), and
+    at the very first position."""
+    rng = np.random.default_rng(29)
+    chunk = 4096
+    for ng in (1, 2, 3, 7, 64):
+        ctxs = []
+        for n in (chunk + ng + 1, 2 * chunk + ng + 5, 3 * chunk + 2 * ng + 3):
+            last = n - ng - 1                     # the most recent candidate start
+            for j in (1, 2):
+                b = last + 1 - j * chunk          # a round boundary (first start of round j)
+                for s in (b - ng, b - 1, b, b + 1, 0):
+                    if not 0 <= s <= last:
+                        continue
+                    ctx = rng.integers(0, 1 << 20, n).astype(np.int32)
+                    pat = np.arange(7_000_000, 7_000_000 + ng, dtype=np.int32)
+                    ctx[n - ng:] = pat
+                    ctx[s:s + ng] = pat
+                    ctxs.append(ctx.tolist())
+        for md in (5, 256):
+            got, _ = sampler.ngram_draft(ctxs, ng, md)
+            for c, g in zip(ctxs, got):
+                want = O.ngram_draft(c, ng, md)
+                assert g == want, (len(c), ng, md)
+                assert len(want) > 0
+
+
+@pytest.mark.gpu
 def test_draft_rejects_bad_arguments(sampler):
     from locus_amd.sampler import SamplerError
     with pytest.raises(SamplerError):
