@@ -1039,10 +1039,27 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
         }
         return x;
     };
+    {
+        // the first kNucKeyCache keys into LDS, every load issued before the
+        // first is used (indices past n read entry 0 of the row's list, unused)
+        static_assert(kNucKeyCache % NT == 0, "key cache per thread");
+        constexpr uint32_t KP = kNucKeyCache / NT;
+        uint64_t kq[KP];
+#pragma unroll
+        for (uint32_t j = 0; j < KP; ++j) {
+            const uint32_t i = tid + j * NT;
+            kq[j] = list[i < n ? i : 0u];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < KP; ++j) {
+            const uint32_t i = tid + j * NT;
+            if (i < n) sm.u.fc.lkey[i] = kq[j];
+        }
+    }
+    __syncthreads();
     for (uint32_t i = tid; i < n; i += NT) {
         uint32_t k, s;
-        const uint64_t key = list[i];
-        if (i < kNucKeyCache) sm.u.fc.lkey[i] = key;
+        const uint64_t key = i < kNucKeyCache ? sm.u.fc.lkey[i] : list[i];
         const float x = locate(key, k, s);
         g_code[i] = k < kNucRanges ? (uint16_t)(k * kNucSub + s) : kNoCode;
         if (k < kNucRanges) {
