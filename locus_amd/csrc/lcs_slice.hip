@@ -862,7 +862,7 @@ struct FinSmem {
             uint64_t sorted[kRowWin];
             float sortedraw[kRowWin];
             double sw[kRowWin];
-            uint64_t tkey[kSsTopKMerge];   // top-k rows: each slice's list, rank order
+            uint64_t tkey[kSsTopKMerge];   // top-k rows past kRowWin candidates: the slices' lists, kTopKMax apart
             float traw[kSsTopKMerge];
         } f;
         ExactSmem<kFinThreads, kFbBins, kFbCap, kFbHistCap> ex;
