@@ -286,21 +286,9 @@ __device__ __forceinline__ uint32_t wave_scan_incl_u(uint32_t v) {
     return v;
 }
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
-// The n-th largest of the wave's 4 x 64 keys k[c] (1 <= n <= 256): the
-// largest T with at least n keys >= T, built bit by bit from the top with
-// ballot counts. Wave-uniform result.
-__device__ __forceinline__ uint32_t wave_kth_largest4(const uint32_t (&k)[4], uint32_t n) {
-    uint32_t T = 0;
-    for (int b = 31; b >= 0; --b) {
-        const uint32_t Tb = T | (1u << b);
-        uint32_t cnt = 0;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) cnt += (uint32_t)__builtin_popcountll(__ballot(k[c] >= Tb));
-        if (cnt >= n) T = Tb;
-    }
-    return T;
-}
-// As wave_kth_largest4, over keys below 2^16 (16 steps).
+// The n-th largest of the wave's 4 x 64 keys k[c] below 2^16 (1 <= n <= 256):
+// the largest T with at least n keys >= T, built bit by bit from the top
+// with ballot counts (16 steps). Wave-uniform result.
 __device__ __forceinline__ uint32_t wave_kth_largest4_16(const uint32_t (&k)[4], uint32_t n) {
     uint32_t T = 0;
     for (int b = 15; b >= 0; --b) {

@@ -424,7 +424,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     sm.l.lmax[tid] = lm;
     if (in.hany) in.count_gather(sm);
     __syncthreads();
-    // raw slice max; one wave finds the ntop-th largest lane maximum
+    // raw slice max; one wave finds a lower bound of the ntop-th largest lane
+    // maximum (the slice max itself for ntop = 1; else a 16-step select on
+    // keys cut to 16 bits): every element of the slice's top-n is >= it
     float Ms;
     {
         float m4[kNW];
@@ -432,10 +434,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         for (int c = 0; c < kNW; ++c) m4[c] = sm.l.lmax[lane + c * kWave];
         Ms = wave_max(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])));
         if (ntop && wv == kNW - 1) {
-            uint32_t k4[kNW];
+            float t = Ms;
+            if (ntop > 1u) {
+                uint32_t k4[kNW];
 #pragma unroll
-            for (int c = 0; c < kNW; ++c) k4[c] = fkey(m4[c]);
-            const float t = key_to_f(wave_kth_largest4(k4, ntop));
+                for (int c = 0; c < kNW; ++c) k4[c] = fkey(m4[c]) >> 16;
+                t = key_to_f(max(wave_kth_largest4_16(k4, ntop) << 16, 0x007fffffu));
+            }
             if (lane == 0) sm.l.t_s = t;
         }
     }
