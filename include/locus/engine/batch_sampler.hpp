@@ -38,6 +38,8 @@
 #include <memory>
 #include <random>
 #include <span>
+#include <stdexcept>
+#include <string>
 #include <type_traits>
 #include <vector>
 
@@ -45,6 +47,23 @@
 #include "locus_sampler.h"
 
 namespace locus::engine {
+
+namespace detail {
+/** Throws std::runtime_error for the first row whose id is -1: a row the
+ * device could not serve. Every device status bit comes with id -1 on the
+ * affected rows (locus_sampler.h), so `status` (which reads and resets the
+ * context's status word) is called only then. */
+template <class StatusFn>
+void check_served(const std::int32_t* ids, std::uint32_t rows, StatusFn&& status) {
+    for (std::uint32_t r = 0; r < rows; ++r) {
+        if (ids[r] < 0) {
+            const std::uint32_t st = status();
+            throw std::runtime_error("BatchSampler: row " + std::to_string(r) + " not sampled (device status " +
+                                     std::to_string(st) + ")");
+        }
+    }
+}
+}  // namespace detail
 
 /** What sample_from reads from one request (borrowed for one step). */
 struct SampleRow {
@@ -74,7 +93,10 @@ class BatchSampler {
      * requests are updated in row order and the sampled ids returned.
      * Every row's limits are checked before any rng is advanced: on
      * std::invalid_argument (sizes beyond the constructor's limits) no
-     * request has changed. std::runtime_error on device errors.
+     * request has changed. std::runtime_error on device errors, including a
+     * row the device could not serve (id -1): then no request has been
+     * updated either, except that the stochastic rows' rngs have advanced
+     * (their uniforms were drawn for the launch).
      */
     template <class Request>
     std::vector<tok::TokenId> sample_step(const void* logits, lcs_dtype dtype, std::uint32_t row_stride,

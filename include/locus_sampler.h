@@ -196,8 +196,8 @@ int lcs_sample(lcs_ctx* ctx, const lcs_batch* batch, const lcs_out* out, void* s
  * call hipMalloc (code under HIP graph capture, tight serving loops, harnesses
  * that forbid it). No counterpart in the reference. Runs on the current
  * device with the same batch, outputs and results as lcs_sample; its
- * workspace is one static device array per GPU (about 20 MiB, held until the
- * process ends), sized for rows <= 32, any vocabulary up to 262144, n_top <=
+ * workspace is one static device array per GPU (about 39 MiB, held until the
+ * process ends), sized for rows <= 64, any vocabulary up to 262144, n_top <=
  * 20 and penalty windows up to 8192. More rows return LCS_ERR_CAPACITY with
  * nothing launched. Calls share that array: calls that overlap on one GPU
  * (two streams, or two threads) race and must be serialised by the caller.
@@ -212,7 +212,8 @@ int lcs_verify(lcs_ctx* ctx, const lcs_verify_batch* batch, const lcs_verify_out
 
 /* Batched n-gram drafts: replaces the per-sequence host call of
  * engine.cpp:328-329 (speculative.cpp:7-28) when contexts live on the device.
- * Drafts feed lcs_verify. Allocates nothing. */
+ * Drafts feed lcs_verify. Allocates nothing and uses no context workspace, so
+ * n_seq is not bounded by the context's max_rows. */
 int lcs_ngram_draft(lcs_ctx* ctx, const lcs_draft_batch* batch, const lcs_draft_out* out, void* stream);
 
 /* The fused lm-head product (see lcs_lmhead_batch); no counterpart call in
@@ -221,7 +222,9 @@ int lcs_ngram_draft(lcs_ctx* ctx, const lcs_draft_batch* batch, const lcs_draft_
 int lcs_lmhead(lcs_ctx* ctx, const lcs_lmhead_batch* batch, const lcs_lmhead_out* out, void* stream);
 
 /* Sticky device-side status bits of ctx (LCS_STATUS_*), set by kernels that
- * met an input they could not serve (the affected rows get id -1). Blocking:
+ * met an input they could not serve. Every bit comes with id -1 on each
+ * affected row (also from lcs_sample_noalloc, whose status is not readable),
+ * so a caller that sees no -1 id needs no status read. Blocking:
  * reads device memory; call after the work's stream has been synchronised.
  * No counterpart in the reference (its sampler cannot fail). */
 int lcs_get_status(lcs_ctx* ctx, uint32_t* status_out, int reset);

@@ -4,6 +4,7 @@
 // workspace is a static device array, see below).
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -304,7 +305,7 @@ int sample_impl(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream, 
 // and the general path's largest penalty window. Host code never uses the
 // array's name as an address: the per-device address comes from
 // hipGetSymbolAddress on the first call on that device.
-constexpr uint32_t kNoAllocRows = 32;
+constexpr uint32_t kNoAllocRows = 64;   // the headline C2 batch in one call
 constexpr uint32_t kNoAllocHist = lcs::kGenHistCap;
 constexpr size_t kAlign = 256;
 constexpr size_t up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
@@ -327,12 +328,15 @@ constexpr size_t kOffNrow = kOffDPen + kSzD;
 constexpr size_t kOffNhCnt = kOffNrow + kSzNrow;
 constexpr size_t kOffNhMass = kOffNhCnt + kSzNhCnt;
 constexpr size_t kOffNlist = kOffNhMass + kSzNhMass;
-constexpr size_t kScratchBytes = kOffNlist + kSzNlist;   // about 20 MiB
-static_assert(kScratchBytes <= (24u << 20), "the no-alloc workspace stays modest");
+constexpr size_t kScratchBytes = kOffNlist + kSzNlist;   // about 39 MiB
+static_assert(kScratchBytes <= (40u << 20), "the no-alloc workspace stays modest");
 
 constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-unsigned char* g_scratch_ptr[kMaxDevices] = {};   // per device: the address of `scratch`
+std::mutex g_scratch_mu;   // serialises the first call on a device
+// Per device: the address of `scratch`, published once that device has been
+// checked to be a gfx950 and the address looked up; after that a call reads
+// it with one atomic load and takes no lock.
+std::atomic<unsigned char*> g_scratch_ptr[kMaxDevices] = {};
 
 }  // namespace
 
@@ -346,25 +350,31 @@ int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
 }
 
 int lcs_sample_noalloc(const lcs_batch* b, const lcs_out* o, void* stream) {
-    g_create_error.clear();
+    if (!g_create_error.empty()) g_create_error.clear();
     int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices || !is_gfx950(dev)) {
-        g_create_error = "lcs_sample_noalloc: the current device is not a usable gfx950";
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        g_create_error = "lcs_sample_noalloc: no current device";
         return LCS_ERR_NO_DEVICE;
     }
-    unsigned char* base = nullptr;
-    {
+    unsigned char* base = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!base) {
+        // first call on this device: check it and look the array up, once
         std::lock_guard<std::mutex> lk(g_scratch_mu);
-        if (!g_scratch_ptr[dev]) {
+        base = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!base) {
+            if (!is_gfx950(dev)) {
+                g_create_error = "lcs_sample_noalloc: the current device is not a usable gfx950";
+                return LCS_ERR_NO_DEVICE;
+            }
             void* p = nullptr;
             const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
             if (e != hipSuccess || !p) {
                 g_create_error = std::string("lcs_sample_noalloc: hipGetSymbolAddress: ") + hipGetErrorString(e);
                 return LCS_ERR_HIP;
             }
-            g_scratch_ptr[dev] = static_cast<unsigned char*>(p);
+            base = static_cast<unsigned char*>(p);
+            g_scratch_ptr[dev].store(base, std::memory_order_release);
         }
-        base = g_scratch_ptr[dev];
     }
     // a context view of the static workspace: nothing here allocates device
     // memory (the string stays empty unless a call fails)
@@ -436,7 +446,7 @@ int lcs_ngram_draft(lcs_ctx* c, const lcs_draft_batch* b, const lcs_draft_out* o
     if (b->ngram > lcs::kDraftMaxNgram || b->max_draft > lcs::kDraftMaxLen) {
         return fail(c, LCS_ERR_INVALID_ARG, "ngram must be <= 64 and max_draft <= 256");
     }
-    if (b->n_seq > c->max_rows) return fail(c, LCS_ERR_CAPACITY, "n_seq above max_rows");
+    // (no limit on n_seq: one workgroup per sequence, and no context workspace)
     lcs::DraftArgs a{};
     a.n_seq = b->n_seq;
     a.ngram = b->ngram;

@@ -118,6 +118,7 @@ struct ExactSmem {
     uint32_t nlist;
     uint32_t mp_count;
     uint32_t flag;
+    uint32_t bincap;   // thread 0: a selection bin overflowed, so the row's id is -1
     int32_t out_id;
     uint32_t out_keep;
     float out_boundary;
@@ -194,6 +195,8 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
     uint32_t* d_ids = a.d_ids + (uint64_t)row * a.max_hist;
     float* d_raw = a.d_raw + (uint64_t)row * a.max_hist;
     float* d_pen = a.d_pen + (uint64_t)row * a.max_hist;
+
+    if (tid == 0) sm.bincap = 0u;   // (thread 0 alone writes and reads it)
 
     // ---- P0: distinct penalised ids of the window (apply_penalties) ----
     uint32_t nD = 0;
@@ -609,7 +612,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
             uint32_t off = 0;
             for (int s = 0; s < na; ++s) { all[s].off = off; off += all[s].cnt; segs[s] = all[s]; }
             nseg = na;
-            if (sm.nlist > CAP && tid == 0) atomicOr(a.status, kStatusBinCap);
+            if (sm.nlist > CAP && tid == 0) { atomicOr(a.status, kStatusBinCap); sm.bincap = 1u; }
         };
         // Narrows one bin holding > CAP candidates to a rank-key interval
         // containing candidate position `pos` (by_count) or the crossing of
@@ -807,7 +810,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
                     }
                     if (kp == 0) {
                         kp = end;
-                        if (end < kk) atomicOr(a.status, kStatusBinCap);
+                        if (end < kk) { atomicOr(a.status, kStatusBinCap); sm.bincap = 1u; }
                     }
                     sm.out_keep = kp;
                 }
@@ -861,7 +864,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
                     if (r <= 0.0) { id = (int32_t)rank_idx(k); break; }
                 }
                 if (id < 0) {
-                    if (end < keep) atomicOr(a.status, kStatusBinCap);
+                    if (end < keep) { atomicOr(a.status, kStatusBinCap); sm.bincap = 1u; }
                     id = (int32_t)rank_idx(list_at(keep - 1));  // reference fallback (last survivor)
                 }
                 const uint64_t kb = list_at(keep - 1);
@@ -873,7 +876,9 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
             boundary = sm.out_boundary;
         }
         if (tid == 0) {
-            a.ids[row] = chosen;
+            // a row whose selection overflowed a bin reports -1 (with the
+            // status bit), like a row whose penalty window overflowed
+            a.ids[row] = sm.bincap ? -1 : chosen;
             if (want_lp) {
                 const int32_t lid = a.lp_ids ? a.lp_ids[row] : chosen;
                 const bool inr = lid >= 0 && (uint32_t)lid < V;

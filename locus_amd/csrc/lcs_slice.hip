@@ -869,13 +869,21 @@ struct FinSmem {
     } u;
     double log_z, fin_S, fin_rel, fin_invS;
     float chosen_raw, fin_maxl;
-    uint32_t fin_fb, fin_L0;
+    uint32_t fin_fb[4];      // per wave: the records cannot settle the row (exact path)
+    uint32_t fin_fb_decide;  // wave 0's decision could not be certified (exact path)
+    uint32_t fin_L0;
     uint32_t tk_ns[kSsMaxSlices];                    // top-k rows: entries of each slice's list,
     uint32_t tk_cs[kSsMaxSlices], tk_base[kSsMaxSlices];   // its candidates (keys <= U), their offset
     uint64_t tk_u[4];                                // top-k rows: each wave's bound
     uint32_t tn_ns[kSsMaxSlices];                    // top-n list lengths (logprobs)
     SampleArgs args;   // the kernel arguments (exact_row reads them from here)
 };
+
+// Whether a wave flagged the row for the exact path (read after a barrier
+// that follows every wave's write of its flag).
+__device__ __forceinline__ bool fin_any_fb(const FinSmem& sm) {
+    return (sm.fin_fb[0] | sm.fin_fb[1] | sm.fin_fb[2] | sm.fin_fb[3]) != 0u;
+}
 
 constexpr uint32_t kSpecWin = 8;    // window entries fetched per slice per round
 
@@ -1002,6 +1010,7 @@ __device__ __forceinline__ void fin_window_rank(FinSmem& sm, uint32_t L0, float 
     uint64_t k[4];
     uint32_t rk[4];
     lds_rank4(sm.u.f.ent, L0, k, rk);
+    PROF_AT(kProfFin + wg_x(), 27);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
@@ -1012,6 +1021,10 @@ __device__ __forceinline__ void fin_window_rank(FinSmem& sm, uint32_t L0, float 
         }
     }
     if (lane == 0) { sm.fin_L0 = L0; sm.fin_maxl = maxl; }
+#ifdef LCS_PROFILE
+    wait_all_memory();
+#endif
+    PROF_AT(kProfFin + wg_x(), 28);
 }
 
 // Window rows: every entry with p >= maxl - delta, gathered from the slices'
@@ -1036,15 +1049,26 @@ __device__ __forceinline__ bool fin_window(const uint64_t (&hd)[rec::kHdr], cons
     const double thr = (double)maxl - delta;
     float thr_up = (float)thr;
     if ((double)thr_up < thr) thr_up = next_up(thr_up);
+    PROF_AT(kProfFin + wg_x(), 24);
     // a slice that could hold row-window entries must not have lost any
     if (ballot(mine && (flags & rec::kFlagWinLost) && m_pen >= thr_up)) return true;
-    // entries are in ascending rank order, so the qualifying ones lead
+    // entries are in ascending rank order, so the qualifying ones lead; an
+    // entry qualifies when its value is >= thr_up, i.e. its rank key's value
+    // half is <= that of thr_up. Offsets by ballots: lane s's entries go
+    // after those of the lanes below it (no dependent cross-lane steps)
+    const uint32_t kthr = ~fkey(thr_up);
     uint32_t q = 0;
 #pragma unroll
-    for (int j = 0; j < (int)kSpecWin; ++j) q += ((uint32_t)j < n_win && rank_val(wk[j]) >= thr_up) ? 1u : 0u;
-    const uint32_t base = wave_scan_incl_u(q) - q;
-    uint32_t L0 = wave_sum_u(q);
+    for (int j = 0; j < (int)kSpecWin; ++j) q += ((uint32_t)j < n_win && (uint32_t)(wk[j] >> 32) <= kthr) ? 1u : 0u;
+    uint32_t base = 0, L0 = 0;
+#pragma unroll
+    for (int j = 0; j < (int)kSpecWin; ++j) {
+        const uint64_t m = ballot(q > (uint32_t)j);
+        base += __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        L0 += (uint32_t)__builtin_popcountll(m);
+    }
     if (L0 > kRowWin) return true;
+    PROF_AT(kProfFin + wg_x(), 25);
 #pragma unroll
     for (int j = 0; j < (int)kSpecWin; ++j) {
         if ((uint32_t)j < q) {
@@ -1083,6 +1107,7 @@ __device__ __forceinline__ bool fin_window(const uint64_t (&hd)[rec::kHdr], cons
     }
     // a truncated slice whose every kept entry qualifies may hold more
     if (ballot(mine && (flags & rec::kFlagWinTrunc) && qtot == n_win)) return true;
+    PROF_AT(kProfFin + wg_x(), 26);
     fin_window_rank(sm, L0, maxl, inv_t);
     return false;
 }
@@ -1123,8 +1148,9 @@ __device__ __forceinline__ void fin_load_topk(const uint64_t* recs, uint32_t S, 
 //      LDS, kTopKMax apart): branch-free lower bounds, 7 halving steps over 16
 //      lists at a time in lockstep (loads always in bounds). Rank keys are
 //      unique, so ranks below Ke are distinct.
-// The row's exact-path flag sm.fin_fb, set before the call, is read after the
-// first barrier; the function returns early (uniformly) when it is set.
+// The waves' exact-path flags sm.fin_fb, each written by its wave before the
+// call, are read after the first barrier; the function returns early
+// (uniformly) when one is set.
 __device__ __forceinline__ void fin_merge_topk(uint64_t h0, const uint64_t (&kk)[kTkPer], const float (&rr)[kTkPer],
                                                uint32_t S, uint32_t K, FinSmem& sm, float inv_t) {
     const uint32_t tid = tid_x();
@@ -1151,7 +1177,7 @@ __device__ __forceinline__ void fin_merge_topk(uint64_t h0, const uint64_t (&kk)
     um = wave_max_u64(um);
     if (lane == 0) sm.tk_u[wv] = um;
     __syncthreads();
-    if (sm.fin_fb) return;
+    if (fin_any_fb(sm)) return;
     uint64_t U = sm.tk_u[0];
 #pragma unroll
     for (int w = 1; w < 4; ++w) U = sm.tk_u[w] > U ? sm.tk_u[w] : U;
@@ -1327,6 +1353,7 @@ __device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, Fi
         Wc = bits_d(readlane_u64(d_bits(W), kWave - 1));
     }
     if (P.top_p < 1.0f && keep_p == 0xffffffffu && tp - Wc * inv_S <= rel * Wc * inv_S + 1e-13) uncertain = true;
+    PROF_AT(kProfFin + wg_x(), 29);
     if (uncertain) return true;
     if (keep < 1) keep = 1;
     if (pos == 0xffffffffu) {
@@ -1348,6 +1375,7 @@ __device__ __forceinline__ bool fin_decide(const SampleArgs& a, uint32_t row, Fi
         }
         if (pos == 0xffffffffu) pos = keep - 1;  // reference fallback: cand[keep-1]
     }
+    PROF_AT(kProfFin + wg_x(), 30);
     if (lane == 0) {
         const uint64_t ck = sm.u.f.sorted[pos];
         a.ids[row] = (int32_t)rank_idx(ck);
@@ -1424,16 +1452,16 @@ __global__ __launch_bounds__(kFinThreads) void row_fin(const lcs_params* params,
     const bool stoch = mode == kModeWindow, topk = mode == kModeTopK;
     const float inv_t = stoch || topk ? fdiv(1.0f, P.temperature) : 1.0f;
     const double u = (stoch || topk) && wv == 0 ? a.u[row] : 0.0;
-    if (tid == 0) sm.fin_fb = 0u;
-    __syncthreads();
     PROF_AT(kProfFin + row, 4 + wv);
+    // each wave reports its exact-path flag in its own word before the next
+    // barrier, so no barrier is needed to clear a shared one first
     bool fb = false;
     if (topk) {
         if (!TK) fin_load_topk(recs, S, wv, tkk, tkr);
         if (wv == 1 && want_lp) fb = fin_logz(hd, tk, S, ntop, sm);
         // a slice that could not rank its list sends the row to the exact path
         if (wv == 0) fb = ballot((uint32_t)lane < S && ((uint32_t)(hd[0] >> 48) & rec::kFlagWinLost)) != 0;
-        if (fb && lane == 0) sm.fin_fb = 1u;
+        if (lane == 0) sm.fin_fb[wv] = fb ? 1u : 0u;
         fin_merge_topk(hd[0], tkk, tkr, S, P.top_k, sm, inv_t);
     } else if (wv == 0) {
         if (stoch && TK) load_window();
@@ -1445,10 +1473,10 @@ __global__ __launch_bounds__(kFinThreads) void row_fin(const lcs_params* params,
         if (stoch) fin_norm(hd, S, sm, inv_t);
     }
     PROF_AT(kProfFin + row, 8 + wv);
-    if (fb && lane == 0) sm.fin_fb = 1u;
+    if (lane == 0) sm.fin_fb[wv] = fb ? 1u : 0u;
     __syncthreads();
     PROF_AT(kProfFin + row, 12 + wv);
-    if (!sm.fin_fb) {
+    if (!fin_any_fb(sm)) {
         // logprob of the chosen token, or of the caller's lp_ids token (thread
         // 0, once the row's choice and log-normaliser are in)
         auto write_lp = [&]() {
@@ -1471,7 +1499,7 @@ __global__ __launch_bounds__(kFinThreads) void row_fin(const lcs_params* params,
         }
         if (wv == 0) {
             fb = fin_decide(a, row, sm, topk ? LCS_PATH_TOPK : LCS_PATH_WINDOW, P, u);
-            if (fb && lane == 0) sm.fin_fb = 1u;
+            if (lane == 0) sm.fin_fb_decide = fb ? 1u : 0u;
             if (!fb && tid == 0 && want_lp) write_lp();
 #ifdef LCS_PROFILE
             wait_all_memory();
@@ -1479,7 +1507,7 @@ __global__ __launch_bounds__(kFinThreads) void row_fin(const lcs_params* params,
 #endif
         }
         __syncthreads();
-        if (!sm.fin_fb) return;
+        if (!sm.fin_fb_decide) return;
     }
     // the records cannot settle this row: the exact single-workgroup path
     // (out of line: it reads the kernel arguments from an LDS copy)

@@ -233,14 +233,11 @@ void BatchSampler::run(const void* logits, lcs_dtype dtype, std::uint32_t row_st
     check(hipStreamSynchronize(st), "hipStreamSynchronize");
     // A row the kernels could not serve comes back as id -1 (locus_sampler.h),
     // so the status word is read only then.
-    for (std::uint32_t r = 0; r < rows; ++r) {
-        if (b.ids_h[r] < 0) {
-            std::uint32_t status = 0;
-            (void)lcs_get_status(b.ctx, &status, 1);
-            throw std::runtime_error("BatchSampler: row " + std::to_string(r) + " not sampled (device status " +
-                                     std::to_string(status) + ")");
-        }
-    }
+    detail::check_served(b.ids_h, rows, [&] {
+        std::uint32_t status = 0;
+        (void)lcs_get_status(b.ctx, &status, 1);
+        return status;
+    });
     b.rows = rows;
     b.n_top = n_top;
 }

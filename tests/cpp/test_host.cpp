@@ -508,6 +508,26 @@ static void test_batch_gpu() {
     CHECK(lim[0].generated.empty() && lim[1].generated.empty());
 }
 
+// A row the device could not serve (id -1, locus_sampler.h) fails the step;
+// the status word is read only then.
+static void test_unserved_rows() {
+    int reads = 0;
+    auto status = [&] { ++reads; return 2u; };
+    const std::int32_t ok[3] = {5, 0, 7};
+    locus::engine::detail::check_served(ok, 3, status);
+    CHECK(reads == 0);
+    const std::int32_t bad[3] = {5, -1, 7};
+    bool thrown = false;
+    try {
+        locus::engine::detail::check_served(bad, 3, status);
+    } catch (const std::runtime_error& e) {
+        thrown = std::string(e.what()).find("row 1") != std::string::npos &&
+                 std::string(e.what()).find("status 2") != std::string::npos;
+    }
+    CHECK(thrown);
+    CHECK(reads == 1);
+}
+
 int main(int argc, char** argv) {
     const std::string mode = argc > 1 ? argv[1] : "cpu";
     try {
@@ -516,6 +536,7 @@ int main(int argc, char** argv) {
             test_mask_builder();
             test_ngram();
             test_registry(false);
+            test_unserved_rows();
         } else if (mode == "gpu") {
             test_registry(true);
             test_sampling_gpu();

@@ -12,7 +12,7 @@ import pytest
 
 from locus_amd import workloads as W
 from oracle import pyoracle as O
-from tests.util import LOGPROB_TOL, excluded_rows, load
+from tests.util import LOGPROB_TOL, excluded_rows, load, near_tie_rows, penalized_value
 
 pytestmark = pytest.mark.gpu
 
@@ -52,6 +52,19 @@ def compare(w, g, o, label, expect_paths=None):
     kb = np.nonzero(stoch & (g["diag"]["keep"] != o.diag["keep"]))[0]
     assert len(kb) == 0, f"{label}: survivor counts differ at rows {kb[:10].tolist()} " \
                          f"gpu {g['diag']['keep'][kb[:10]].tolist()} oracle {o.diag['keep'][kb[:10]].tolist()}"
+    # exact-tie rows (not near ties): the order among equal logits cannot
+    # change the survivor count, the kept mass (equal weights give equal f64
+    # sums in any order) or the drawn position, so only which of several
+    # equal-logit ids is drawn may differ: its penalised logit must be the
+    # reference's id's
+    tie = (o.diag["tie_flags"] != 0) & ~near_tie_rows(o.diag) & ~greedy
+    for r in np.nonzero(tie)[0]:
+        assert g["diag"]["keep"][r] == o.diag["keep"][r], \
+            f"{label} tie row {r}: keep {g['diag']['keep'][r]} vs {o.diag['keep'][r]}"
+        ks, oks = float(g["diag"]["kept_sum"][r]), float(o.diag["kept_sum"][r])
+        assert abs(ks - oks) <= 1e-12 * oks, f"{label} tie row {r}: kept_sum {ks!r} vs {oks!r}"
+        gv, ov = penalized_value(w, r, int(g["ids"][r])), penalized_value(w, r, int(o.ids[r]))
+        assert gv == ov, f"{label} tie row {r}: drew {g['ids'][r]} ({gv!r}), reference {o.ids[r]} ({ov!r})"
     if w.want_logprobs:
         same = g["ids"] == o.ids
         err = np.abs(g["chosen_lp"] - o.chosen_lp)[same]
@@ -65,8 +78,8 @@ def compare(w, g, o, label, expect_paths=None):
     if expect_paths is not None:
         assert set(np.unique(g["diag"]["path"]).tolist()) <= set(expect_paths), \
             f"{label}: paths {np.unique(g['diag']['path']).tolist()}"
-    say(label, "rows", w.rows, "excluded", int(excl.sum()), "paths",
-        np.unique(g["diag"]["path"]).tolist())
+    say(label, "rows", w.rows, "excluded", int(excl.sum()), "of which exact ties checked", int(tie.sum()),
+        "paths", np.unique(g["diag"]["path"]).tolist())
     return excl
 
 
