@@ -85,6 +85,18 @@ typedef struct lcs_batch {
                                   reports the logprob of lp_ids[row] instead of the
                                   sampled id (logprobs_from's `chosen` argument,
                                   sampling.hpp:86-89); ids outside [0, V) give 0 */
+    /* Device-resident penalty windows (lcs_windows_reserve). NULL: every row's
+     * window comes from hist_off / hist_ids. Otherwise every row must be a
+     * min-p window row (temperature > 0, min_p > 0, top_k 0, no mask; checked
+     * against params_host, which is then required): */
+    const int32_t* win_slot;   /* rows: the row's window slot, or -1 (hist_off / hist_ids) */
+    const int32_t* win_push;   /* rows: the id the sequence appended since the slot's last
+                                  call (its previous sample, engine.cpp:436), read when
+                                  win_len grows by one */
+    const uint32_t* win_len;   /* rows: the history length after that append: the slot's
+                                  stored length (nothing appended) or one more; the slot's
+                                  window, vocabulary and repeat_last_n must match the row,
+                                  else the row gets id -1 and LCS_STATUS_WINDOW */
 } lcs_batch;
 
 /* Per-row diagnostics (optional output): the survivor set of the reference's
@@ -188,6 +200,23 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab,
                     uint32_t max_hist, uint32_t max_top);
 void lcs_destroy(lcs_ctx* ctx);
 
+/* Device-resident penalty windows: the counts apply_penalties builds from
+ * the history's last repeat_last_n ids (sampling.cpp:22-28) kept per
+ * sequence slot on the device and updated in place by each lcs_sample call
+ * that names the slot (one id enters the window, at most one leaves), so a
+ * serving loop uploads no history. Allocates room for `slots` slots of
+ * windows up to `max_window` ids (<= 4096), once (call it before the hot
+ * loop; calling again with larger limits reallocates and clears every slot).
+ * No counterpart in the reference, which rescans the history per call. */
+int lcs_windows_reserve(lcs_ctx* ctx, uint32_t slots, uint32_t max_window);
+
+/* (Re)starts slot `slot` for a sequence whose generated history so far is
+ * ids[0..n) (device memory; n may be 0, ids may then be NULL), penalised
+ * over its last `window` ids (1..max_window: the rows' repeat_last_n) for
+ * a vocabulary of `vocab` ids. Asynchronous on `stream`. */
+int lcs_windows_load(lcs_ctx* ctx, uint32_t slot, const int32_t* ids, uint32_t n, uint32_t window,
+                     uint32_t vocab, void* stream);
+
 /* Batched sample (+ logprobs): replaces per-row sample()/logprobs_from()
  * (sampling.hpp:70-89) as called from engine.cpp:430-442. */
 int lcs_sample(lcs_ctx* ctx, const lcs_batch* batch, const lcs_out* out, void* stream);
@@ -231,7 +260,9 @@ int lcs_get_status(lcs_ctx* ctx, uint32_t* status_out, int reset);
 
 enum lcs_status_bits {
     LCS_STATUS_HIST_CAPACITY = 1u,  /* a penalty window exceeded max_hist */
-    LCS_STATUS_SELECT = 2u          /* a selection bin exceeded its capacity */
+    LCS_STATUS_SELECT = 2u,         /* a selection bin exceeded its capacity */
+    LCS_STATUS_WINDOW = 4u          /* a row's window slot did not match it (win_len, window,
+                                       vocabulary) */
 };
 
 /* Message of the last failure on ctx (or, when NULL, of the last lcs_create

@@ -34,7 +34,7 @@ HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
              "-fno-honor-nans", "-mno-amdgpu-ieee",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I" + INCLUDE]
-HIP_SOURCES = ["lcs_api.hip", "lcs_sample.hip", "lcs_slice.hip", "lcs_nucleus.hip", "lcs_verify.hip", "lcs_draft.hip",
+HIP_SOURCES = ["lcs_api.hip", "lcs_sample.hip", "lcs_slice.hip", "lcs_windows.hip", "lcs_nucleus.hip", "lcs_verify.hip", "lcs_draft.hip",
                "lcs_lmhead.hip"]
 # the leading scalar arguments (8) of slice_stats and the nucleus kernels
 # arrive preloaded in SGPRs; the code object keeps a prologue that loads them

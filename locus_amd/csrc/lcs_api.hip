@@ -16,6 +16,8 @@
 
 namespace lcs {
 hipError_t launch_slice(const SampleArgs& a, hipStream_t st);
+hipError_t launch_win_load(WinHdr* wh, int32_t* wring, uint64_t* wbkt, uint32_t H, uint32_t slot, const int32_t* ids,
+                           uint32_t n, uint32_t W, uint32_t V, uint32_t slen, hipStream_t st);
 hipError_t launch_general(const SampleArgs& a, hipStream_t st);
 hipError_t launch_nucleus(const SampleArgs& a, hipStream_t st);
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t st);
@@ -41,6 +43,12 @@ struct lcs_ctx {
     uint32_t* nh_cnt = nullptr;
     double* nh_mass = nullptr;
     uint64_t* nlist = nullptr;
+    // device-resident penalty windows (lcs_windows_reserve)
+    uint32_t win_slots = 0, win_max = 0, win_h = 0;
+    lcs::WinHdr* wh = nullptr;
+    lcs::WinStage* wstage = nullptr;   // max_rows
+    int32_t* wring = nullptr;
+    uint64_t* wbkt = nullptr;
     std::string err;
 };
 
@@ -127,7 +135,7 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t 
     c->max_top = max_top;
     c->max_slices = slices_for(max_vocab, lcs::kSliceMax);
     const size_t rec_bytes = (size_t)max_rows * c->max_slices * lcs::rec::kWords * 4;
-    const size_t srec_bytes = (size_t)max_rows * lcs::kSsMaxSlices * lcs::rec::kWords64 * 8;
+    const size_t srec_bytes = (size_t)max_rows * lcs::kRecsPerRow * lcs::rec::kWords64 * 8;
     const size_t d_elems = (size_t)max_rows * c->max_hist;
     const size_t nuc_rows = max_rows < lcs::kNucRows ? max_rows : lcs::kNucRows;
     const size_t nh_elems = nuc_rows * lcs::kMaxSlices * lcs::kNucBins;
@@ -168,6 +176,10 @@ void lcs_destroy(lcs_ctx* c) {
     (void)hipFree(c->d_pen);
     (void)hipFree(c->status);
     (void)hipFree(c->lmrecs);
+    (void)hipFree(c->wh);
+    (void)hipFree(c->wring);
+    (void)hipFree(c->wbkt);
+    (void)hipFree(c->wstage);
     delete c;
 }
 
@@ -210,6 +222,21 @@ int sample_impl(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream, 
     if (b->hist_off && !b->hist_ids) return fail(c, LCS_ERR_INVALID_ARG, "hist_ids missing");
     if ((b->flags & LCS_WRITE_PENALIZED) && b->dtype != LCS_F32) {
         return fail(c, LCS_ERR_INVALID_ARG, "LCS_WRITE_PENALIZED needs f32 logits");
+    }
+    // device-resident windows serve batches of min-p window rows (the sliced
+    // path); the host's copy of the params shows that every row is one
+    if (b->win_slot) {
+        if (!b->win_push || !b->win_len) return fail(c, LCS_ERR_INVALID_ARG, "win_slot needs win_push and win_len");
+        if (!c->wh) return fail(c, LCS_ERR_INVALID_ARG, "win_slot without lcs_windows_reserve");
+        if (!b->params_host || b->mask || (b->flags & LCS_WRITE_PENALIZED)) {
+            return fail(c, LCS_ERR_INVALID_ARG, "win_slot needs params_host, no mask and no LCS_WRITE_PENALIZED");
+        }
+        for (uint32_t r = 0; r < b->rows; ++r) {
+            if (lcs::row_mode(b->params_host[r], false, b->vocab) != lcs::kModeWindow) {
+                return fail(c, LCS_ERR_INVALID_ARG, "win_slot: every row must be a min-p window row (temperature > 0, "
+                                                    "min_p > 0, top_k 0)");
+            }
+        }
     }
     // Stochastic rows read u[row] on the device. With a host copy of the
     // params only those rows need it; without one the row modes are unknown
@@ -285,6 +312,14 @@ int sample_impl(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream, 
     a.nh_cnt = c->nh_cnt;
     a.nh_mass = c->nh_mass;
     a.nlist = c->nlist;
+    a.win_slot = b->win_slot;
+    a.win_push = b->win_push;
+    a.win_len = b->win_len;
+    a.wh = c->wh;
+    a.wring = c->wring;
+    a.wbkt = c->wbkt;
+    a.wring_h = c->win_h;
+    a.wstage = c->wstage;
 
     DeviceGuard g(c->device);
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -310,7 +345,7 @@ constexpr uint32_t kNoAllocHist = lcs::kGenHistCap;
 constexpr size_t kAlign = 256;
 constexpr size_t up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
 constexpr size_t kSzRecs = up((size_t)kNoAllocRows * lcs::kMaxSlices * lcs::rec::kWords * 4);
-constexpr size_t kSzSrecs = up((size_t)kNoAllocRows * lcs::kSsMaxSlices * lcs::rec::kWords64 * 8);
+constexpr size_t kSzSrecs = up((size_t)kNoAllocRows * lcs::kRecsPerRow * lcs::rec::kWords64 * 8);
 constexpr size_t kSzStatus = up(4);
 constexpr size_t kSzD = up((size_t)kNoAllocRows * kNoAllocHist * 4);
 constexpr size_t kSzNrow = up((size_t)kNoAllocRows * sizeof(lcs::NucRow));
@@ -328,8 +363,8 @@ constexpr size_t kOffNrow = kOffDPen + kSzD;
 constexpr size_t kOffNhCnt = kOffNrow + kSzNrow;
 constexpr size_t kOffNhMass = kOffNhCnt + kSzNhCnt;
 constexpr size_t kOffNlist = kOffNhMass + kSzNhMass;
-constexpr size_t kScratchBytes = kOffNlist + kSzNlist;   // about 39 MiB
-static_assert(kScratchBytes <= (40u << 20), "the no-alloc workspace stays modest");
+constexpr size_t kScratchBytes = kOffNlist + kSzNlist;   // about 42 MiB
+static_assert(kScratchBytes <= (44u << 20), "the no-alloc workspace stays modest");
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;   // serialises the first call on a device
@@ -343,6 +378,54 @@ std::atomic<unsigned char*> g_scratch_ptr[kMaxDevices] = {};
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 extern "C" {
+
+int lcs_windows_reserve(lcs_ctx* c, uint32_t slots, uint32_t max_window) {
+    if (!c) return LCS_ERR_INVALID_ARG;
+    if (slots == 0 || max_window == 0 || max_window > lcs::kWinMax) {
+        return fail(c, LCS_ERR_INVALID_ARG, "lcs_windows_reserve: slots >= 1, 1 <= max_window <= 4096");
+    }
+    if (c->wh && slots <= c->win_slots && max_window <= c->win_max) return LCS_OK;
+    DeviceGuard g(c->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(c->wh);
+    (void)hipFree(c->wring);
+    (void)hipFree(c->wbkt);
+    c->wh = nullptr; c->wring = nullptr; c->wbkt = nullptr; c->win_slots = 0; c->win_max = 0;
+    uint32_t h = 1;
+    while (h <= max_window) h <<= 1;   // H > max_window: the id that leaves never shares the new id's place
+    const size_t bkt_words = (size_t)slots * lcs::kSsMaxSlices * (lcs::kBktCap + 1);
+    hipError_t e = hipSuccess;
+    if ((!c->wstage && (e = hipMalloc(&c->wstage, (size_t)c->max_rows * sizeof(lcs::WinStage))) != hipSuccess) ||
+        (e = hipMalloc(&c->wh, (size_t)slots * sizeof(lcs::WinHdr))) != hipSuccess ||
+        (e = hipMalloc(&c->wring, (size_t)slots * 2 * h * 4)) != hipSuccess ||
+        (e = hipMalloc(&c->wbkt, bkt_words * 8)) != hipSuccess ||
+        (e = hipMemset(c->wh, 0xff, (size_t)slots * sizeof(lcs::WinHdr))) != hipSuccess ||
+        (e = hipDeviceSynchronize()) != hipSuccess) {
+        (void)hipFree(c->wh);
+        (void)hipFree(c->wring);
+        (void)hipFree(c->wbkt);
+        c->wh = nullptr; c->wring = nullptr; c->wbkt = nullptr;
+        return hip_fail(c, e, "lcs_windows_reserve");
+    }
+    c->win_slots = slots;
+    c->win_max = max_window;
+    c->win_h = h;
+    return LCS_OK;
+}
+
+int lcs_windows_load(lcs_ctx* c, uint32_t slot, const int32_t* ids, uint32_t n, uint32_t window, uint32_t vocab,
+                     void* stream) {
+    if (!c) return LCS_ERR_INVALID_ARG;
+    if (!c->wh) return fail(c, LCS_ERR_INVALID_ARG, "lcs_windows_load without lcs_windows_reserve");
+    if (slot >= c->win_slots) return fail(c, LCS_ERR_CAPACITY, "lcs_windows_load: slot above the reserved slots");
+    if (window == 0 || window > c->win_max) return fail(c, LCS_ERR_INVALID_ARG, "lcs_windows_load: window out of range");
+    if (vocab == 0 || vocab > lcs::kMaxVocab) return fail(c, LCS_ERR_INVALID_ARG, "lcs_windows_load: vocab out of range");
+    if (n > 0 && !ids) return fail(c, LCS_ERR_INVALID_ARG, "lcs_windows_load: null ids");
+    DeviceGuard g(c->device);
+    const hipError_t e = lcs::launch_win_load(c->wh, c->wring, c->wbkt, c->win_h, slot, ids, n, window, vocab,
+                                              slice_len_for(vocab, lcs::kSsMax), static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? LCS_OK : hip_fail(c, e, "window load launch");
+}
 
 int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
     if (!c) return LCS_ERR_INVALID_ARG;

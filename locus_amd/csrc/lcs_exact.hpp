@@ -21,6 +21,149 @@ constexpr float kInfF = __builtin_huge_valf();
 constexpr uint32_t kNoIdx = 0xffffffffu;
 constexpr double kTwo63 = 9223372036854775808.0;
 
+// ------------------------------------------------------ penalty windows --
+// Whether a row's device-resident window slot matches it: its vocabulary and
+// slice length, a history length this call keeps or grows by one, and, for a
+// row with penalties, its window. The call applies the append iff so.
+__device__ inline bool slot_ok(const WinHdr& hd, uint32_t len_new, uint32_t vocab, uint32_t slen, const lcs_params& P) {
+    return hd.vocab == vocab && hd.slen == slen && (len_new == hd.len || len_new == hd.len + 1u) &&
+           (!penalties_active(P) || hd.win == P.repeat_last_n);
+}
+
+// The row's penalty window, the last repeat_last_n ids of its history: a
+// contiguous span of ids and, for a device-resident window whose history
+// grows by one in this call, the appended id. The header read is the one
+// before the call's append, or (in row_fin, where the header advances) the
+// one after it: len is the only field that changes, and both give the same
+// window, since the ring holds the appended id before row_fin starts.
+// bad: the slot does not match the row.
+struct HistView {
+    const int32_t* ids;
+    uint32_t n;
+    int32_t extra;
+    uint32_t has_extra;
+    uint32_t bad;
+};
+__device__ inline HistView hist_view(const SampleArgs& a, uint32_t row, const lcs_params& P) {
+    HistView h{nullptr, 0u, 0, 0u, 0u};
+    const int32_t slot = a.win_slot != nullptr ? a.win_slot[row] : -1;
+    if (slot >= 0) {
+        const WinHdr hd = a.wh[slot];
+        const uint32_t len_new = a.win_len[row];
+        if (!slot_ok(hd, len_new, a.vocab, a.ss_len, P)) {
+            h.bad = 1u;
+            return h;
+        }
+        const bool push = len_new == hd.len + 1u;
+        const uint32_t wn = len_new < hd.win ? len_new : hd.win;   // the window after the append
+        const uint32_t start = len_new - wn;
+        h.ids = a.wring + (uint64_t)slot * 2u * a.wring_h + (start & (a.wring_h - 1u));
+        h.n = push ? wn - 1u : wn;
+        h.extra = push ? a.win_push[row] : 0;
+        h.has_extra = push ? 1u : 0u;
+        return h;
+    }
+    if (a.hist_off != nullptr) {
+        const uint32_t off = a.hist_off[row];
+        const uint32_t n = a.hist_off[row + 1] - off;
+        const uint32_t start = n > P.repeat_last_n ? n - P.repeat_last_n : 0u;
+        h.ids = a.hist_ids + off + start;
+        h.n = n - start;
+    }
+    return h;
+}
+
+// A device-resident window's bucket (lcs_internal.hpp), by one wave: a
+// call's append (the quad of position d_in gains a count, that of d_out loses
+// one; a quad left with no count is removed, the last entry moving into its
+// place), on the entries held in registers (R rounds of 64) and stored back;
+// a bucket past them is updated in memory by lane 0. Returns the new count.
+template <uint32_t R>
+__device__ __forceinline__ uint32_t bucket_update(uint64_t* bkt, uint64_t (&ent)[R], uint32_t n, uint32_t d_in,
+                                                  uint32_t d_out, uint32_t len) {
+    const int lane = lane_id();
+    const uint32_t l = (uint32_t)lane;
+    if (n + 1u > R * kWave) {
+        if (l == 0) {
+            if (d_in < len) {
+                uint32_t i = 0;
+                while (i < n && bkt_quad(bkt[1u + i]) != (d_in >> 2)) ++i;
+                bkt[1u + i] = (i < n ? bkt[1u + i] : (uint64_t)(d_in >> 2)) + bkt_one(d_in & 3u);
+                if (i == n) ++n;
+            }
+            if (d_out < len) {
+                uint32_t i = 0;
+                while (i < n && bkt_quad(bkt[1u + i]) != (d_out >> 2)) ++i;
+                if (i < n) {
+                    const uint64_t v = bkt[1u + i] - bkt_one(d_out & 3u);
+                    if ((v >> 11) == 0u) { bkt[1u + i] = bkt[n]; --n; } else { bkt[1u + i] = v; }
+                }
+            }
+            *reinterpret_cast<uint32_t*>(bkt) = n;
+        }
+        n = (uint32_t)__builtin_amdgcn_readfirstlane((int)n);
+        wait_all_memory();   // (lane 0's stores are done before the wave reads the entries)
+        wave_sync();
+#pragma unroll
+        for (uint32_t r = 0; r < R; ++r) {
+            const uint32_t e = r * kWave + l;
+            ent[r] = e < n ? bkt[1u + e] : 0ull;
+        }
+        return n;
+    }
+    if (d_in < len) {
+        const uint32_t q = d_in >> 2;
+        int hr = -1, hl = 0;
+#pragma unroll
+        for (uint32_t r = 0; r < R; ++r) {
+            const uint64_t m = ballot(r * kWave + l < n && bkt_quad(ent[r]) == q);
+            if (hr < 0 && m) { hr = (int)r; hl = __builtin_ctzll(m); }
+        }
+        const bool app = hr < 0;   // a new quad: appended at entry n
+        if (app) { hr = (int)(n / kWave); hl = (int)(n % kWave); ++n; }
+#pragma unroll
+        for (uint32_t r = 0; r < R; ++r) {
+            if ((int)r == hr && lane == hl) {
+                ent[r] = (app ? (uint64_t)q : ent[r]) + bkt_one(d_in & 3u);
+                bkt[1u + r * kWave + l] = ent[r];
+            }
+        }
+    }
+    if (d_out < len) {
+        const uint32_t q = d_out >> 2;
+        int hr = -1, hl = 0;
+#pragma unroll
+        for (uint32_t r = 0; r < R; ++r) {
+            const uint64_t m = ballot(r * kWave + l < n && bkt_quad(ent[r]) == q);
+            if (hr < 0 && m) { hr = (int)r; hl = __builtin_ctzll(m); }
+        }
+        if (hr >= 0) {
+            uint64_t v = 0, lv = 0;
+            const uint32_t last = n - 1u;
+#pragma unroll
+            for (uint32_t r = 0; r < R; ++r) {
+                if ((int)r == hr) v = readlane_u64(ent[r], hl);
+                if (r == last / kWave) lv = readlane_u64(ent[r], (int)(last % kWave));
+            }
+            v -= bkt_one(d_out & 3u);
+            const bool gone = (v >> 11) == 0u;
+            const uint32_t at = (uint32_t)hr * kWave + (uint32_t)hl;
+#pragma unroll
+            for (uint32_t r = 0; r < R; ++r) {
+                const uint32_t e = r * kWave + l;
+                if (e == at) {
+                    ent[r] = gone ? lv : v;
+                    if (!(gone && at == last)) bkt[1u + e] = ent[r];
+                }
+                if (gone && e == last) ent[r] = 0ull;
+            }
+            if (gone) --n;
+        }
+    }
+    if (l == 0) *reinterpret_cast<uint32_t*>(bkt) = n;
+    return n;
+}
+
 // ------------------------------------------------------------- top-n list --
 // Per-thread descending (value, index) list of the n best raw logits seen.
 struct TopList {
@@ -200,11 +343,16 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
 
     // ---- P0: distinct penalised ids of the window (apply_penalties) ----
     uint32_t nD = 0;
-    if (penalties_active(P) && a.hist_off != nullptr) {
-        const uint32_t off = a.hist_off[row];
-        const uint32_t n = a.hist_off[row + 1] - off;
-        const uint32_t start = n > P.repeat_last_n ? n - P.repeat_last_n : 0u;
-        const uint32_t wl = n - start;
+    const HistView hv = hist_view(a, row, P);
+    if (hv.bad) {
+        if (tid == 0) {
+            atomicOr(a.status, kStatusWindow);
+            a.ids[row] = -1;
+        }
+        return;
+    }
+    if (penalties_active(P) && hv.n + hv.has_extra > 0u) {
+        const uint32_t wl = hv.n + hv.has_extra;
         if (wl > DCAP || wl > a.max_hist) {
             if (tid == 0) {
                 atomicOr(a.status, kStatusHistCap);
@@ -215,7 +363,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
         if (wl > 0) {
             const uint32_t p2 = next_pow2(wl);
             for (uint32_t i = tid; i < p2; i += NT) {
-                sm.u.dsort[i] = i < wl ? (uint32_t)a.hist_ids[off + start + i] : 0xffffffffu;
+                sm.u.dsort[i] = i < hv.n ? (uint32_t)hv.ids[i] : i < wl ? (uint32_t)hv.extra : 0xffffffffu;
             }
             __syncthreads();
             bitonic_sort_u32<NT>(sm.u.dsort, p2);

@@ -77,7 +77,7 @@ __device__ __forceinline__ double ent_bound(double S, uint32_t n, float mk) {
 struct FinSmem {
     union {
         struct {
-            uint64_t top[kSsMaxSlices * kTopMax];   // the slices' top-n lists
+            uint64_t top[kRecsPerRow * kTopMax];    // the records' top-n lists
             uint64_t ent[kRowWin];
             float entraw[kRowWin];
             uint64_t sorted[kRowWin];
@@ -96,7 +96,7 @@ struct FinSmem {
     uint32_t tk_ns[kSsMaxSlices];                    // top-k rows: entries of each slice's list,
     uint32_t tk_cs[kSsMaxSlices], tk_base[kSsMaxSlices];   // its candidates (keys <= U), their offset
     uint64_t tk_u[4];                                // top-k rows: each wave's bound
-    uint32_t tn_ns[kSsMaxSlices];                    // top-n list lengths (logprobs)
+    uint32_t tn_ns[kRecsPerRow];                     // top-n list lengths (logprobs)
     uint32_t prof_row;   // (phase clocks: the row)
     SampleArgs args;   // the kernel arguments (exact_row reads them from here)
 };
@@ -136,7 +136,7 @@ __device__ __forceinline__ bool fin_logz(const uint64_t (&hd)[rec::kHdr], const 
     for (int j = 0; j < (int)kTopMax; ++j) {
         if (mine && (uint32_t)j < ntop) sm.u.f.top[lane * kTopMax + j] = (uint32_t)j < nts ? tk[j] : ~0ull;
     }
-    if (lane < (int)kSsMaxSlices) sm.tn_ns[lane] = nts;
+    if (lane < (int)kRecsPerRow) sm.tn_ns[lane] = nts;
     return false;
 }
 
@@ -630,7 +630,7 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
     const int lane = lane_id();
     const int wv = __builtin_amdgcn_readfirstlane((int)(tid / kWave));   // (an SGPR: wave-uniform branches)
     const uint32_t S = slices;
-    const uint64_t* recs = srecs + (uint64_t)row * kSsMaxSlices * rec::kWords64;
+    const uint64_t* recs = srecs + (uint64_t)row * kRecsPerRow * rec::kWords64;
     const uint64_t* my = recs + ((uint32_t)lane < S ? lane : 0) * rec::kWords64;   // lane s: slice s
     const bool want_lp = (flags & LCS_WANT_LOGPROBS) != 0;
     const uint32_t ntop = want_lp ? min(n_top, kTopMax) : 0u;
@@ -751,6 +751,14 @@ __global__ __launch_bounds__(kFinThreads) void row_fin(const lcs_params* params,
     if ((rows & 7u) == 0u) row = (row & 7u) * (rows >> 3) + (row >> 3);
     PROF_AT(kProfFin + row, 0 + tid_x() / 64);
     if (row >= rows || (flags & LCS_WRITE_PENALIZED) != 0) return;
+    // a device-resident window's header takes the state its slice kernel
+    // staged (its buckets and ring have advanced there); the exact path reads
+    // the same window either way (the appended id is in the ring, and the
+    // old header names it as the pending append)
+    if (a.win_slot != nullptr && tid_x() == 3u * kWave) {
+        const WinStage st = scalar_load(a.wstage + row);
+        if (st.flag == 1u) a.wh[st.slot] = st.hdr;
+    }
     fin_row<G, TK>(params, srecs, row, vocab, flags, slices, n_top, a, sm);
 }
 

@@ -24,6 +24,8 @@ constexpr int kSsThreads = 256;         // threads per slice workgroup
 constexpr int kSsElems = 32;            // logits per thread (8 f32 / 4 bf16 16-byte groups)
 constexpr uint32_t kSsMax = kSsThreads * kSsElems;          // 8192 per slice
 constexpr uint32_t kSsMaxSlices = kMaxVocab / kSsMax;       // 32
+constexpr uint32_t kRecsPerRow = 64;    // slice records a row owns in the workspace (sliced path: one per
+                                        // slice; wave path: one per wave-slice)
 constexpr uint32_t kSsTopKMerge = 2048;  // slices x top_k entries row_fin merges
 constexpr int kFinThreads = 256;         // row_fin workgroup
 
@@ -109,6 +111,36 @@ struct NucRow {
     NucRange r[kNucRanges];
 };
 
+// ---- device-resident penalty windows (lcs_windows_reserve / _load): per
+// slot a header, a ring holding the history's last ids (position i at
+// i mod H and i mod H + H, so that any run of at most H positions is
+// contiguous) and per slice of the sliced path a bucket of the window's
+// counts, one entry per 4-position quad that holds a counted id ----
+struct WinHdr {
+    uint32_t len;     // history length
+    uint32_t win;     // the window W (the rows' repeat_last_n)
+    uint32_t vocab;   // the vocabulary the buckets are cut for
+    uint32_t slen;    // the slice length they are cut at
+    int32_t out_id;   // the id at history position len - W (it leaves the window with the next append)
+    uint32_t pad[3];
+};
+// A row's next slot header, staged by its slice 0 workgroup (which wrote the
+// appended id into the ring) and copied into place by row_fin: the slice
+// kernel's other workgroups read the header, so it cannot change there.
+struct WinStage {
+    uint32_t flag;    // 1: copy hdr to wh[slot]
+    int32_t slot;
+    uint32_t pad[6];
+    WinHdr hdr;
+};
+constexpr uint32_t kWinMax = kFastHistMax;   // largest window a slot holds
+constexpr uint32_t kBktCap = kSsMax / 4;     // entries a bucket holds (a slice's quads)
+// bucket entry: the quad's index in the slice (bits 0-10), then its 4 counts
+// (positions 4q + k) of 13 bits at bits 11 + 13k
+__host__ __device__ inline uint32_t bkt_quad(uint64_t e) { return (uint32_t)(e & 2047u); }
+__host__ __device__ inline uint32_t bkt_count(uint64_t e, uint32_t k) { return (uint32_t)(e >> (11u + 13u * k)) & 8191u; }
+__host__ __device__ inline uint64_t bkt_one(uint32_t k) { return 1ull << (11u + 13u * k); }
+
 struct SampleArgs {   // (at most 128 dwords: kernels stage it in LDS, two dwords per lane)
     const void* logits;
     uint64_t row_stride;
@@ -127,7 +159,7 @@ struct SampleArgs {   // (at most 128 dwords: kernels stage it in LDS, two dword
     lcs_row_diag* diag;
     // workspace
     uint32_t* recs;          // nucleus: rows x slices x rec::kWords
-    uint64_t* srecs;         // sliced path: rows x kSsMaxSlices x rec::kWords64
+    uint64_t* srecs;         // sliced and wave paths: rows x kRecsPerRow x rec::kWords64
     uint32_t ss_slices;      // sliced path: slices per row (<= kSsMaxSlices)
     uint32_t ss_len;         // sliced path: elements per slice (multiple of 8, <= kSsMax)
     uint32_t* d_ids;         // rows x max_hist (distinct penalised ids)
@@ -146,7 +178,17 @@ struct SampleArgs {   // (at most 128 dwords: kernels stage it in LDS, two dword
     uint32_t* nh_cnt;        // kNucRows x kMaxSlices x kNucBins
     double* nh_mass;         // kNucRows x kMaxSlices x kNucBins
     uint64_t* nlist;         // kNucRows x kNucList rank keys
+    // device-resident penalty windows
+    const int32_t* win_slot; // rows: slot, or -1 (NULL: none)
+    const int32_t* win_push; // rows: id appended before this call
+    const uint32_t* win_len; // rows: history length after the push
+    WinHdr* wh;              // slots
+    int32_t* wring;          // slots x 2 wring_h
+    uint64_t* wbkt;          // slots x kSsMaxSlices x (kBktCap + 1): word 0 the count, then entries
+    uint32_t wring_h;        // H: ring half (a power of two above kWinMax)
+    WinStage* wstage;        // rows
 };
+
 
 struct VerifyArgs {
     const void* logits;
@@ -198,5 +240,6 @@ struct LmArgs {
 // status bits
 constexpr uint32_t kStatusHistCap = 1u;   // a penalty window exceeded the capacity
 constexpr uint32_t kStatusBinCap = 2u;    // selection could not narrow a bin (unexpected)
+constexpr uint32_t kStatusWindow = 4u;    // a device-resident window did not match its row
 
 }  // namespace lcs

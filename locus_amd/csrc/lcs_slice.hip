@@ -167,6 +167,9 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
     const lcs_params P = scalar_load(a.params + row);
     const bool masked = a.mask != nullptr && (a.has_mask == nullptr || scalar_load_u8(a.has_mask + row) != 0);
     const uint32_t mode = row_mode(P, masked, V);
+    // (a device-resident window's header keeps its state unless slice 0
+    // stages the next one below, from this same thread)
+    if (a.win_slot != nullptr && slice == 0 && tid == (uint32_t)((kSsWaves - 1) * kWave)) a.wstage[row].flag = 0u;
     if (mode == kModeGeneral || mode == kModeNucleus) {   // rows of other kernels
         wait_all_memory();   // (loads issued only when the host's parameter copy disagreed)
         return;
@@ -174,7 +177,7 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
     const uint32_t* mrow = masked ? a.mask + (uint64_t)row * a.mask_words : nullptr;
     const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
     const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
-    uint64_t* myrec = a.srecs + ((uint64_t)row * kSsMaxSlices + slice) * rec::kWords64;
+    uint64_t* myrec = a.srecs + ((uint64_t)row * kRecsPerRow + slice) * rec::kWords64;
     const float NEG = -__builtin_huge_valf();
     if ((mode & MS) == 0u) {
         // a sliced row this instantiation leaves out (the host's parameter
@@ -183,10 +186,36 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
         wait_all_memory();
         return;
     }
+    // a device-resident window (win_slot): this call's append, as positions
+    // in the slice of the id that enters and of the one that falls out of
+    // the window (>= len: elsewhere, or not counted: ids < 0 or >= V)
+    const int32_t slot = a.win_slot != nullptr ? scalar_load(a.win_slot + row) : -1;
+    uint64_t* bkt = nullptr;
+    uint32_t bn = 0, d_in = 0xffffffffu, d_out = 0xffffffffu;
+    WinHdr hd{};
+    bool push = false;
+    if (slot >= 0) {
+        hd = scalar_load(a.wh + slot);
+        const uint32_t len_new = scalar_load(a.win_len + row);
+        if (!slot_ok(hd, len_new, V, slice_len, P)) {
+            // the exact path reports the row (id -1, LCS_STATUS_WINDOW)
+            if (tid == 0) myrec[0] = (uint64_t)rec::kFlagExact << 48;
+            wait_all_memory();
+            return;
+        }
+        push = len_new == hd.len + 1u;
+        bkt = a.wbkt + ((uint64_t)slot * kSsMaxSlices + slice) * (kBktCap + 1u);
+        bn = scalar_load(reinterpret_cast<const uint32_t*>(bkt));
+        if (len_new == hd.len + 1u) {
+            d_in = (uint32_t)scalar_load(a.win_push + row) - lo;
+            if (hd.len >= hd.win) d_out = (uint32_t)hd.out_id - lo;
+            if (d_in == d_out) d_in = d_out = 0xffffffffu;   // (the same id: no change)
+        }
+    }
     const bool greedy = (MS & kModeGreedy) != 0u && mode == kModeGreedy;
     const bool stoch = (MS & kModeWindow) != 0u && mode == kModeWindow;
     const bool topk = (MS & kModeTopK) != 0u && mode == kModeTopK;
-    const bool pen = penalties_active(P) && a.hist_off != nullptr && P.repeat_last_n > 0;
+    const bool pen = penalties_active(P) && P.repeat_last_n > 0 && (slot >= 0 || a.hist_off != nullptr);
     const float inv_t = stoch ? fdiv(1.0f, P.temperature) : 1.0f;
     const float kk = fmul(inv_t, kLog2E);   // tempered offsets in log2 units
     if (!early) load_logits();
@@ -197,12 +226,13 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
     // hend, so the words past it (up to the last row of 64 groups) read as 0:
     // id 0, counted at position 0 of slice 0 and taken out again (zpad)
     const uint32_t hn = hend - hoff;
-    const uint32_t nwin_h = pen ? min(hn, P.repeat_last_n) : 0u;
+    const uint32_t nwin_h = pen && slot < 0 ? min(hn, P.repeat_last_n) : 0u;
     const uint32_t hs = hend - nwin_h;
     const uint32_t w0 = hs & ~3u;
     const uint32_t nq = (hend - w0 + 3) / 4;   // groups of the window, <= (kFastHistMax + 6) / 4
-    const bool hany = nwin_h > 0;              // (uniform over the workgroup)
-    const uint32_t zpad = lo == 0u && hany ? 4u * kWave * ((nq + kWave - 1) / kWave) - (hend - w0) : 0u;
+    // (uniform over the workgroup) counted positions may lie in the slice
+    const bool hany = nwin_h > 0 || (pen && (bn > 0u || d_in < len));
+    const uint32_t zpad = lo == 0u && nwin_h > 0 ? 4u * kWave * ((nq + kWave - 1) / kWave) - (hend - w0) : 0u;
     constexpr int HC = 3;                      // groups per lane per pass (3072 ids a pass)
     constexpr uint32_t kPass = HC * kSsWaves * kWave;
     static_assert(kPass * 4 == kHistPass, "history pass size");
@@ -255,8 +285,34 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
         }
         wave_sync();   // (the queue is reused by the next pass)
     };
+    // the slot's bucket as it stood before this call (row_fin applies the
+    // call's append to it): wave w holds rounds w, w + 4, .. of 64 entries
+    constexpr uint32_t kBr = 4;   // rounds a wave holds (more: loaded in the count loop)
+    uint64_t bent[kBr];
+#pragma unroll
+    for (uint32_t r = 0; r < kBr; ++r) bent[r] = 0ull;
+    if (slot >= 0 && pen) {
+#pragma unroll
+        for (uint32_t r = 0; r < kBr; ++r) {
+            const uint32_t e = (r * kSsWaves + (uint32_t)wv) * kWave + (uint32_t)lane;
+            if ((r * kSsWaves + (uint32_t)wv) * kWave < bn && e < bn) bent[r] = bkt[1u + e];
+        }
+    }
+    // the workgroup whose slice holds the id that enters or leaves advances
+    // the bucket once its record is out (wave 3, from entries loaded here)
+    const bool bupd = slot >= 0 && (d_in < len || d_out < len);
+    uint64_t uent[kBr];
+#pragma unroll
+    for (uint32_t r = 0; r < kBr; ++r) uent[r] = 0ull;
+    if (bupd && wv == kSsWaves - 1) {
+#pragma unroll
+        for (uint32_t r = 0; r < kBr; ++r) {
+            const uint32_t e = r * kWave + (uint32_t)lane;
+            if (r * kWave < bn && e < bn) uent[r] = bkt[1u + e];
+        }
+    }
     if (hany) {
-        hload(0);
+        if (nwin_h > 0) hload(0);
         // clear the tables (16 count words and one group word a thread)
 #pragma unroll
         for (int i = 0; i < (int)(kSsMax / 2 / 4 / NT); ++i)
@@ -334,11 +390,36 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
             sm.mraw[wv] = Mw;
         }
         PROF_W0(wg_x(), 2);
-        if (hany) {
+        if (nwin_h > 0) {
             hcount(0);
             for (uint32_t b = kPass; b < nq; b += kPass) {   // windows past 3000 ids
                 hload(b);
                 hcount(b);
+            }
+        } else if (slot >= 0 && pen) {
+            // the window's counts: the bucket's entries (four 16-bit counts
+            // a quad, and its group's bit), then this call's append as
+            // deltas: the id that enters +1, the one that leaves -1 (LDS
+            // atomics, so the order does not matter)
+            auto put = [&](uint64_t e) {
+                const uint32_t q = bkt_quad(e);
+                atomicAdd(&sm.cnt[2u * q], bkt_count(e, 0) | (bkt_count(e, 1) << 16));
+                atomicAdd(&sm.cnt[2u * q + 1u], bkt_count(e, 2) | (bkt_count(e, 3) << 16));
+                const uint32_t g = (4u * q) / G;   // the 16-byte group holding the quad
+                atomicOr(&sm.gbit[g % NT], 1u << (g / NT));
+            };
+#pragma unroll
+            for (uint32_t r = 0; r < kBr; ++r) {
+                if ((r * kSsWaves + (uint32_t)wv) * kWave + (uint32_t)lane < bn) put(bent[r]);
+            }
+            for (uint32_t e = (kBr * kSsWaves + (uint32_t)wv) * kWave + (uint32_t)lane; e < bn; e += kSsWaves * kWave)
+                put(bkt[1u + e]);   // (a bucket past the registers)
+            if (tid == 0) {
+                if (d_in < len) {
+                    atomicAdd(&sm.cnt[d_in >> 1], 1u << ((d_in & 1u) << 4));
+                    atomicOr(&sm.gbit[(d_in / G) % NT], 1u << (d_in / (G * NT)));
+                }
+                if (d_out < len) atomicSub(&sm.cnt[d_out >> 1], 1u << ((d_out & 1u) << 4));
             }
         }
         // the wave's raw max travels to the penalised phase in bref (window rows)
@@ -791,6 +872,25 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
         const float Ms = fmaxf(fmaxf(sm.mraw[0], sm.mraw[1]), fmaxf(sm.mraw[2], sm.mraw[3]));
         if (lane == 0)
             myrec[0] = (uint64_t)__float_as_uint(Ms) | ((uint64_t)min(nwr, kWinCap) << 32) | ((uint64_t)fl << 48);
+    }
+    if (bupd && wv == kSsWaves - 1) (void)bucket_update<kBr>(bkt, uent, bn, d_in, d_out, len);
+    if (slot >= 0 && slice == 0 && tid == (uint32_t)((kSsWaves - 1) * kWave)) {
+        // slice 0 advances the ring (nothing in this call reads the appended
+        // id's place) and stages the next header for row_fin
+        WinStage st{};
+        st.slot = slot;
+        st.flag = push ? 1u : 0u;
+        if (push) {
+            int32_t* ring = a.wring + (uint64_t)slot * 2u * a.wring_h;
+            const uint32_t p = hd.len & (a.wring_h - 1u);
+            const int32_t id = a.win_push[row];
+            ring[p] = id;
+            ring[p + a.wring_h] = id;
+            st.hdr = hd;
+            st.hdr.len = hd.len + 1u;
+            st.hdr.out_id = st.hdr.len >= hd.win ? ring[(st.hdr.len - hd.win) & (a.wring_h - 1u)] : 0;
+        }
+        a.wstage[row] = st;
     }
 #ifdef LCS_PROFILE
     wait_all_memory();

@@ -34,7 +34,8 @@ class _Batch(C.Structure):
                 ("flags", C.c_uint32), ("row_stride", C.c_uint64), ("logits", _P),
                 ("params", _P), ("params_host", _P), ("hist_off", _P), ("hist_ids", _P),
                 ("u", _P), ("mask", _P), ("has_mask", _P), ("mask_words", C.c_uint32),
-                ("n_top", C.c_uint32), ("lp_ids", _P)]
+                ("n_top", C.c_uint32), ("lp_ids", _P), ("win_slot", _P), ("win_push", _P),
+                ("win_len", _P)]
 
 
 class _Out(C.Structure):
@@ -101,6 +102,10 @@ def lib():
         L.lcs_lmhead.argtypes = [_P, C.POINTER(_LBatch), C.POINTER(_LOut), _P]
         L.lcs_last_error.restype = C.c_char_p
         L.lcs_last_error.argtypes = [_P]
+        L.lcs_windows_reserve.restype = C.c_int
+        L.lcs_windows_reserve.argtypes = [_P, C.c_uint32, C.c_uint32]
+        L.lcs_windows_load.restype = C.c_int
+        L.lcs_windows_load.argtypes = [_P, C.c_uint32, _P, C.c_uint32, C.c_uint32, C.c_uint32, _P]
         L.lcs_get_status.restype = C.c_int
         L.lcs_get_status.argtypes = [_P, C.POINTER(C.c_uint32), C.c_int]
         _lib = L
@@ -156,6 +161,17 @@ class Sampler:
         self._check(lib().lcs_get_status(self.ctx, C.byref(s), int(reset)))
         return s.value
 
+    # ------------------------------------------------- device-resident windows
+    def windows_reserve(self, slots: int, max_window: int):
+        self._check(lib().lcs_windows_reserve(self.ctx, slots, max_window))
+
+    def windows_load(self, slot: int, ids, window: int, vocab: int, stream=None):
+        """Starts `slot` from a history (a device int32 tensor, or None for an
+        empty one)."""
+        n = 0 if ids is None else int(ids.numel())
+        self._check(lib().lcs_windows_load(self.ctx, slot, _dptr(ids) if n else None, n, window, vocab,
+                                           _stream_handle(self.torch, stream)))
+
     # ---------------------------------------------------------------- inputs
     def upload(self, w, stride: int | None = None):
         """Device copies of a workloads.Workload (sampling configs)."""
@@ -204,7 +220,7 @@ class Sampler:
 
     # ---------------------------------------------------------------- calls
     def prepare(self, d, out, n_top: int | None = None, want_lp: bool | None = None,
-                has_mask=None, flags_extra: int = 0, use_host_params: bool = True):
+                has_mask=None, flags_extra: int = 0, use_host_params: bool = True, win=None):
         """Builds the C structs of one lcs_sample call once; returns a
         zero-argument launcher (for tight benchmark loops)."""
         w = d["w"]
@@ -226,6 +242,9 @@ class Sampler:
         b.has_mask = _dptr(has_mask)
         b.mask_words = w.mask_words
         b.n_top = n_top if want_lp else 0
+        if win is not None:
+            b.win_slot, b.win_push, b.win_len = _dptr(win["slot"]), _dptr(win["push"]), _dptr(win["len"])
+            b.hist_off = b.hist_ids = None
         o = _Out()
         o.ids = _dptr(out["ids"])
         o.chosen_lp = _dptr(out.get("chosen_lp"))
@@ -233,7 +252,7 @@ class Sampler:
         o.top_lp = _dptr(out.get("top_lp"))
         o.diag = _dptr(out.get("diag"))
         fn, ctx, bp, op = lib().lcs_sample, self.ctx, C.byref(b), C.byref(o)
-        keep = (ph, b, o, d, out)
+        keep = (ph, b, o, d, out, win)
 
         def launch(stream_handle):
             _ = keep
@@ -269,10 +288,13 @@ class Sampler:
 
     def sample_dev(self, d, out, n_top: int | None = None, want_lp: bool | None = None,
                    has_mask=None, flags_extra: int = 0, use_host_params: bool = True, stream=None,
-                   lp_ids=None, noalloc: bool = False):
+                   lp_ids=None, noalloc: bool = False, win=None):
         """Enqueues lcs_sample on device buffers from upload()/alloc_out();
         `lp_ids` (device int32 per row) makes chosen_lp report those ids;
-        `noalloc` calls lcs_sample_noalloc (no context) instead."""
+        `noalloc` calls lcs_sample_noalloc (no context) instead; `win`
+        ({"slot", "push", "len"}: device int32 / int32 / uint32 per row) takes
+        the rows' penalty windows from device-resident slots instead of the
+        workload's history."""
         w = d["w"]
         want_lp = w.want_logprobs if want_lp is None else want_lp
         n_top = w.n_top if n_top is None else n_top
@@ -293,13 +315,16 @@ class Sampler:
         b.mask_words = w.mask_words
         b.n_top = n_top if want_lp else 0
         b.lp_ids = _dptr(lp_ids)
+        if win is not None:
+            b.win_slot, b.win_push, b.win_len = _dptr(win["slot"]), _dptr(win["push"]), _dptr(win["len"])
+            b.hist_off = b.hist_ids = None
         o = _Out()
         o.ids = _dptr(out["ids"])
         o.chosen_lp = _dptr(out.get("chosen_lp"))
         o.top_ids = _dptr(out.get("top_ids"))
         o.top_lp = _dptr(out.get("top_lp"))
         o.diag = _dptr(out.get("diag"))
-        self._keep = (ph, b, o, lp_ids)
+        self._keep = (ph, b, o, lp_ids, win)
         sh = _stream_handle(self.torch, stream)
         if noalloc:
             rc = lib().lcs_sample_noalloc(C.byref(b), C.byref(o), sh)
