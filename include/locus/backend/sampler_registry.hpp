@@ -1,10 +1,13 @@
 /*
  * Sampler backend table, resolved with the reference's registry rules
  * (src/locus/backend/registry.hpp:107-131, registry.cpp:94-137): an explicit
- * choice, else the LOCUS_SAMPLER_BACKEND environment variable, else the best
- * available and selectable entry; std::invalid_argument for an unknown or
- * unusable name. (The variable is not the reference's LOCUS_BACKEND: that one
- * names math backends such as "cuda", which are not sampler names.)
+ * choice, else the reference's LOCUS_BACKEND environment variable when it
+ * names a sampler entry ("hip", or a registered one such as "scalar"), else
+ * LOCUS_SAMPLER_BACKEND, else the best available and selectable entry;
+ * std::invalid_argument for an unknown or unusable name. LOCUS_BACKEND also
+ * names the reference's math backends ("cuda", "vulkan", ...), which are not
+ * sampler entries: such a value leaves the sampler's choice to
+ * LOCUS_SAMPLER_BACKEND or the best entry.
  *
  * The library's own entry is "hip" (available when lcs_probe finds a gfx950
  * device). The reference's best_backend() never throws because its "scalar"
@@ -36,6 +39,8 @@ struct SamplerOps {
     /** Batched, device-resident (the C ABI of locus_sampler.h). */
     int (*sample_batch)(lcs_ctx*, const lcs_batch*, const lcs_out*, void* stream) = nullptr;
     int (*verify_batch)(lcs_ctx*, const lcs_verify_batch*, const lcs_verify_out*, void* stream) = nullptr;
+    /** Batched logprobs_from without a draw (lcs_logprobs). */
+    int (*logprobs_batch)(lcs_ctx*, const lcs_batch*, const int32_t* chosen, const lcs_out*, void* stream) = nullptr;
     /** Per-row host API with the signatures of sampling.hpp:70-89. */
     tok::TokenId (*sample)(std::span<float>, const model::SamplingParams&, std::span<const tok::TokenId>,
                            std::mt19937_64&, const model::TokenConstraint*) = nullptr;

@@ -25,6 +25,16 @@ extern "C" {
 
 typedef struct lcs_ctx lcs_ctx;
 
+/* A row's raw statistics, as the fused lm-head's epilogue leaves them
+ * (lcs_lmhead_out.stats): the log-normaliser of logprobs_from
+ * (sampling.cpp:155-163) and the first index of the max (llama.cpp:1237-1245)
+ * over the row's raw logits. 16 bytes. */
+typedef struct lcs_row_stats {
+    double log_z;              /* log sum_i exp(logit_i) */
+    float max;                 /* largest raw logit */
+    int32_t argmax;            /* its first index */
+} lcs_row_stats;
+
 enum lcs_status {
     LCS_OK = 0,
     LCS_ERR_INVALID_ARG = -1, /* bad pointer, size, alignment or dtype */
@@ -97,6 +107,12 @@ typedef struct lcs_batch {
                                   stored length (nothing appended) or one more; the slot's
                                   window, vocabulary and repeat_last_n must match the row,
                                   else the row gets id -1 and LCS_STATUS_WINDOW */
+    /* Optional (NULL: computed here): each row's raw statistics over the same
+     * logits, from the lcs_lmhead call that wrote them (lcs_lmhead_out.stats).
+     * With LCS_WANT_LOGPROBS, greedy, min-p window and sliced top-k rows then
+     * take their log-normaliser from it instead of summing the row's
+     * exponentials again; the other paths compute their own. */
+    const lcs_row_stats* raw_stats;
 } lcs_batch;
 
 /* Per-row diagnostics (optional output): the survivor set of the reference's
@@ -188,6 +204,9 @@ typedef struct lcs_lmhead_out {
     float* log_z;              /* rows: log sum exp of the row, or NULL */
     float* draft_lp;           /* rows (when draft != NULL), 0 for ids outside [0, vocab) */
     uint32_t* accept_len;      /* rows / rows_per_seq, or NULL */
+    lcs_row_stats* stats;      /* rows, or NULL: each row's log_z, max and argmax, for
+                                  lcs_batch.raw_stats of the lcs_sample call that samples
+                                  these logits */
 } lcs_lmhead_out;
 
 /* Number of usable gfx950 devices (0 when none). Replaces the runtime probe
@@ -220,6 +239,16 @@ int lcs_windows_load(lcs_ctx* ctx, uint32_t slot, const int32_t* ids, uint32_t n
 /* Batched sample (+ logprobs): replaces per-row sample()/logprobs_from()
  * (sampling.hpp:70-89) as called from engine.cpp:430-442. */
 int lcs_sample(lcs_ctx* ctx, const lcs_batch* batch, const lcs_out* out, void* stream);
+
+/* Batched logprobs_from (sampling.hpp:86-89, sampling.cpp:150-190) with no
+ * draw: per row, into out->chosen_lp, the log-probability of chosen[row]
+ * under the row's raw logits (0 for an id outside [0, V); chosen NULL: of the
+ * row's argmax), and into out->top_ids / top_lp the batch's n_top most likely
+ * ids with theirs; out->ids, when given, receives each row's argmax. Reads
+ * rows, vocab, dtype, row_stride, logits, n_top and raw_stats of batch and
+ * ignores the rest (params, history, u, mask, flags, windows). The backend
+ * registry's logprobs_batch op. */
+int lcs_logprobs(lcs_ctx* ctx, const lcs_batch* batch, const int32_t* chosen, const lcs_out* out, void* stream);
 
 /* lcs_sample without a context, allocating nothing: for callers that cannot
  * call hipMalloc (code under HIP graph capture, tight serving loops, harnesses

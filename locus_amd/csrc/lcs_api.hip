@@ -10,6 +10,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "lcs_internal.hpp"
 #include "locus_sampler.h"
@@ -49,6 +50,11 @@ struct lcs_ctx {
     lcs::WinStage* wstage = nullptr;   // max_rows
     int32_t* wring = nullptr;
     uint64_t* wbkt = nullptr;
+    // lcs_logprobs: greedy parameters (all fields zero) for max_rows rows, on
+    // the device and on the host, and its argmax ids when the caller wants none
+    lcs_params* lp_params = nullptr;
+    std::vector<lcs_params> lp_params_host;
+    int32_t* lp_ids = nullptr;
     std::string err;
 };
 
@@ -133,6 +139,7 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t 
     c->max_vocab = max_vocab;
     c->max_hist = max_hist > 0 ? max_hist : 1;
     c->max_top = max_top;
+    c->lp_params_host.assign(max_rows, lcs_params{});
     c->max_slices = slices_for(max_vocab, lcs::kSliceMax);
     const size_t rec_bytes = (size_t)max_rows * c->max_slices * lcs::rec::kWords * 4;
     const size_t srec_bytes = (size_t)max_rows * lcs::kRecsPerRow * lcs::rec::kWords64 * 8;
@@ -152,6 +159,9 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t 
         (e = hipMalloc(&c->nh_cnt, nh_elems * 4)) != hipSuccess ||
         (e = hipMalloc(&c->nh_mass, nh_elems * 8)) != hipSuccess ||
         (e = hipMalloc(&c->nlist, nuc_rows * lcs::kNucList * 8)) != hipSuccess ||
+        (e = hipMalloc(&c->lp_params, (size_t)max_rows * sizeof(lcs_params))) != hipSuccess ||
+        (e = hipMalloc(&c->lp_ids, (size_t)max_rows * 4)) != hipSuccess ||
+        (e = hipMemset(c->lp_params, 0, (size_t)max_rows * sizeof(lcs_params))) != hipSuccess ||
         (e = hipMemset(c->status, 0, 4)) != hipSuccess ||
         (e = hipDeviceSynchronize()) != hipSuccess) {
         g_create_error = std::string("lcs_create: ") + hipGetErrorString(e);
@@ -176,6 +186,8 @@ void lcs_destroy(lcs_ctx* c) {
     (void)hipFree(c->d_pen);
     (void)hipFree(c->status);
     (void)hipFree(c->lmrecs);
+    (void)hipFree(c->lp_params);
+    (void)hipFree(c->lp_ids);
     (void)hipFree(c->wh);
     (void)hipFree(c->wring);
     (void)hipFree(c->wbkt);
@@ -320,6 +332,7 @@ int sample_impl(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream, 
     a.wbkt = c->wbkt;
     a.wring_h = c->win_h;
     a.wstage = c->wstage;
+    a.raw_stats = b->raw_stats;
 
     DeviceGuard g(c->device);
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -430,6 +443,30 @@ int lcs_windows_load(lcs_ctx* c, uint32_t slot, const int32_t* ids, uint32_t n, 
 int lcs_sample(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream) {
     if (!c) return LCS_ERR_INVALID_ARG;
     return sample_impl(c, b, o, stream, false);
+}
+
+// logprobs_from over a batch: the sliced path's greedy rows with no
+// penalties report the raw log-normaliser, the top-n and chosen's logprob.
+int lcs_logprobs(lcs_ctx* c, const lcs_batch* b, const int32_t* chosen, const lcs_out* o, void* stream) {
+    if (!c) return LCS_ERR_INVALID_ARG;
+    if (!b || !o) return fail(c, LCS_ERR_INVALID_ARG, "null batch or output");
+    if (b->rows > c->max_rows) return fail(c, LCS_ERR_CAPACITY, "rows above the context limits");
+    lcs_batch g = *b;
+    g.flags = LCS_WANT_LOGPROBS;
+    g.params = c->lp_params;
+    g.params_host = c->lp_params_host.data();
+    g.hist_off = nullptr;
+    g.hist_ids = nullptr;
+    g.u = nullptr;
+    g.mask = nullptr;
+    g.has_mask = nullptr;
+    g.lp_ids = chosen;
+    g.win_slot = nullptr;
+    g.win_push = nullptr;
+    g.win_len = nullptr;
+    lcs_out go = *o;
+    if (!go.ids) go.ids = c->lp_ids;
+    return sample_impl(c, &g, &go, stream, false);
 }
 
 int lcs_sample_noalloc(const lcs_batch* b, const lcs_out* o, void* stream) {
@@ -582,6 +619,7 @@ int lcs_lmhead(lcs_ctx* c, const lcs_lmhead_batch* b, const lcs_lmhead_out* o, v
     a.draft_lp = b->draft ? o->draft_lp : nullptr;
     a.accept_len = o->accept_len;
     a.recs = c->lmrecs;
+    a.stats = o->stats;
     DeviceGuard g(c->device);
     const hipError_t e = lcs::launch_lmhead(a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(c, e, "lm-head kernel launch");

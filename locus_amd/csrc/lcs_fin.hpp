@@ -115,21 +115,27 @@ constexpr uint32_t kSpecWin = 8;    // window entries fetched per slice per roun
 // term within a few ulp and the f64 sum of at most 32 of them: well inside
 // the logprob tolerance of the outputs (which are f32). Returns true when a
 // slice's candidate list overflowed.
+// With the row's statistics from the lm-head (rs), its log-normaliser is
+// taken from there (the slices then skipped their raw sums).
 __device__ __forceinline__ bool fin_logz(const uint64_t (&hd)[rec::kHdr], const uint64_t (&tk)[kTopMax], uint32_t S,
-                                         uint32_t ntop, FinSmem& sm) {
+                                         uint32_t ntop, FinSmem& sm, const lcs_row_stats* rs) {
     const int lane = lane_id();
     const bool mine = (uint32_t)lane < S;
     const float NEG = -__builtin_huge_valf();
     const uint64_t h0 = hd[0], h1 = hd[1], h4 = hd[4];
-    const float m_raw = mine ? __uint_as_float((uint32_t)h0) : NEG;
     const uint32_t flags = mine ? (uint32_t)(h0 >> 48) : 0u;
-    const double s_raw = mine ? bits_d(h1) : 0.0;
     const uint32_t nts = mine ? (uint32_t)(h4 >> 32) : 0u;
-    const float M = wave_max(m_raw);
-    const double term = mine && m_raw != NEG ? s_raw * (double)fast_exp2((m_raw - M) * kLog2E) : 0.0;
-    const double z = wave_sum(term);   // in [1, V]
-    const double log_z = (double)__builtin_amdgcn_logf((float)z) * 0.6931471805599453 + (double)M;
-    if (lane == 0) sm.log_z = log_z;
+    if (rs != nullptr) {
+        if (lane == 0) sm.log_z = rs->log_z;
+    } else {
+        const float m_raw = mine ? __uint_as_float((uint32_t)h0) : NEG;
+        const double s_raw = mine ? bits_d(h1) : 0.0;
+        const float M = wave_max(m_raw);
+        const double term = mine && m_raw != NEG ? s_raw * (double)fast_exp2((m_raw - M) * kLog2E) : 0.0;
+        const double z = wave_sum(term);   // in [1, V]
+        const double log_z = (double)__builtin_amdgcn_logf((float)z) * 0.6931471805599453 + (double)M;
+        if (lane == 0) sm.log_z = log_z;
+    }
     if (ntop == 0) return false;
     if (ballot(mine && (flags & rec::kFlagCandOverflow))) return true;
 #pragma unroll
@@ -679,7 +685,7 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
     bool fb = false;
     if (topk) {
         if (!TK) fin_load_topk(recs, S, wv, tkk, tkr);
-        if (wv == 1 && want_lp) fb = fin_logz(hd, tk, S, ntop, sm);
+        if (wv == 1 && want_lp) fb = fin_logz(hd, tk, S, ntop, sm, a.raw_stats ? a.raw_stats + row : nullptr);
         // a slice that could not rank its list sends the row to the exact path
         if (wv == 0) fb = ballot((uint32_t)lane < S && ((uint32_t)(hd[0] >> 48) & rec::kFlagWinLost)) != 0;
         if (lane == 0) sm.fin_fb[wv] = fb ? 1u : 0u;
@@ -689,7 +695,7 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
         if (stoch) fb = fin_window(hd, wk, wr, my, S, P, sm, inv_t);
         else fin_greedy(a, hd, S, vocab, row, masked, sm);
     } else if (wv == 1) {
-        if (want_lp) fb = fin_logz(hd, tk, S, ntop, sm);
+        if (want_lp) fb = fin_logz(hd, tk, S, ntop, sm, a.raw_stats ? a.raw_stats + row : nullptr);
     } else if (wv == 2) {
         if (stoch) fin_norm(hd, S, sm, inv_t);
     }

@@ -187,6 +187,7 @@ struct SampleArgs {   // (at most 128 dwords: kernels stage it in LDS, two dword
     uint64_t* wbkt;          // slots x kSsMaxSlices x (kBktCap + 1): word 0 the count, then entries
     uint32_t wring_h;        // H: ring half (a power of two above kWinMax)
     WinStage* wstage;        // rows
+    const lcs_row_stats* raw_stats;   // rows, or NULL: the rows' raw log-normalisers (lcs_lmhead)
 };
 
 
@@ -235,6 +236,7 @@ struct LmArgs {
     float* draft_lp;
     uint32_t* accept_len;
     LmRec* recs;                    // rows x nblocks
+    lcs_row_stats* stats;           // rows, or NULL
 };
 
 // status bits

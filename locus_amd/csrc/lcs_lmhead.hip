@@ -301,6 +301,7 @@ __global__ __launch_bounds__(kLmThreads) void lmhead_fin(LmArgs a) {
             a.argmax_ids[row] = (int32_t)rank_idx(best);
             if (a.log_z) a.log_z[row] = (float)log_z;
             if (a.draft_lp) a.draft_lp[row] = own ? (float)((double)dl - log_z) : 0.0f;
+            if (a.stats) a.stats[row] = lcs_row_stats{log_z, M, (int32_t)rank_idx(best)};
             am[j] = (int32_t)rank_idx(best);
         }
     }

@@ -176,6 +176,7 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
     }
     const uint32_t* mrow = masked ? a.mask + (uint64_t)row * a.mask_words : nullptr;
     const bool want_lp = (a.flags & LCS_WANT_LOGPROBS) != 0;
+    const bool raw_sum = want_lp && a.raw_stats == nullptr;   // (else row_fin takes the lm-head's log_z)
     const uint32_t ntop = want_lp ? min(a.n_top, kTopMax) : 0u;
     uint64_t* myrec = a.srecs + ((uint64_t)row * kRecsPerRow + slice) * rec::kWords64;
     const float NEG = -__builtin_huge_valf();
@@ -361,7 +362,7 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
         if (Mw != NEG) {   // (a wave past the slice's end holds no term)
 #pragma unroll
             for (int j = 0; j < NG; ++j) {
-                if (want_lp) {
+                if (raw_sum) {
                     float c[G];
 #pragma unroll
                     for (int k = 0; k < G; ++k) c[k] = fast_exp2(fmaf(v[j * G + k], kLog2E, br));
@@ -383,7 +384,7 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
                 }
             }
         }
-        if (want_lp) {
+        if (raw_sum) {
             const float sw = Mw != NEG ? wave_sum_f(sr) * fast_exp2(-fmaf(Mw, kLog2E, br)) : 0.0f;
             if (lane == 0) { sm.sraw[wv] = sw; sm.mraw[wv] = Mw; }
         } else if (lane == 0) {
@@ -758,7 +759,7 @@ __global__ __launch_bounds__(kSsThreads) void slice_stats(const void* logits, ui
         const bool lr = lane < kSsWaves;
         const float mwr = lr ? sm.mraw[lr ? lane : 0] : NEG;
         const float Ms = wave_max(mwr);
-        const float tw = lr && want_lp && mwr != NEG ? sm.sraw[lr ? lane : 0] * fast_exp2((mwr - Ms) * kLog2E) : 0.0f;
+        const float tw = lr && raw_sum && mwr != NEG ? sm.sraw[lr ? lane : 0] * fast_exp2((mwr - Ms) * kLog2E) : 0.0f;
         double tq[kSsWaves];
 #pragma unroll
         for (int w = 0; w < kSsWaves; ++w) tq[w] = (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(tw), w));

@@ -29,6 +29,7 @@ struct Table {
         SamplerOps ops;
         ops.sample_batch = &lcs_sample;
         ops.verify_batch = &lcs_verify;
+        ops.logprobs_batch = &lcs_logprobs;
         ops.sample = &model::sample;
         ops.logprobs_from = &model::logprobs_from;
         ops.mt_safe = true;
@@ -66,6 +67,11 @@ const SamplerBackend& best_sampler_backend() {
 
 const SamplerBackend& resolve_sampler_backend(std::string_view choice) {
     std::string_view name = choice;
+    if (name.empty()) {
+        // the reference's variable, when it names a sampler entry
+        const char* env = std::getenv("LOCUS_BACKEND");
+        if (env != nullptr && find_sampler_backend(env) != nullptr) name = env;
+    }
     if (name.empty()) {
         const char* env = std::getenv("LOCUS_SAMPLER_BACKEND");
         if (env != nullptr && *env != '\0') name = env;

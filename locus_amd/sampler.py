@@ -35,7 +35,7 @@ class _Batch(C.Structure):
                 ("params", _P), ("params_host", _P), ("hist_off", _P), ("hist_ids", _P),
                 ("u", _P), ("mask", _P), ("has_mask", _P), ("mask_words", C.c_uint32),
                 ("n_top", C.c_uint32), ("lp_ids", _P), ("win_slot", _P), ("win_push", _P),
-                ("win_len", _P)]
+                ("win_len", _P), ("raw_stats", _P)]
 
 
 class _Out(C.Structure):
@@ -67,7 +67,7 @@ class _LBatch(C.Structure):
 
 class _LOut(C.Structure):
     _fields_ = [("logits", _P), ("ld_logits", C.c_uint64), ("argmax_ids", _P), ("log_z", _P),
-                ("draft_lp", _P), ("accept_len", _P)]
+                ("draft_lp", _P), ("accept_len", _P), ("stats", _P)]
 
 
 class SamplerError(RuntimeError):
@@ -102,6 +102,8 @@ def lib():
         L.lcs_lmhead.argtypes = [_P, C.POINTER(_LBatch), C.POINTER(_LOut), _P]
         L.lcs_last_error.restype = C.c_char_p
         L.lcs_last_error.argtypes = [_P]
+        L.lcs_logprobs.restype = C.c_int
+        L.lcs_logprobs.argtypes = [_P, C.POINTER(_Batch), _P, C.POINTER(_Out), _P]
         L.lcs_windows_reserve.restype = C.c_int
         L.lcs_windows_reserve.argtypes = [_P, C.c_uint32, C.c_uint32]
         L.lcs_windows_load.restype = C.c_int
@@ -220,7 +222,7 @@ class Sampler:
 
     # ---------------------------------------------------------------- calls
     def prepare(self, d, out, n_top: int | None = None, want_lp: bool | None = None,
-                has_mask=None, flags_extra: int = 0, use_host_params: bool = True, win=None):
+                has_mask=None, flags_extra: int = 0, use_host_params: bool = True, win=None, raw_stats=None):
         """Builds the C structs of one lcs_sample call once; returns a
         zero-argument launcher (for tight benchmark loops)."""
         w = d["w"]
@@ -245,6 +247,7 @@ class Sampler:
         if win is not None:
             b.win_slot, b.win_push, b.win_len = _dptr(win["slot"]), _dptr(win["push"]), _dptr(win["len"])
             b.hist_off = b.hist_ids = None
+        b.raw_stats = _dptr(raw_stats)
         o = _Out()
         o.ids = _dptr(out["ids"])
         o.chosen_lp = _dptr(out.get("chosen_lp"))
@@ -252,7 +255,7 @@ class Sampler:
         o.top_lp = _dptr(out.get("top_lp"))
         o.diag = _dptr(out.get("diag"))
         fn, ctx, bp, op = lib().lcs_sample, self.ctx, C.byref(b), C.byref(o)
-        keep = (ph, b, o, d, out, win)
+        keep = (ph, b, o, d, out, win, raw_stats)
 
         def launch(stream_handle):
             _ = keep
@@ -288,13 +291,14 @@ class Sampler:
 
     def sample_dev(self, d, out, n_top: int | None = None, want_lp: bool | None = None,
                    has_mask=None, flags_extra: int = 0, use_host_params: bool = True, stream=None,
-                   lp_ids=None, noalloc: bool = False, win=None):
+                   lp_ids=None, noalloc: bool = False, win=None, raw_stats=None):
         """Enqueues lcs_sample on device buffers from upload()/alloc_out();
         `lp_ids` (device int32 per row) makes chosen_lp report those ids;
         `noalloc` calls lcs_sample_noalloc (no context) instead; `win`
         ({"slot", "push", "len"}: device int32 / int32 / uint32 per row) takes
         the rows' penalty windows from device-resident slots instead of the
-        workload's history."""
+        workload's history; `raw_stats` (the "stats" output of lmhead_dev on
+        the same logits) gives the rows' raw log-normalisers."""
         w = d["w"]
         want_lp = w.want_logprobs if want_lp is None else want_lp
         n_top = w.n_top if n_top is None else n_top
@@ -318,13 +322,14 @@ class Sampler:
         if win is not None:
             b.win_slot, b.win_push, b.win_len = _dptr(win["slot"]), _dptr(win["push"]), _dptr(win["len"])
             b.hist_off = b.hist_ids = None
+        b.raw_stats = _dptr(raw_stats)
         o = _Out()
         o.ids = _dptr(out["ids"])
         o.chosen_lp = _dptr(out.get("chosen_lp"))
         o.top_ids = _dptr(out.get("top_ids"))
         o.top_lp = _dptr(out.get("top_lp"))
         o.diag = _dptr(out.get("diag"))
-        self._keep = (ph, b, o, lp_ids, win)
+        self._keep = (ph, b, o, lp_ids, win, raw_stats)
         sh = _stream_handle(self.torch, stream)
         if noalloc:
             rc = lib().lcs_sample_noalloc(C.byref(b), C.byref(o), sh)
@@ -340,6 +345,27 @@ class Sampler:
         self.sample_dev(d, out, **kw)
         self.torch.cuda.synchronize()
         return self.fetch(out, w.n_top)
+
+    def logprobs_dev(self, d, out, chosen=None, n_top: int | None = None, raw_stats=None, stream=None):
+        """Enqueues lcs_logprobs (logprobs_from over the batch, no draw) on
+        device buffers from upload()/alloc_out(): `chosen` (device int32 per
+        row, or None for each row's argmax)."""
+        w = d["w"]
+        b = _Batch()
+        b.rows, b.vocab = w.rows, w.vocab
+        b.dtype = LCS_BF16 if w.dtype == "bf16" else LCS_F32
+        b.row_stride = d["stride"]
+        b.logits = _dptr(d["logits"])
+        b.n_top = w.n_top if n_top is None else n_top
+        b.raw_stats = _dptr(raw_stats)
+        o = _Out()
+        o.ids = _dptr(out.get("ids"))
+        o.chosen_lp = _dptr(out.get("chosen_lp"))
+        o.top_ids = _dptr(out.get("top_ids"))
+        o.top_lp = _dptr(out.get("top_lp"))
+        self._keep = (b, o, chosen, raw_stats)
+        self._check(lib().lcs_logprobs(self.ctx, C.byref(b), _dptr(chosen), C.byref(o),
+                                       _stream_handle(self.torch, stream)))
 
     @staticmethod
     def fetch(out, n_top: int):
@@ -403,7 +429,9 @@ class Sampler:
         """The fused lm-head product (lcs_lmhead) on device tensors: x (rows,
         hidden) and w (vocab, hidden) bf16, contiguous; `out` holds any of
         "logits" (rows, >= vocab) f32, "argmax_ids", "log_z", "draft_lp",
-        "accept_len" (missing keys are not written; argmax_ids is required)."""
+        "accept_len", "stats" (rows x 16 bytes, lcs_row_stats: pass it as
+        sample_dev's raw_stats) (missing keys are not written; argmax_ids is
+        required)."""
         torch = self.torch
         if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
             raise SamplerError("x and w must be bfloat16")
@@ -422,14 +450,14 @@ class Sampler:
             if lg.dtype != torch.float32 or lg.stride(1) != 1:
                 raise SamplerError("logits must be f32 with unit column stride")
             o.logits, o.ld_logits = _dptr(lg), lg.stride(0)
-        for k in ("argmax_ids", "log_z", "draft_lp", "accept_len"):
+        for k in ("argmax_ids", "log_z", "draft_lp", "accept_len", "stats"):
             setattr(o, k, _dptr(out.get(k)))
         self._keep = (b, o)
         self._check(lib().lcs_lmhead(self.ctx, C.byref(b), C.byref(o),
                                      _stream_handle(torch, stream)))
 
     def alloc_lmhead_out(self, rows: int, vocab: int, logits: bool = True, draft: bool = False,
-                         n_seq: int = 0):
+                         n_seq: int = 0, stats: bool = False):
         torch = self.torch
         dev = torch.device("cuda", self.device)
         out = {"argmax_ids": torch.full((rows,), -7, dtype=torch.int32, device=dev),
@@ -440,6 +468,8 @@ class Sampler:
             out["draft_lp"] = torch.full((rows,), -7.0, dtype=torch.float32, device=dev)
         if n_seq:
             out["accept_len"] = torch.full((n_seq,), 99, dtype=torch.int32, device=dev)
+        if stats:   # lcs_row_stats: (f64 log_z, f32 max, i32 argmax) per row
+            out["stats"] = torch.full((rows, 2), -7.0, dtype=torch.float64, device=dev)
         return out
 
     def verify(self, w):

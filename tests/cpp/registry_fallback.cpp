@@ -12,6 +12,7 @@
 //                           parameters (continuous logits: no ties).
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <random>
 #include <string>
 #include <vector>
@@ -55,6 +56,25 @@ int main(int argc, char** argv) {
     CHECK(best->name == (gpu ? "hip" : "scalar"));
     CHECK(&resolve_sampler_backend("") == best);
     const SamplerBackend& cpu = resolve_sampler_backend("scalar");
+    {
+        // LOCUS_BACKEND (registry.cpp:114-137) selects a sampler entry it
+        // names; a math backend's name leaves the choice to
+        // LOCUS_SAMPLER_BACKEND, then to the best entry
+        setenv("LOCUS_BACKEND", "scalar", 1);
+        CHECK(&resolve_sampler_backend("") == &cpu);
+        if (gpu) CHECK(resolve_sampler_backend("hip").name == "hip");   // (an explicit choice first)
+        setenv("LOCUS_BACKEND", "cuda", 1);
+        CHECK(&resolve_sampler_backend("") == best);
+        setenv("LOCUS_SAMPLER_BACKEND", "scalar", 1);
+        CHECK(&resolve_sampler_backend("") == &cpu);
+        if (gpu) {
+            setenv("LOCUS_BACKEND", "hip", 1);
+            CHECK(resolve_sampler_backend("").name == "hip");
+        }
+        unsetenv("LOCUS_BACKEND");
+        unsetenv("LOCUS_SAMPLER_BACKEND");
+        CHECK(&resolve_sampler_backend("") == best);
+    }
     {
         // test_sampling.cpp:27-31 through the selected entry
         std::vector<float> l{1.0f, 3.0f, 2.0f, 0.5f};
