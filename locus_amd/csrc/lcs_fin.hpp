@@ -107,7 +107,7 @@ __device__ __forceinline__ bool fin_any_fb(const FinSmem& sm) {
     return (sm.fin_fb[0] | sm.fin_fb[1] | sm.fin_fb[2] | sm.fin_fb[3]) != 0u;
 }
 
-constexpr uint32_t kSpecWin = 8;    // window entries fetched per slice per round
+constexpr uint32_t kSpecWin = 16;   // window entries fetched per slice per round
 
 // Raw log-normaliser over the slices (logprobs_from, sampling.cpp:150-190),
 // and the slices' top-n lists staged in LDS for fin_topn_merge. The
@@ -230,29 +230,39 @@ __device__ __forceinline__ void fin_greedy(const SampleArgs& a, const uint64_t (
     }
 }
 
-// The row window's L0 entries (ent / entraw) ranked into sorted / sortedraw,
-// with their weights exp((double)((p - maxl) * inv_t)) in sw.
-__device__ __forceinline__ void fin_window_rank(FinSmem& sm, uint32_t L0, float maxl, float inv_t) {
+// The row window's fin_L0 entries (ent / entraw) ranked into sorted /
+// sortedraw, with their weights exp((double)((p - maxl) * inv_t)) in sw: by
+// every wave of the workgroup (after a barrier that follows fin_window's
+// stores), wave w taking entries w * 64 + lane and counting the smaller keys
+// with broadcast reads, so that a large window (up to kRowWin entries) costs
+// one pass over the keys rather than one per 64 entries.
+__device__ __forceinline__ void fin_window_rank(FinSmem& sm, int wv, float inv_t) {
     const int lane = lane_id();
-    wave_sync();
-    uint64_t k[4];
-    uint32_t rk[4];
-    lds_rank4(sm.u.f.ent, L0, k, rk);
-    PROF_AT(kProfFin + sm.prof_row, 27);
+    const uint32_t L0 = sm.fin_L0;
+    const float maxl = sm.fin_maxl;
+    const uint32_t e = (uint32_t)wv * kWave + (uint32_t)lane;
+    if ((uint32_t)wv * kWave >= L0) return;   // (wave-uniform)
+    const uint64_t k = e < L0 ? sm.u.f.ent[e] : ~0ull;
+    uint32_t rk = 0;
+    uint32_t f = 0;
+    for (; f + 8 <= L0; f += 8) {
+        uint64_t o[8];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const uint32_t e = (uint32_t)lane + (uint32_t)c * kWave;
-        if (e < L0) {
-            sm.u.f.sorted[rk[c]] = k[c];
-            sm.u.f.sortedraw[rk[c]] = sm.u.f.entraw[e];
-            sm.u.f.sw[rk[c]] = exp_f64((double)tempered(rank_val(k[c]), maxl, inv_t));
-        }
+        for (int j = 0; j < 8; ++j) o[j] = sm.u.f.ent[f + j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) rk += o[j] < k ? 1u : 0u;
     }
-    if (lane == 0) { sm.fin_L0 = L0; sm.fin_maxl = maxl; }
+    for (; f < L0; ++f) rk += sm.u.f.ent[f] < k ? 1u : 0u;
+    if (wv == 0) PROF_AT(kProfFin + sm.prof_row, 27);
+    if (e < L0) {
+        sm.u.f.sorted[rk] = k;
+        sm.u.f.sortedraw[rk] = sm.u.f.entraw[e];
+        sm.u.f.sw[rk] = exp_f64((double)tempered(rank_val(k), maxl, inv_t));
+    }
 #ifdef LCS_PROFILE
     wait_all_memory();
 #endif
-    PROF_AT(kProfFin + sm.prof_row, 28);
+    if (wv == 0) PROF_AT(kProfFin + sm.prof_row, 28);
 }
 
 // Window rows: every entry with p >= maxl - delta, gathered from the slices'
@@ -336,7 +346,7 @@ __device__ __forceinline__ bool fin_window(const uint64_t (&hd)[rec::kHdr], cons
     // a truncated slice whose every kept entry qualifies may hold more
     if (ballot(mine && (flags & rec::kFlagWinTrunc) && qtot == n_win)) return true;
     PROF_AT(kProfFin + sm.prof_row, 26);
-    fin_window_rank(sm, L0, maxl, inv_t);
+    if (lane == 0) { sm.fin_L0 = L0; sm.fin_maxl = maxl; }   // (ranked by fin_window_rank)
     return false;
 }
 
@@ -703,6 +713,10 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
     if (lane == 0) sm.fin_fb[wv] = fb ? 1u : 0u;
     __syncthreads();
     PROF_AT(kProfFin + row, 12 + wv);
+    if (stoch && !fin_any_fb(sm)) {   // (uniform over the workgroup)
+        fin_window_rank(sm, wv, inv_t);
+        __syncthreads();
+    }
     if (!fin_any_fb(sm)) {
         // logprob of the chosen token, or of the caller's lp_ids token (thread
         // 0, once the row's choice and log-normaliser are in)
