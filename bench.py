@@ -255,6 +255,24 @@ def mask_bench(budget_s: float = 5.0):
             "trie_cached_ms": float(np.mean(warm)) * 1e3, "cpu": cpu_model()}
 
 
+def batch_sampler_bench(steps: int, warmup: int):
+    """The serving path's step on C2 (locus_amd/host/batch_bench.cpp, a C++
+    program over BatchSampler::sample_step: host staging, uploads,
+    lcs_sample, read-back, synchronisation and the per-request updates), next
+    to lcs_sample alone on resident inputs (the headline's timed call)."""
+    import subprocess
+    exe = os.path.join(ROOT, "locus_amd", "batch_bench")
+    if not os.path.exists(exe):
+        raise SystemExit(f"{exe} is missing: run __graft_entry__.build()")
+    r = subprocess.run([exe, str(steps), str(warmup)], capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        raise SystemExit(f"batch_bench failed ({r.returncode}): {r.stderr.strip()}")
+    line = json.loads(r.stdout.strip().splitlines()[-1])
+    _, ms_step, _, _, _ = gpu_bench("c2", steps, warmup)
+    line["kernel_only_us_per_call"] = ms_step * 1e3
+    return line
+
+
 def draft_bench(n_seq: int = 512, ctx_len: int = 4096, ngram: int = 3, max_draft: int = 7,
                 steps: int = 200, cpu_seconds: float = 3.0):
     """Batched n-gram drafts on the device (lcs_ngram_draft) for C5's 512
@@ -516,7 +534,12 @@ def main():
                     help="only time batched n-gram drafts on the device against the CPU reference")
     ap.add_argument("--lmhead-bench", action="store_true",
                     help="only time the fused lm-head product at the decode shape")
+    ap.add_argument("--batch-sampler", action="store_true",
+                    help="only time the engine's batched step (BatchSampler::sample_step) end to end on C2")
     args = ap.parse_args()
+    if args.batch_sampler:
+        print(json.dumps(batch_sampler_bench(args.steps, args.warmup)))
+        return
     if args.lmhead_bench:
         print(json.dumps(lmhead_bench()))
         return

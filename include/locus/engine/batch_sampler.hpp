@@ -29,6 +29,17 @@
  * All staging memory (pinned host and device) is allocated by the
  * constructor; a step allocates nothing on the device. One BatchSampler
  * serves one thread at a time.
+ *
+ * A step whose rows are all min-p window rows (temperature > 0, min_p > 0, no
+ * top-k, no constraint, repeat_last_n <= min(max_hist, 4096) where penalties
+ * are on) keeps each request's penalty window on the device, in a slot keyed
+ * by the address of its `generated` vector: the slot takes the one id the
+ * history gained since the request's last step and uploads nothing else. A
+ * slot is (re)loaded from `generated` when the request is new, when its
+ * history did not grow by exactly that one id (or its id before it is not
+ * the one the slot saw last), or when its repeat_last_n changed; a request
+ * absent from a step loses its slot. The engine only appends to a request's
+ * history between steps, which is what the slot relies on.
  */
 #pragma once
 

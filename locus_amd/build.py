@@ -47,6 +47,7 @@ HOST_SOURCES = ["grammar.cpp", "speculative.cpp", "sampler_registry.cpp", "host_
                 "batch_sampler.cpp"]
 HOST_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-Wall", "-I" + INCLUDE]
 TEST_HOST = os.path.join(ROOT, "tests", "cpp", "test_host")
+BATCH_BENCH = os.path.join(HERE, "batch_bench")   # bench.py --batch-sampler
 
 
 def _run(cmd):
@@ -92,6 +93,11 @@ def build_host(jobs: int = 4) -> str:
     _run([HIPCC, "-o", TEST_HOST + ".tmp", tobj, "-L" + HERE, "-llocus_host", "-llocus_sampler",
           "-Wl,-rpath," + os.path.relpath(HERE, os.path.dirname(TEST_HOST)).join(["$ORIGIN/", ""])])
     os.replace(TEST_HOST + ".tmp", TEST_HOST)
+    bobj = os.path.join(BUILD, "batch_bench.o")
+    _run([HIPCC, *HOST_FLAGS, "-c", os.path.join(HERE, "host", "batch_bench.cpp"), "-o", bobj])
+    _run([HIPCC, "-o", BATCH_BENCH + ".tmp", bobj, "-L" + HERE, "-llocus_host", "-llocus_sampler",
+          "-Wl,-rpath,$ORIGIN"])
+    os.replace(BATCH_BENCH + ".tmp", BATCH_BENCH)
     return HOST_SO
 
 

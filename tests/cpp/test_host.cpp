@@ -508,6 +508,95 @@ static void test_batch_gpu() {
     CHECK(lim[0].generated.empty() && lim[1].generated.empty());
 }
 
+// BatchSampler on steps whose rows are all min-p window rows: the penalty
+// windows live in device slots that each step advances by the sampled id.
+// Requests leave and rejoin (their slots are released and reloaded), one
+// request's history is replaced between steps (the slot must reload), and
+// one has penalties off. Every step's ids and logprobs are checked against
+// the CPU oracle run on the request's whole history (sample_from,
+// engine.cpp:423-450).
+static void test_batch_gpu_windows() {
+    using locus::engine::BatchSampler;
+    using locus::sampler::SampleRequest;
+    constexpr std::uint32_t V = 32003, B = 12, K = 8, STRIDE = (V + 3) / 4 * 4;
+    const Oracle orc = load_oracle();
+    std::mt19937_64 pr(23);
+    std::vector<SampleRequest> a(B), c(B);
+    for (std::uint32_t r = 0; r < B; ++r) {
+        SamplingParams& p = a[r].sampling;
+        p.temperature = 0.7f + 0.05f * (float)(r % 3);
+        p.min_p = 0.05f;
+        p.top_p = 0.9f;
+        p.repeat_penalty = 1.1f;
+        p.frequency_penalty = 0.5f;
+        p.presence_penalty = 0.3f;
+        p.repeat_last_n = r % 3 == 0 ? 64 : 2048;
+        if (r == 5) p.repeat_penalty = 1.0f, p.frequency_penalty = 0.0f, p.presence_penalty = 0.0f;
+        a[r].rng.seed(500 + r);
+        const std::uint32_t n = r % 4 == 0 ? 3 : 200 + 100 * r;
+        // few distinct ids, so that counts repeat and entries leave the window
+        for (std::uint32_t i = 0; i < n; ++i) a[r].generated.push_back(static_cast<TokenId>(pr() % 700));
+        a[r].logprobs_opt = {r % 2 == 0, 5u};
+        c[r] = a[r];
+    }
+    BatchSampler bs(0, B, V, 4096, 20);
+    float* dlog = nullptr;
+    CHECK(hipMalloc(&dlog, (std::size_t)B * STRIDE * sizeof(float)) == hipSuccess);
+    std::mt19937 lr(7);
+    std::normal_distribution<float> nd(0.0f, 3.0f);
+    std::vector<float> host((std::size_t)B * STRIDE, 0.0f);
+    for (std::uint32_t step = 0; step < K; ++step) {
+        // rows 0-3 sit out steps 3 and 4; row 7's history is replaced before step 5
+        std::vector<std::uint32_t> in;
+        for (std::uint32_t r = 0; r < B; ++r)
+            if (!(r < 4 && (step == 3 || step == 4))) in.push_back(r);
+        if (step == 5) {
+            for (SampleRequest* q : {&a[7], &c[7]}) {
+                q->generated.assign(150, 0);
+                for (std::uint32_t i = 0; i < 150; ++i) q->generated[i] = static_cast<TokenId>((i * 37u) % 500u);
+            }
+        }
+        std::vector<SampleRequest*> ap;
+        for (std::uint32_t r : in) ap.push_back(&a[r]);
+        const std::uint32_t n = static_cast<std::uint32_t>(in.size());
+        for (std::uint32_t i = 0; i < n; ++i)
+            for (std::uint32_t t = 0; t < V; ++t) host[(std::size_t)i * STRIDE + t] = nd(lr);
+        CHECK(hipMemcpy(dlog, host.data(), (std::size_t)n * STRIDE * sizeof(float), hipMemcpyHostToDevice) ==
+              hipSuccess);
+        const std::vector<TokenId> ids = bs.sample_step(dlog, LCS_F32, STRIDE, ap);
+        CHECK(ids.size() == n);
+        for (std::uint32_t i = 0; i < n; ++i) {
+            SampleRequest& o = c[in[i]];
+            std::vector<float> raw(host.begin() + (std::ptrdiff_t)i * STRIDE,
+                                   host.begin() + (std::ptrdiff_t)i * STRIDE + V);
+            std::vector<float> row(raw);
+            OracleParams op;
+            std::memcpy(&op, &o.sampling, sizeof op);
+            const std::size_t nh = o.generated.size(), w = std::min<std::size_t>(nh, o.sampling.repeat_last_n);
+            const double u = std::generate_canonical<double, 53>(o.rng);
+            const TokenId oid = orc.sample(row.data(), V, &op, o.generated.data() + (nh - w),
+                                           static_cast<std::uint32_t>(w), u, nullptr, nullptr);
+            o.generated.push_back(oid);
+            if (oid != ids[i]) std::fprintf(stderr, "window step %u row %u: batch %d oracle %d\n", step, in[i], ids[i], oid);
+            CHECK(oid == ids[i]);
+            CHECK(a[in[i]].generated == o.generated);
+            if (o.logprobs_opt.enabled) {
+                float lp = 0.0f;
+                std::vector<std::int32_t> tid(6);
+                std::vector<float> tlp(6);
+                orc.logprobs(raw.data(), V, oid, 5, &lp, tid.data(), tlp.data(), nullptr);
+                const auto& e = a[in[i]].logprobs.back();
+                CHECK(std::fabs(e.logprob - lp) <= 1e-5f);
+                CHECK(e.top.size() == 5);
+                for (std::size_t j = 0; j < 5 && j < e.top.size(); ++j)
+                    CHECK(e.top[j].token == tid[j] && std::fabs(e.top[j].logprob - tlp[j]) <= 1e-5f);
+            }
+        }
+        for (std::uint32_t r : in) CHECK(a[r].rng == c[r].rng);
+    }
+    (void)hipFree(dlog);
+}
+
 // A row the device could not serve (id -1, locus_sampler.h) fails the step;
 // the status word is read only then.
 static void test_unserved_rows() {
@@ -541,6 +630,7 @@ int main(int argc, char** argv) {
             test_registry(true);
             test_sampling_gpu();
             test_batch_gpu();
+            test_batch_gpu_windows();
         } else {
             std::fprintf(stderr, "usage: test_host cpu|gpu\n");
             return 2;
