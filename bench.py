@@ -273,6 +273,87 @@ def batch_sampler_bench(steps: int, warmup: int):
     return line
 
 
+# phase clocks of the sliced path (the LCS_PROFILE build): slot k of a slice
+# workgroup, and of a row's finalize (row_fin), with what precedes it
+SLICE_PHASES = ["start", "logits decoded", "raw and tempered sums", "history counted (barrier B1)",
+                "reductions, penalised groups listed", "penalties applied, top-n bound",
+                "barrier B2", "top-n and window entries collected", "barrier B3", "record stored"]
+FIN_CHAIN = [(0, "start"), (4, "parameters and records in"), (24, "window threshold"),
+             (25, "window offsets"), (26, "window gathered"), (12, "barrier (all waves' parts in)"),
+             (27, "window ranked (4 waves)"), (28, "exact weights"), (29, "top-p / min-p scan"),
+             (30, "draw"), (16, "outputs written")]
+FIN_OTHER = [(9, "log-normaliser and top-n staged (wave 1)"), (10, "normaliser (wave 2)")]
+
+
+def phase_clocks(workload: str, rows: int | None, calls: int = 16):
+    """Per-phase wall clocks (s_memrealtime, 100 MHz) of the sliced path's
+    kernels on `workload`, from the LCS_PROFILE build of the library:
+    medians and maxima over workgroups and calls, in us from the call's first
+    slice start. Clocks of different XCDs may be offset from each other."""
+    import ctypes as C
+    import torch
+
+    from locus_amd import build as B
+    from locus_amd import sampler as SM
+    if not os.path.exists(B.PROFILE_SO):
+        raise SystemExit(f"{B.PROFILE_SO} is missing: run __graft_entry__.build()")
+    SM.LIB_PATH = B.PROFILE_SO
+    L = SM.lib()
+    L.lcs_prof_read.restype = C.c_int
+    L.lcs_prof_read.argtypes = [C.c_void_p, C.c_uint32]
+    ws = [W.make(workload, rows=rows, set_index=k) for k in range(4)]
+    s = SM.Sampler(device=0, max_rows=max(w.rows for w in ws), max_vocab=262144, max_hist=4096, max_top=20)
+    sets = []
+    for w in ws:
+        d = s.upload(w)
+        out = s.alloc_out(w.rows, w.n_top, w.want_logprobs, diag=False)
+        sets.append(s.prepare(d, out))
+    h = s.stream_handle()
+    kf, nrow = 16384, 4096
+    n = (kf + nrow) * 32
+    S_, F_ = [], []
+    for it in range(calls + 4):
+        sets[it % 4](h)
+        torch.cuda.synchronize()
+        buf = np.zeros(n, dtype=np.uint64)
+        if L.lcs_prof_read(buf.ctypes.data, n) != 0:
+            raise SystemExit("lcs_prof_read failed")
+        if it < 4:
+            continue
+        r = buf.reshape(-1, 32).astype(np.int64)
+        w = ws[it % 4]
+        nwg = w.rows * ((w.vocab + 8191) // 8192)
+        t0 = r[:nwg, 0].min()
+        S_.append((r[:nwg, :10] - t0) / 100.0)
+        F_.append((r[kf:kf + w.rows] - t0) / 100.0)
+    s.close()
+    S, F = np.concatenate(S_), np.concatenate(F_)
+    # absolute times (median over workgroups; clocks of different XCDs may be
+    # offset) and each phase's own duration in its workgroup (one XCD's clock)
+    lines = [f"# phase clocks, workload {workload} ({ws[0].rows} rows), {calls} calls: 'at' = us from the call's "
+             "first slice start (median), then the phase's own duration in us (median / p90 / max over "
+             "workgroups, or rows for row_fin)",
+             "slice_stats phase                                      at   median     p90     max"]
+    for k, name in enumerate(SLICE_PHASES):
+        d = S[:, k] - S[:, k - 1] if k else S[:, 0] * 0.0
+        lines.append(f"  {k}  {name:46s} {np.median(S[:, k]):6.2f}  {np.median(d):6.2f}  "
+                     f"{np.percentile(d, 90):6.2f}  {d.max():6.2f}")
+    lines.append("row_fin slot (wave 0's chain)                          at   median     p90     max")
+    prev = None
+    for k, name in FIN_CHAIN:
+        d = F[:, k] - F[:, prev] if prev is not None else F[:, k] * 0.0
+        lines.append(f"  {k:2d} {name:46s} {np.median(F[:, k]):6.2f}  {np.median(d):6.2f}  "
+                     f"{np.percentile(d, 90):6.2f}  {d.max():6.2f}")
+        prev = k
+    for k, name in FIN_OTHER:
+        d = F[:, k] - F[:, 0]
+        lines.append(f"  {k:2d} {name:46s} {np.median(F[:, k]):6.2f}  (from start: {np.median(d):.2f} median, "
+                     f"{d.max():.2f} max)")
+    tot = F[:, 16] - F[:, 0]
+    lines.append(f"row_fin per row, start to outputs: median {np.median(tot):.2f}, max {tot.max():.2f}")
+    return "\n".join(lines)
+
+
 def draft_bench(n_seq: int = 512, ctx_len: int = 4096, ngram: int = 3, max_draft: int = 7,
                 steps: int = 200, cpu_seconds: float = 3.0):
     """Batched n-gram drafts on the device (lcs_ngram_draft) for C5's 512
@@ -443,9 +524,16 @@ def summarize_trace(path, kernel):
     cond, par = _like("name", kernel)
     ks = c.execute("select name, count(*), avg(duration), min(duration), max(duration) from kernels "
                    f"where {cond} group by name", par).fetchall()
+    meds = []
     for name, n, avg, mn, mx in ks:
-        out.append(f"kernel_avg_us[{name}]: {avg / 1e3:.3f}  (n={n}, min {mn / 1e3:.3f}, max {mx / 1e3:.3f})")
+        d = np.array([r[0] for r in c.execute("select duration from kernels where name = ?", (name,))])
+        meds.append(float(np.median(d)))
+        out.append(f"kernel_avg_us[{name}]: {avg / 1e3:.3f}  (n={n}, median {meds[-1] / 1e3:.3f}, "
+                   f"min {mn / 1e3:.3f}, max {mx / 1e3:.3f})")
     out.append(f"call_kernel_avg_us[{kernel}]: {sum(k[2] for k in ks) / 1e3:.3f}  ({len(ks)} kernel(s) per call)")
+    # (the first dispatches of a process include one-time costs; the median
+    # is the steady state the timed region sees)
+    out.append(f"call_kernel_median_us[{kernel}]: {sum(meds) / 1e3:.3f}")
     return "\n".join(out)
 
 
@@ -536,7 +624,13 @@ def main():
                     help="only time the fused lm-head product at the decode shape")
     ap.add_argument("--batch-sampler", action="store_true",
                     help="only time the engine's batched step (BatchSampler::sample_step) end to end on C2")
+    ap.add_argument("--phase-clocks", action="store_true",
+                    help="only print the sliced path's phase clocks (the LCS_PROFILE build) on --workload")
+    ap.add_argument("--rows", type=int, default=None, help="rows of the workload (--phase-clocks)")
     args = ap.parse_args()
+    if args.phase_clocks:
+        print(phase_clocks(args.workload, args.rows))
+        return
     if args.batch_sampler:
         print(json.dumps(batch_sampler_bench(args.steps, args.warmup)))
         return

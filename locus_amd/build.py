@@ -58,20 +58,29 @@ def _run(cmd):
         raise RuntimeError(f"build failed: {' '.join(cmd)}\n{err}")
 
 
-def build_sampler(jobs: int = 4) -> str:
-    os.makedirs(BUILD, exist_ok=True)
+# the same library with the sliced path's phase clocks (LCS_PROFILE:
+# s_memrealtime stamps per workgroup phase, read by bench.py --phase-clocks)
+PROFILE_SO = os.path.join(HERE, "_prof", "liblocus_sampler.so")
+
+
+def build_sampler(jobs: int = 4, profile: bool = False) -> str:
+    out_so = PROFILE_SO if profile else SAMPLER_SO
+    bdir = os.path.join(BUILD, "prof") if profile else BUILD
+    os.makedirs(bdir, exist_ok=True)
+    os.makedirs(os.path.dirname(out_so), exist_ok=True)
+    defs = ["-DLCS_PROFILE"] if profile else []
     objs = []
     cmds = []
     for src in HIP_SOURCES:
-        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+        obj = os.path.join(bdir, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([HIPCC, *HIP_FLAGS, *HIP_EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([HIPCC, *HIP_FLAGS, *HIP_EXTRA.get(src, []), *defs, "-c", os.path.join(CSRC, src), "-o", obj])
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
-    tmp = SAMPLER_SO + ".tmp"
+    tmp = out_so + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-o", tmp, *objs])
-    os.replace(tmp, SAMPLER_SO)
-    return SAMPLER_SO
+    os.replace(tmp, out_so)
+    return out_so
 
 
 def build_host(jobs: int = 4) -> str:
@@ -137,6 +146,7 @@ def build_sanitized(jobs: int = 4) -> dict:
 def build_all() -> None:
     build_sampler()
     build_host()
+    build_sampler(profile=True)
 
 
 if __name__ == "__main__":
