@@ -264,10 +264,14 @@ def batch_sampler_bench(steps: int, warmup: int):
     exe = os.path.join(ROOT, "locus_amd", "batch_bench")
     if not os.path.exists(exe):
         raise SystemExit(f"{exe} is missing: run __graft_entry__.build()")
-    r = subprocess.run([exe, str(steps), str(warmup)], capture_output=True, text=True, timeout=600)
-    if r.returncode != 0:
-        raise SystemExit(f"batch_bench failed ({r.returncode}): {r.stderr.strip()}")
-    line = json.loads(r.stdout.strip().splitlines()[-1])
+    runs = []
+    for mode in ("windows", "uploads"):
+        r = subprocess.run([exe, str(steps), str(warmup), mode], capture_output=True, text=True, timeout=600)
+        if r.returncode != 0:
+            raise SystemExit(f"batch_bench failed ({r.returncode}): {r.stderr.strip()}")
+        runs.append(json.loads(r.stdout.strip().splitlines()[-1]))
+    line = runs[0]
+    line["uploaded_histories"] = {k: runs[1][k] for k in ("us_per_step", "us_median", "us_p90", "rows_per_s")}
     _, ms_step, _, _, _ = gpu_bench("c2", steps, warmup)
     line["kernel_only_us_per_call"] = ms_step * 1e3
     return line

@@ -90,9 +90,11 @@ class BatchSampler {
   public:
     /** `max_rows` requests per step over a vocabulary of `vocab` ids; penalty
      * windows up to `max_hist` ids; up to `max_top` logprob alternatives
-     * (<= 20). Throws std::runtime_error without a usable gfx950 device. */
+     * (<= 20). `device_windows` false keeps every step on uploaded histories
+     * (no device slots). Throws std::runtime_error without a usable gfx950
+     * device. */
     BatchSampler(int device, std::uint32_t max_rows, std::uint32_t vocab, std::uint32_t max_hist = 4096,
-                 std::uint32_t max_top = 20);
+                 std::uint32_t max_top = 20, bool device_windows = true);
     ~BatchSampler();
     BatchSampler(const BatchSampler&) = delete;
     BatchSampler& operator=(const BatchSampler&) = delete;

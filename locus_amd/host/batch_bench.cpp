@@ -9,7 +9,8 @@
 // read-back of ids and logprobs, the synchronisation, and the per-request
 // updates (the sampled id appended, so every window slides by one).
 //
-// Prints one JSON line. Usage: batch_bench [steps] [warmup]
+// Prints one JSON line. Usage: batch_bench [steps] [warmup] [uploads]
+// ("uploads": every step uploads the histories, no device-resident windows)
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -19,6 +20,7 @@
 #include <cstdlib>
 #include <numeric>
 #include <random>
+#include <string>
 #include <vector>
 
 #include "locus/engine/batch_sampler.hpp"
@@ -37,6 +39,7 @@ void check(hipError_t e, const char* what) {
 int main(int argc, char** argv) {
     const int steps = argc > 1 ? std::atoi(argv[1]) : 200;
     const int warmup = argc > 2 ? std::atoi(argv[2]) : 20;
+    const bool windows = !(argc > 3 && std::string(argv[3]) == "uploads");
     constexpr std::uint32_t rows = 64, V = 128256, hist = 2048, sets = 8;
     using locus::sampler::SampleRequest;
 
@@ -81,7 +84,7 @@ int main(int argc, char** argv) {
         ptrs.push_back(&q);
     }
 
-    locus::engine::BatchSampler bs(0, rows, V, 4096, 20);
+    locus::engine::BatchSampler bs(0, rows, V, 4096, 20, windows);
     hipStream_t st = nullptr;
     check(hipStreamCreate(&st), "hipStreamCreate");
     auto step = [&](int i) {
@@ -100,11 +103,12 @@ int main(int argc, char** argv) {
     const double total = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
     std::sort(us.begin(), us.end());
     const double mean = total / steps;
-    std::printf("{\"metric\": \"BatchSampler::sample_step end to end (C2 batch)\", \"us_per_step\": %.2f, "
+    std::printf("{\"metric\": \"BatchSampler::sample_step end to end (C2 batch)\", \"histories\": \"%s\", "
+                "\"us_per_step\": %.2f, "
                 "\"us_median\": %.2f, \"us_p90\": %.2f, \"rows_per_s\": %.1f, \"steps\": %d, \"warmup\": %d, "
                 "\"rows\": %u, \"vocab\": %u, \"history\": %u, \"logit_sets\": %u}\n",
-                mean, us[us.size() / 2], us[us.size() * 9 / 10], rows / (mean * 1e-6), steps, warmup, rows, V, hist,
-                sets);
+                windows ? "device windows" : "uploaded each step", mean, us[us.size() / 2], us[us.size() * 9 / 10],
+                rows / (mean * 1e-6), steps, warmup, rows, V, hist, sets);
     (void)hipStreamDestroy(st);
     (void)hipFree(dev);
     return 0;

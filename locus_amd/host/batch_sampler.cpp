@@ -95,7 +95,7 @@ struct BatchSampler::Buffers {
 };
 
 BatchSampler::BatchSampler(int device, std::uint32_t max_rows, std::uint32_t vocab, std::uint32_t max_hist,
-                           std::uint32_t max_top)
+                           std::uint32_t max_top, bool device_windows)
     : b_(new Buffers) {
     Buffers& b = *b_;
     if (max_rows == 0 || vocab == 0 || max_top > 20) {
@@ -128,7 +128,7 @@ BatchSampler::BatchSampler(int device, std::uint32_t max_rows, std::uint32_t voc
         // a slot per request a step can hold, twice over: the requests of a
         // step keep theirs, the others are released at its end
         b.win_max = std::min(b.max_hist, kWinMax);
-        b.win_ok = lcs_windows_reserve(b.ctx, 2 * max_rows, b.win_max) == LCS_OK;
+        b.win_ok = device_windows && lcs_windows_reserve(b.ctx, 2 * max_rows, b.win_max) == LCS_OK;
         for (std::uint32_t s = 2 * max_rows; s-- > 0;) b.free_slots.push_back(s);
     } catch (...) {
         b.release();
