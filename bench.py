@@ -358,6 +358,60 @@ def phase_clocks(workload: str, rows: int | None, calls: int = 16):
     return "\n".join(lines)
 
 
+def lmhead_rows_sweep(rows_list, vocab: int = 163840, hidden: int = 4096):
+    """lcs_lmhead (argmax and log z from the epilogue, no logits written)
+    against the unfused pair (torch's bf16 GEMM, i.e. hipBLASLt, to bf16
+    logits, then lcs_verify on them) at several row counts: where the fused
+    product's one-weight-read-per-64-rows design stops paying."""
+    import ctypes as C
+    import torch
+
+    from locus_amd import sampler as SM
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    w = (torch.randn((vocab, hidden), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    L = SM.lib()
+    stream = torch.cuda.current_stream()
+    out = []
+    for rows in rows_list:
+        x = torch.randn((rows, hidden), generator=gen, device=dev).to(torch.bfloat16)
+        s = SM.Sampler(device=0, max_rows=rows, max_vocab=vocab, max_hist=64, max_top=4)
+        h = s.stream_handle(stream)
+        am = torch.empty(rows, dtype=torch.int32, device=dev)
+        lz = torch.empty(rows, dtype=torch.float32, device=dev)
+        steps = max(3, 400 // rows)
+
+        def timed(fn):
+            for _ in range(2):
+                fn()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(steps):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / steps * 1e3
+        b = SM._LBatch(rows, vocab, hidden, 0, SM._dptr(x), SM._dptr(w), None)
+        o = SM._LOut(None, 0, SM._dptr(am), SM._dptr(lz), None, None)
+        t_f = timed(lambda: L.lcs_lmhead(s.ctx, C.byref(b), C.byref(o), h))
+        lb = torch.empty((rows, vocab), dtype=torch.bfloat16, device=dev)
+        dr = torch.zeros(rows, dtype=torch.int32, device=dev)
+        dlp = torch.empty(rows, dtype=torch.float32, device=dev)
+        acc = torch.empty(rows, dtype=torch.int32, device=dev)
+        vb = SM._VBatch(rows, 1, vocab, SM.LCS_BF16, vocab, SM._dptr(lb), SM._dptr(dr))
+        vo = SM._VOut(SM._dptr(am), SM._dptr(dlp), SM._dptr(acc))
+        t_g = timed(lambda: torch.mm(x, w.t(), out=lb))
+        t_v = timed(lambda: L.lcs_verify(s.ctx, C.byref(vb), C.byref(vo), h))
+        fl = 2.0 * rows * vocab * hidden
+        out.append({"rows": rows, "vocab": vocab, "hidden": hidden, "lcs_lmhead_us": t_f,
+                    "lcs_lmhead_tflops": fl / t_f / 1e6, "gemm_us": t_g, "gemm_tflops": fl / t_g / 1e6,
+                    "verify_us": t_v, "gemm_plus_verify_us": t_g + t_v})
+        s.close()
+        del lb, x
+        torch.cuda.empty_cache()
+    return out
+
+
 def draft_bench(n_seq: int = 512, ctx_len: int = 4096, ngram: int = 3, max_draft: int = 7,
                 steps: int = 200, cpu_seconds: float = 3.0):
     """Batched n-gram drafts on the device (lcs_ngram_draft) for C5's 512
@@ -626,6 +680,8 @@ def main():
                     help="only time batched n-gram drafts on the device against the CPU reference")
     ap.add_argument("--lmhead-bench", action="store_true",
                     help="only time the fused lm-head product at the decode shape")
+    ap.add_argument("--lmhead-rows", default=None, metavar="R1,R2,..",
+                    help="only time lcs_lmhead against GEMM + lcs_verify at these row counts (V=163840, hidden 4096)")
     ap.add_argument("--batch-sampler", action="store_true",
                     help="only time the engine's batched step (BatchSampler::sample_step) end to end on C2")
     ap.add_argument("--phase-clocks", action="store_true",
@@ -640,6 +696,10 @@ def main():
         return
     if args.lmhead_bench:
         print(json.dumps(lmhead_bench()))
+        return
+    if args.lmhead_rows:
+        for r in lmhead_rows_sweep([int(v) for v in args.lmhead_rows.split(",")]):
+            print(json.dumps(r), flush=True)
         return
     if args.mask_bench:
         print(json.dumps(mask_bench()))

@@ -228,6 +228,7 @@ struct LmArgs {
     const uint16_t* w;              // vocab x hidden bf16
     uint32_t rows, vocab, hidden, m0, nblocks, rows_per_seq;
     uint32_t cols;                  // columns per block (lmhead_cols)
+    uint32_t nchunks;               // 64-row chunks of one launch (see lmhead_kernel)
     uint64_t ld_logits;             // elements between logits rows
     const int32_t* draft;
     float* logits;

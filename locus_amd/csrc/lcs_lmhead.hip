@@ -66,7 +66,12 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 }  // namespace
 
-// a.m0: first row of this launch's chunk (<= kLmRows rows). WC: 16-column
+// A workgroup computes one block of columns for one chunk of <= kLmRows
+// rows. With one chunk (a.nchunks 1) workgroup w takes block w of chunk
+// a.m0. With several, one launch covers every chunk, and the workgroups of a
+// block are placed on one XCD in consecutive dispatch slots (workgroups are
+// dealt to the 8 XCDs in turn): they run together, so the block's weight rows
+// come from HBM once and from that XCD's L2 for the other chunks. WC: 16-column
 // MFMA tiles per wave (the workgroup's block is 64 WC columns); kDepth:
 // weight k-steps in flight ahead of the product.
 template <int WC, int kDepth>
@@ -77,9 +82,15 @@ __global__ __launch_bounds__(kLmThreads, 2) void lmhead_kernel(LmArgs a) {
     __shared__ uint32_t pfound[kLmRows];
     const uint32_t tid = tid_x();
     const int lane = lane_id(), wv = (int)(tid / kWave);
-    const uint32_t nb = wg_x();
+    uint32_t nb = wg_x(), m0 = a.m0;
+    if (a.nchunks > 1u) {
+        const uint32_t slot = nb >> 3;
+        m0 = (slot % a.nchunks) * kLmRows;
+        nb = 8u * (slot / a.nchunks) + (nb & 7u);
+        if (nb >= a.nblocks) return;   // (the grid is a multiple of 8 blocks)
+    }
     const uint32_t K = a.hidden, V = a.vocab;
-    const uint32_t m0 = a.m0, mrows = min((uint32_t)kLmRows, a.rows - m0);
+    const uint32_t mrows = min((uint32_t)kLmRows, a.rows - m0);
     constexpr uint32_t kCols = 4u * 16u * WC;
     const uint32_t nw = nb * kCols + (uint32_t)wv * (16u * WC);   // this wave's first column
     const uint32_t lr = (uint32_t)lane & 15u, kq = (uint32_t)lane >> 4;
@@ -329,10 +340,12 @@ uint32_t lmhead_cols(uint32_t vocab, uint32_t cus) {
 hipError_t launch_lmhead(const LmArgs& a0, hipStream_t st) {
     LmArgs a = a0;
     const bool wide = a0.cols == 320u;
-    for (uint32_t m0 = 0; m0 < a0.rows; m0 += kLmRows) {
-        a.m0 = m0;
-        if (wide) hipLaunchKernelGGL((lmhead_kernel<5, 2>), dim3(a.nblocks), dim3(kLmThreads), 0, st, a);
-        else hipLaunchKernelGGL((lmhead_kernel<4, 3>), dim3(a.nblocks), dim3(kLmThreads), 0, st, a);
+    a.m0 = 0;
+    a.nchunks = (a0.rows + kLmRows - 1) / kLmRows;
+    const uint32_t grid = a.nchunks > 1u ? 8u * ((a.nblocks + 7u) / 8u) * a.nchunks : a.nblocks;
+    if (wide) hipLaunchKernelGGL((lmhead_kernel<5, 2>), dim3(grid), dim3(kLmThreads), 0, st, a);
+    else hipLaunchKernelGGL((lmhead_kernel<4, 3>), dim3(grid), dim3(kLmThreads), 0, st, a);
+    {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
