@@ -2,12 +2,15 @@
 // src/locus/engine/engine.cpp:541-557, with Engine::sample_from's per-request
 // effects, engine.cpp:423-450) over one lcs_sample call.
 //
-// A step moves its inputs in one host-to-device copy and its outputs in one
-// device-to-host copy: every per-step array lives in one pinned block with a
-// device mirror of the same layout. When every row of a step is a min-p window
-// row (the C2 configuration's rows), the penalty windows stay on the device
-// (lcs_windows_reserve / lcs_windows_load): a request's slot receives the one
-// id its history gained since the last step, so the step uploads no history.
+// A step's small per-row arrays (parameters, uniforms, offsets, window
+// fields) live in one pinned host block that the kernels read in place, and
+// the kernels write the outputs into another pinned block: no copy is queued
+// for them. Histories and masks, which every slice workgroup of a row reads,
+// are copied to a device mirror in one copy. When every row of a step is a
+// min-p window row (the C2 configuration's rows), the penalty windows stay on
+// the device (lcs_windows_reserve / lcs_windows_load): a request's slot
+// receives the one id its history gained since the last step, so the step
+// uploads no history and queues no copy at all.
 #include "locus/engine/batch_sampler.hpp"
 
 #include <algorithm>
@@ -63,12 +66,16 @@ struct BatchSampler::Buffers {
     std::vector<std::uint32_t> want_h;
     lcs_ctx* ctx = nullptr;
     hipStream_t own = nullptr;
-    // inputs: pinned block and device mirror; outputs: the same
+    // inputs: a pinned block, its device address (the kernels read the small
+    // per-row arrays from it in place) and a device mirror for the histories
+    // and masks (copied: every slice workgroup reads them); outputs: a pinned
+    // block the kernels write in place
     unsigned char* in_h = nullptr;
+    unsigned char* in_hd = nullptr;
     unsigned char* in_d = nullptr;
     std::size_t in_cap = 0;
     unsigned char* out_h = nullptr;
-    unsigned char* out_d = nullptr;
+    unsigned char* out_hd = nullptr;
     std::size_t out_cap = 0;
     // the last run's outputs, inside out_h
     const std::int32_t* ids_h = nullptr;
@@ -87,8 +94,7 @@ struct BatchSampler::Buffers {
         if (in_h) (void)hipHostFree(in_h);
         if (out_h) (void)hipHostFree(out_h);
         if (in_d) (void)hipFree(in_d);
-        if (out_d) (void)hipFree(out_d);
-        in_h = out_h = in_d = out_d = nullptr;
+        in_h = out_h = in_d = in_hd = out_hd = nullptr;
         if (own) (void)hipStreamDestroy(own);
         own = nullptr;
     }
@@ -124,7 +130,8 @@ BatchSampler::BatchSampler(int device, std::uint32_t max_rows, std::uint32_t voc
         check(hipHostMalloc(reinterpret_cast<void**>(&b.in_h), b.in_cap, hipHostMallocDefault), "hipHostMalloc");
         check(hipHostMalloc(reinterpret_cast<void**>(&b.out_h), b.out_cap, hipHostMallocDefault), "hipHostMalloc");
         check(hipMalloc(reinterpret_cast<void**>(&b.in_d), b.in_cap), "hipMalloc");
-        check(hipMalloc(reinterpret_cast<void**>(&b.out_d), b.out_cap), "hipMalloc");
+        check(hipHostGetDevicePointer(reinterpret_cast<void**>(&b.in_hd), b.in_h, 0), "hipHostGetDevicePointer");
+        check(hipHostGetDevicePointer(reinterpret_cast<void**>(&b.out_hd), b.out_h, 0), "hipHostGetDevicePointer");
         // a slot per request a step can hold, twice over: the requests of a
         // step keep theirs, the others are released at its end
         b.win_max = std::min(b.max_hist, kWinMax);
@@ -276,7 +283,10 @@ void BatchSampler::run(const void* logits, lcs_dtype dtype, std::uint32_t row_st
         }
     } forget{b};
     check(hipSetDevice(b.device), "hipSetDevice");
-    check(hipMemcpyAsync(b.in_d, b.in_h, in_bytes, hipMemcpyHostToDevice, st), "copy");
+    // the histories (or the windows a step loads) and the masks travel to
+    // the device; the small arrays before them are read in place
+    if (in_bytes > o_hist && (off > 0 || any_mask))
+        check(hipMemcpyAsync(b.in_d + o_hist, b.in_h + o_hist, in_bytes - o_hist, hipMemcpyHostToDevice, st), "copy");
     for (const Load& l : loads) {
         const auto* ids = reinterpret_cast<const std::int32_t*>(b.in_d + o_hist) + l.off;
         if (lcs_windows_load(b.ctx, l.slot, l.n ? ids : nullptr, l.n, l.win, V, st) != LCS_OK)
@@ -293,25 +303,25 @@ void BatchSampler::run(const void* logits, lcs_dtype dtype, std::uint32_t row_st
     bt.flags = any_lp ? LCS_WANT_LOGPROBS : 0u;
     bt.row_stride = row_stride;
     bt.logits = logits;
-    bt.params = reinterpret_cast<const lcs_params*>(b.in_d + o_params);
+    bt.params = reinterpret_cast<const lcs_params*>(b.in_hd + o_params);
     bt.params_host = params_h;
-    bt.hist_off = any_hist ? reinterpret_cast<const std::uint32_t*>(b.in_d + o_hoff) : nullptr;
+    bt.hist_off = any_hist ? reinterpret_cast<const std::uint32_t*>(b.in_hd + o_hoff) : nullptr;
     bt.hist_ids = any_hist ? reinterpret_cast<const std::int32_t*>(b.in_d + o_hist) : nullptr;
-    bt.u = reinterpret_cast<const double*>(b.in_d + o_u);
+    bt.u = reinterpret_cast<const double*>(b.in_hd + o_u);
     bt.mask = any_mask ? reinterpret_cast<const std::uint32_t*>(b.in_d + o_mask) : nullptr;
-    bt.has_mask = any_mask ? b.in_d + o_has : nullptr;
+    bt.has_mask = any_mask ? b.in_hd + o_has : nullptr;
     bt.mask_words = b.words;
     bt.n_top = any_lp ? n_top : 0u;
     if (all_win) {
-        bt.win_slot = reinterpret_cast<const std::int32_t*>(b.in_d + o_wslot);
-        bt.win_push = reinterpret_cast<const std::int32_t*>(b.in_d + o_wpush);
-        bt.win_len = reinterpret_cast<const std::uint32_t*>(b.in_d + o_wlen);
+        bt.win_slot = reinterpret_cast<const std::int32_t*>(b.in_hd + o_wslot);
+        bt.win_push = reinterpret_cast<const std::int32_t*>(b.in_hd + o_wpush);
+        bt.win_len = reinterpret_cast<const std::uint32_t*>(b.in_hd + o_wlen);
     }
-    lcs_out o{reinterpret_cast<std::int32_t*>(b.out_d), reinterpret_cast<float*>(b.out_d + q_lp),
-              reinterpret_cast<std::int32_t*>(b.out_d + q_ti), reinterpret_cast<float*>(b.out_d + q_tl), nullptr};
+    lcs_out o{reinterpret_cast<std::int32_t*>(b.out_hd), reinterpret_cast<float*>(b.out_hd + q_lp),
+              reinterpret_cast<std::int32_t*>(b.out_hd + q_ti), reinterpret_cast<float*>(b.out_hd + q_tl), nullptr};
     if (const int rc = lcs_sample(b.ctx, &bt, &o, st); rc != LCS_OK)
         throw std::runtime_error(std::string("lcs_sample: ") + lcs_last_error(b.ctx));
-    check(hipMemcpyAsync(b.out_h, b.out_d, out_bytes, hipMemcpyDeviceToHost, st), "copy");
+    (void)out_bytes;
     check(hipStreamSynchronize(st), "hipStreamSynchronize");
     forget.armed = false;
     // slots of requests that were not in this step are released
