@@ -38,6 +38,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "lcs_device.hpp"
 #include "lcs_exact.hpp"
 #include "lcs_internal.hpp"
@@ -53,10 +55,10 @@ constexpr uint32_t kGroupMax = 4 * kWave;  // candidates one decisive group may 
 constexpr uint32_t kNucKeyCache = 2048;     // compacted candidates the select finalize keeps in LDS
 constexpr float kL2E = 1.4426950408889634f;
 constexpr double kGuard = 1e-10;
+// pass B's packed bin words: the count's unit, and the bits of 1.5 * 2^52
+constexpr uint64_t kPkOne = 1ull << 50;
+constexpr uint64_t kPkMagic = 0x4338000000000000ull;
 }  // namespace
-// 1/k! for k = 10, 9, ..., 3
-__constant__ double kInvFact[8] = {1.0 / 3628800.0, 1.0 / 362880.0, 1.0 / 40320.0, 1.0 / 5040.0,
-                                   1.0 / 720.0,     1.0 / 120.0,    1.0 / 24.0,    1.0 / 6.0};
 
 // ------------------------------------------------------------------ LDS ----
 struct NucLocal {
@@ -97,7 +99,8 @@ struct NucSmem {
             uint32_t cnt[kNucBins];
             double mass[kNucBins];
             uint64_t top[kMaxSlices * kTopMax];   // top-n merge (pass B finalize, wave 1)
-        } h;                              // histogram (pass B)
+        } h;                              // histogram (pass B finalize)
+        uint64_t pk[kNucBins];            // histogram (pass B): packed count and mass per bin
         uint64_t lkeys[kNucStage];        // the slice's selections (pass C), thread order
         NucFinC fc;                       // select finalize
         ExactSmem<kSliceThreads, kFbBins, kFbCap, kFbHistCap> ex;
@@ -697,7 +700,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         }
     }
     in.penalise(sm, P);   // (ends on a barrier when it used the LDS)
-    for (uint32_t b = tid; b < kNucBins; b += NT) { sm.u.h.cnt[b] = 0u; sm.u.h.mass[b] = 0.0; }
+    for (uint32_t b = tid; b < kNucBins; b += NT) sm.u.pk[b] = 0u;
     __syncthreads();
     if (sm.l.st_fallback) {   // resolved by the exact path
         wait_all_memory();
@@ -707,60 +710,89 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     const float sx = sm.l.st_sx;
     const bool use_mask = sm.l.st_use_mask != 0u;
     const float inv_t = fdiv(1.0f, P.temperature);
-    // Bin b holds sum exp(d), d = x + (b + 1/2) / sx, |d| <= 1 / (2 sx); the
-    // finalize scales it by exp(-(b + 1/2) / sx). exp(d) is a Taylor
-    // polynomial: degree 7 for sx >= 16 (|d| <= 1/32), degree 10 otherwise
-    // (sx >= 4, |d| <= 1/8), truncation below 5e-17 relative. Candidates past
-    // the grid (f > kNucBins: x < -128, weight below e^-128) count with no
-    // mass. A wave skips an element position none of its lanes holds a
-    // candidate at (sparse constraint masks).
-    const double inv_sx = 1.0 / (double)sx;
+    // Bin b holds sum exp(d), d = x + (b + 1/2) / sx = (r + 1/2) / sx with
+    // r = b - f in [-1, 0] (|d| <= 1 / (2 sx)); the finalize scales it by
+    // exp(-(b + 1/2) / sx). r is exact in float: b = floor(f) <= f <= b + 1
+    // (Sterbenz for b >= 1, r = -f for b = 0). exp(d) is the Taylor
+    // polynomial of degree n about 0 (n = 7 for sx >= 16, |d| <= 1/32; else
+    // n = 10, sx >= 4, |d| <= 1/8; truncation below 5e-17 relative) written
+    // as a polynomial in r: exp-Taylor_n(r/sx + c) = sum_j q_j r^j with
+    // c = 1/(2 sx) and q_j = sx^-j / j! * sum_{m <= n-j} c^m / m!.
+    //
+    // One LDS atomic per candidate carries its count and its mass: the word
+    // 2^50 + v, v = rint((exp(d) - 1) 2^k) as a two's complement integer,
+    // k = 36 + log2(sx) (the polynomial's coefficients carry the factor, and
+    // adding 1.5 * 2^52 rounds it to an integer in the low mantissa bits).
+    // |exp(d) - 1| <= e^(1/(2sx)) - 1, so over the slice's at most 8192
+    // candidates |sum v| < 2^48.1 and the count (<= 2^13) in
+    // bits 50-63 never meets it. The sums are integers, so the bins do not
+    // depend on the order of the atomics; v's rounding is at most 2^-(k+1),
+    // 2^-37 / sx relative to a candidate's weight (1.8e-12 at sx = 4), far
+    // under the plan's 1e-10 guard.
+    //
+    // Candidates past the grid (f > kNucBins, only when x_lo was floored at
+    // -128, so sx = 4 and x < -128) count in the last bin with r clamped to
+    // -1: mass below e^-128 each, also far under the guard. A wave skips an
+    // element position none of its lanes holds a candidate at (sparse
+    // constraint masks); a wave whose lanes hold only candidates tests none.
     const uint32_t cm = in.cand_bits(use_mask);
-    // Taylor coefficients 1/k! (k = 10 .. 3) from the scalar cache: each
-    // Horner step is one FMA with a scalar operand
-    double ck[8];
+    const bool all_cand = ballot(cm != 0xffffffffu) == 0u;
+    const double two_k = 68719476736.0 * (double)sx;   // 2^36 sx
+    auto fill = [&](auto deg, auto all) {
+        constexpr int n = decltype(deg)::value;
+        const double inv_sx = 1.0 / (double)sx, c = 0.5 * inv_sx;
+        double e[n + 1], q[n + 1];   // e[m] = sum_{1 <= i <= m} c^i / i!
+        double t = 1.0;
+        e[0] = 0.0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) ck[k] = scalar_load(&kInvFact[k]);
-    auto fill = [&](auto poly) {
+        for (int m = 1; m <= n; ++m) {
+            t = t * c / (double)m;
+            e[m] = e[m - 1] + t;
+        }
+        double aj = two_k;   // 2^k sx^-j / j!
+        q[0] = aj * e[n];    // (q_0 - 1) 2^k
 #pragma unroll
-        for (int q = 0; q < kSliceElems; ++q) {
-            if ((cm >> q) & 1u) {
-                const float x = tempered(in.v[q], maxl, inv_t);
+        for (int j = 1; j <= n; ++j) {
+            aj = aj * inv_sx / (double)j;
+            q[j] = aj * (1.0 + e[n - j]);
+        }
+#pragma unroll
+        for (int k = 0; k < kSliceElems; ++k) {
+            if (decltype(all)::value || ((cm >> k) & 1u)) {
+                const float x = tempered(in.v[k], maxl, inv_t);
                 const float f = nuc_f(x, sx);
-                const uint32_t b = nuc_bin(f);
-                const bool on = f <= (float)kNucBins;
-                const double d = on ? __builtin_fma((double)b + 0.5, inv_sx, (double)x) : 0.0;
-                const double pe = poly(d);
-                atomicAdd(&g_nuc.u.h.cnt[b], 1u);
-                atomicAdd(&g_nuc.u.h.mass[b], on ? pe : 0.0);
+                const float fb = fminf(__builtin_floorf(f), (float)(kNucBins - 1));
+                const double r = (double)fmaxf(fb - f, -1.0f);
+                double p = q[n];
+#pragma unroll
+                for (int j = n - 1; j >= 0; --j) p = __builtin_fma(p, r, q[j]);
+                const double y = p + 0x1.8p52;   // rint(p) + 1.5 * 2^52, exactly
+                const uint64_t w = (uint64_t)__double_as_longlong(y) + (kPkOne - kPkMagic);
+                atomicAdd(reinterpret_cast<unsigned long long*>(&g_nuc.u.pk[(uint32_t)fb]), (unsigned long long)w);
             }
         }
     };
+    using D7 = std::integral_constant<int, 7>;
+    using D10 = std::integral_constant<int, 10>;
+    using All = std::true_type;
+    using Some = std::false_type;
     if (sx >= 16.0f) {
-        fill([&](double d) {
-            double p = ck[3];
-#pragma unroll
-            for (int k = 4; k < 8; ++k) p = __builtin_fma(p, d, ck[k]);
-            p = __builtin_fma(p, d, 0.5);
-            p = __builtin_fma(p, d, 1.0);
-            return __builtin_fma(p, d, 1.0);
-        });
+        if (all_cand) fill(D7{}, All{});
+        else fill(D7{}, Some{});
     } else {
-        fill([&](double d) {
-            double p = ck[0];
-#pragma unroll
-            for (int k = 1; k < 8; ++k) p = __builtin_fma(p, d, ck[k]);
-            p = __builtin_fma(p, d, 0.5);
-            p = __builtin_fma(p, d, 1.0);
-            return __builtin_fma(p, d, 1.0);
-        });
+        if (all_cand) fill(D10{}, All{});
+        else fill(D10{}, Some{});
     }
     __syncthreads();
     uint32_t* gc = a.nh_cnt + ((uint64_t)wrow * kMaxSlices + slice) * kNucBins;
     double* gm = a.nh_mass + ((uint64_t)wrow * kMaxSlices + slice) * kNucBins;
+    const double inv_2k = 1.0 / two_k;
     for (uint32_t b = tid; b < kNucBins; b += NT) {
-        gc[b] = sm.u.h.cnt[b];
-        gm[b] = sm.u.h.mass[b];
+        const uint64_t w = sm.u.pk[b];
+        const uint32_t cnt = (uint32_t)((w + (kPkOne >> 1)) >> 50);
+        const int64_t v = (int64_t)(w - ((uint64_t)cnt << 50));
+        gc[b] = cnt;
+        gm[b] = (double)cnt + (double)v * inv_2k;
     }
 }
 
