@@ -254,7 +254,7 @@ int lcs_logprobs(lcs_ctx* ctx, const lcs_batch* batch, const int32_t* chosen, co
  * call hipMalloc (code under HIP graph capture, tight serving loops, harnesses
  * that forbid it). No counterpart in the reference. Runs on the current
  * device with the same batch, outputs and results as lcs_sample; its
- * workspace is one static device array per GPU (about 39 MiB, held until the
+ * workspace is one static device array per GPU (about 38 MiB, held until the
  * process ends), sized for rows <= 64, any vocabulary up to 262144, n_top <=
  * 20 and penalty windows up to 8192. More rows return LCS_ERR_CAPACITY with
  * nothing launched. Calls share that array: calls that overlap on one GPU

@@ -41,8 +41,7 @@ struct lcs_ctx {
     uint32_t cus = 0;               // compute units of the device (the lm-head's block shape)
     // nucleus path workspace (kNucRows rows at a time)
     lcs::NucRow* nrow = nullptr;
-    uint32_t* nh_cnt = nullptr;
-    double* nh_mass = nullptr;
+    uint64_t* nh_pk = nullptr;
     uint64_t* nlist = nullptr;
     // device-resident penalty windows (lcs_windows_reserve)
     uint32_t win_slots = 0, win_max = 0, win_h = 0;
@@ -156,8 +155,7 @@ lcs_ctx* lcs_create(int device, uint32_t max_rows, uint32_t max_vocab, uint32_t 
         (e = hipMalloc(&c->lmrecs, (size_t)max_rows * ((max_vocab + lcs::kLmColsMin - 1) / lcs::kLmColsMin) *
                                        sizeof(lcs::LmRec))) != hipSuccess ||
         (e = hipMalloc(&c->nrow, nuc_rows * sizeof(lcs::NucRow))) != hipSuccess ||
-        (e = hipMalloc(&c->nh_cnt, nh_elems * 4)) != hipSuccess ||
-        (e = hipMalloc(&c->nh_mass, nh_elems * 8)) != hipSuccess ||
+        (e = hipMalloc(&c->nh_pk, nh_elems * 8)) != hipSuccess ||
         (e = hipMalloc(&c->nlist, nuc_rows * lcs::kNucList * 8)) != hipSuccess ||
         (e = hipMalloc(&c->lp_params, (size_t)max_rows * sizeof(lcs_params))) != hipSuccess ||
         (e = hipMalloc(&c->lp_ids, (size_t)max_rows * 4)) != hipSuccess ||
@@ -180,8 +178,7 @@ void lcs_destroy(lcs_ctx* c) {
     (void)hipFree(c->d_ids);
     (void)hipFree(c->d_raw);
     (void)hipFree(c->nrow);
-    (void)hipFree(c->nh_cnt);
-    (void)hipFree(c->nh_mass);
+    (void)hipFree(c->nh_pk);
     (void)hipFree(c->nlist);
     (void)hipFree(c->d_pen);
     (void)hipFree(c->status);
@@ -321,8 +318,7 @@ int sample_impl(lcs_ctx* c, const lcs_batch* b, const lcs_out* o, void* stream, 
     // likewise for the nucleus kernels when every row takes that path
     a.all_nucleus = (b->params_host && !any_general && !any_slice) ? 1u : 0u;
     a.nrow = c->nrow;
-    a.nh_cnt = c->nh_cnt;
-    a.nh_mass = c->nh_mass;
+    a.nh_pk = c->nh_pk;
     a.nlist = c->nlist;
     a.win_slot = b->win_slot;
     a.win_push = b->win_push;
@@ -363,8 +359,7 @@ constexpr size_t kSzStatus = up(4);
 constexpr size_t kSzD = up((size_t)kNoAllocRows * kNoAllocHist * 4);
 constexpr size_t kSzNrow = up((size_t)kNoAllocRows * sizeof(lcs::NucRow));
 constexpr size_t kNhElems = (size_t)kNoAllocRows * lcs::kMaxSlices * lcs::kNucBins;
-constexpr size_t kSzNhCnt = up(kNhElems * 4);
-constexpr size_t kSzNhMass = up(kNhElems * 8);
+constexpr size_t kSzNhPk = up(kNhElems * 8);
 constexpr size_t kSzNlist = up((size_t)kNoAllocRows * lcs::kNucList * 8);
 constexpr size_t kOffRecs = 0;
 constexpr size_t kOffSrecs = kOffRecs + kSzRecs;
@@ -373,10 +368,9 @@ constexpr size_t kOffDIds = kOffStatus + kSzStatus;
 constexpr size_t kOffDRaw = kOffDIds + kSzD;
 constexpr size_t kOffDPen = kOffDRaw + kSzD;
 constexpr size_t kOffNrow = kOffDPen + kSzD;
-constexpr size_t kOffNhCnt = kOffNrow + kSzNrow;
-constexpr size_t kOffNhMass = kOffNhCnt + kSzNhCnt;
-constexpr size_t kOffNlist = kOffNhMass + kSzNhMass;
-constexpr size_t kScratchBytes = kOffNlist + kSzNlist;   // about 42 MiB
+constexpr size_t kOffNhPk = kOffNrow + kSzNrow;
+constexpr size_t kOffNlist = kOffNhPk + kSzNhPk;
+constexpr size_t kScratchBytes = kOffNlist + kSzNlist;   // 37.5 MiB
 static_assert(kScratchBytes <= (44u << 20), "the no-alloc workspace stays modest");
 
 constexpr int kMaxDevices = 64;
@@ -512,8 +506,7 @@ int lcs_sample_noalloc(const lcs_batch* b, const lcs_out* o, void* stream) {
     w.d_raw = reinterpret_cast<float*>(base + kOffDRaw);
     w.d_pen = reinterpret_cast<float*>(base + kOffDPen);
     w.nrow = reinterpret_cast<lcs::NucRow*>(base + kOffNrow);
-    w.nh_cnt = reinterpret_cast<uint32_t*>(base + kOffNhCnt);
-    w.nh_mass = reinterpret_cast<double*>(base + kOffNhMass);
+    w.nh_pk = reinterpret_cast<uint64_t*>(base + kOffNhPk);
     w.nlist = reinterpret_cast<uint64_t*>(base + kOffNlist);
     if (b && o && b->rows > kNoAllocRows) {
         g_create_error = "lcs_sample_noalloc: rows above " + std::to_string(kNoAllocRows);

@@ -175,8 +175,7 @@ struct SampleArgs {   // (at most 128 dwords: kernels stage it in LDS, two dword
     uint32_t nuc_row0;       // first row of this nucleus launch
     // nucleus path workspace, for rows nuc_row0 .. nuc_row0 + kNucRows - 1
     NucRow* nrow;            // kNucRows
-    uint32_t* nh_cnt;        // kNucRows x kMaxSlices x kNucBins
-    double* nh_mass;         // kNucRows x kMaxSlices x kNucBins
+    uint64_t* nh_pk;         // kNucRows x kMaxSlices x kNucBins packed bin words (count << 50 + mass)
     uint64_t* nlist;         // kNucRows x kNucList rank keys
     // device-resident penalty windows
     const int32_t* win_slot; // rows: slot, or -1 (NULL: none)

@@ -101,7 +101,7 @@ struct NucSmem {
             uint64_t top[kMaxSlices * kTopMax];   // top-n merge (pass B finalize, wave 1)
         } h;                              // histogram (pass B finalize)
         uint64_t pk[kNucBins];            // histogram (pass B): packed count and mass per bin
-        uint64_t lkeys[kNucStage];        // the slice's selections (pass C), thread order
+        uint64_t lkeys[kNucStage + kWave];   // the slice's selections (pass C: id << 32 | value bits), thread order; a spare slot per lane
         NucFinC fc;                       // select finalize
         ExactSmem<kSliceThreads, kFbBins, kFbCap, kFbHistCap> ex;
     } u;
@@ -746,14 +746,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         e[0] = 0.0;
 #pragma unroll
         for (int m = 1; m <= n; ++m) {
-            t = t * c / (double)m;
+            t = t * c * (1.0 / (double)m);   // (a constant after unrolling: no division)
             e[m] = e[m - 1] + t;
         }
         double aj = two_k;   // 2^k sx^-j / j!
         q[0] = aj * e[n];    // (q_0 - 1) 2^k
 #pragma unroll
         for (int j = 1; j <= n; ++j) {
-            aj = aj * inv_sx / (double)j;
+            aj = aj * inv_sx * (1.0 / (double)j);
             q[j] = aj * (1.0 + e[n - j]);
         }
 #pragma unroll
@@ -784,16 +784,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         else fill(D10{}, Some{});
     }
     __syncthreads();
-    uint32_t* gc = a.nh_cnt + ((uint64_t)wrow * kMaxSlices + slice) * kNucBins;
-    double* gm = a.nh_mass + ((uint64_t)wrow * kMaxSlices + slice) * kNucBins;
-    const double inv_2k = 1.0 / two_k;
-    for (uint32_t b = tid; b < kNucBins; b += NT) {
-        const uint64_t w = sm.u.pk[b];
-        const uint32_t cnt = (uint32_t)((w + (kPkOne >> 1)) >> 50);
-        const int64_t v = (int64_t)(w - ((uint64_t)cnt << 50));
-        gc[b] = cnt;
-        gm[b] = (double)cnt + (double)v * inv_2k;
-    }
+    uint64_t* gp = a.nh_pk + ((uint64_t)wrow * kMaxSlices + slice) * kNucBins;
+    for (uint32_t b = tid; b < kNucBins; b += NT) gp[b] = sm.u.pk[b];
 }
 
 // Pass B's histograms merged per row and the plan of bin ranges (one
@@ -820,26 +812,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void
     static_assert(kNucBins % NT == 0, "bins per thread");
     uint32_t c[BPT];
     double m[BPT];
-#pragma unroll
-    for (uint32_t k = 0; k < BPT; ++k) { c[k] = 0u; m[k] = 0.0; }
-    const uint32_t* rc = a.nh_cnt + (uint64_t)wrow * kMaxSlices * kNucBins;
-    const double* rm = a.nh_mass + (uint64_t)wrow * kMaxSlices * kNucBins;
     {
-        // slices in chunks of 20: a chunk's words are all issued before any is
-        // summed; sums run in slice order (deterministic)
+        // each slice's packed bin words (count << 50 plus the mass as an
+        // integer v, exp(d) - 1 in units of 2^-k, k = 36 + log2 sx) decoded
+        // and summed exactly as integers (|sum v| < 32 * 2^48.1); slices in
+        // chunks of 20, a chunk's words all issued before any is summed
+        const uint64_t* rp = a.nh_pk + (uint64_t)wrow * kMaxSlices * kNucBins;
+        int64_t vs[BPT];
+#pragma unroll
+        for (uint32_t k = 0; k < BPT; ++k) { c[k] = 0u; vs[k] = 0; }
         constexpr uint32_t CH = 20;
         for (uint32_t s0 = 0; s0 < S; s0 += CH) {
-            uint32_t cc[CH][BPT];
-            double mm[CH][BPT];
+            uint64_t ww[CH][BPT];
 #pragma unroll
             for (uint32_t i = 0; i < CH; ++i) {
                 const uint32_t ss = s0 + i < S ? s0 + i : s0;
 #pragma unroll
-                for (uint32_t k = 0; k < BPT; ++k) {
-                    const uint32_t b = tid * BPT + k;
-                    cc[i][k] = rc[(uint64_t)ss * kNucBins + b];
-                    mm[i][k] = rm[(uint64_t)ss * kNucBins + b];
-                }
+                for (uint32_t k = 0; k < BPT; ++k) ww[i][k] = rp[(uint64_t)ss * kNucBins + tid * BPT + k];
             }
 #pragma unroll
             for (uint32_t i = 0; i < CH; ++i) {
@@ -847,15 +836,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void
                 for (uint32_t k = 0; k < BPT; ++k) {
                     // (selects, not a branch: a branch would let the
                     // compiler sink each load into it, one round trip each)
-                    const bool in = s0 + i < S;
-                    c[k] += in ? cc[i][k] : 0u;
-                    m[k] += in ? mm[i][k] : 0.0;
+                    const uint64_t w = s0 + i < S ? ww[i][k] : 0u;
+                    const uint32_t n = (uint32_t)((w + (kPkOne >> 1)) >> 50);
+                    c[k] += n;
+                    vs[k] += (int64_t)(w - ((uint64_t)n << 50));
                 }
             }
         }
-    }
+        const double inv_2k = 1.0 / (68719476736.0 * (double)sx);
 #pragma unroll
-    for (uint32_t k = 0; k < BPT; ++k) m[k] *= exp_f64(-((double)(tid * BPT + k) + 0.5) * inv_sx);
+        for (uint32_t k = 0; k < BPT; ++k) {
+            m[k] = ((double)c[k] + (double)vs[k] * inv_2k) * exp_f64(-((double)(tid * BPT + k) + 0.5) * inv_sx);
+        }
+    }
     NPROF(row, 1);
     {
         uint32_t cs = 0;
@@ -1522,11 +1515,20 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     const uint32_t cm = in.cand_bits(use_mask);
     uint32_t sel = 0;
     if (iv) {
-        const float l0 = sm.l.piv[0], h0 = sm.l.piv[1], l1 = sm.l.piv[2], h1 = sm.l.piv[3];
+        // l <= p <= h exactly when clamping p to [l, h] leaves it unchanged;
+        // an empty interval (l > h) becomes [+inf, +inf], which no finite
+        // logit meets. Branch-free, with the flags shifted in from the top
+        // (a short-circuit test compiles to a chain of exec-mask operations
+        // per element).
+        const float INF = __builtin_huge_valf();
+        float l0 = sm.l.piv[0], h0 = sm.l.piv[1], l1 = sm.l.piv[2], h1 = sm.l.piv[3];
+        if (!(l0 <= h0)) l0 = h0 = INF;
+        if (!(l1 <= h1)) l1 = h1 = INF;
 #pragma unroll
-        for (int q = 0; q < kSliceElems; ++q) {
+        for (int q = kSliceElems - 1; q >= 0; --q) {
             const float p = in.v[q];
-            sel |= ((p >= l0 && p <= h0) || (p >= l1 && p <= h1)) ? 1u << q : 0u;
+            const bool hit = (__builtin_amdgcn_fmed3f(p, l0, h0) == p) | (__builtin_amdgcn_fmed3f(p, l1, h1) == p);
+            sel = (sel << 1) | (hit ? 1u : 0u);
         }
         sel &= cm;
     } else {
@@ -1555,13 +1557,18 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         tot += t;
     }
     const uint32_t pos0 = pos;
-    if (sel) {
+    if (ballot(sel != 0u)) {
+        // every lane stores (value bits, id) at every position, branch-free:
+        // a selection to its staged place, anything else to the lane's spare
+        // slot; a selection past the stage lands among the spare slots too
+        // (min with the spare index), which nothing reads
+        const uint32_t spare = kNucStage + (uint32_t)lane;
 #pragma unroll
         for (int q = 0; q < kSliceElems; ++q) {
-            if ((sel >> q) & 1u) {
-                if (pos < kNucStage) sm.u.lkeys[pos] = rank_key(in.v[q], in.eid(q));
-                ++pos;
-            }
+            const uint32_t bit = (sel >> q) & 1u;
+            const uint32_t dst = min(bit ? pos : 0xffffffffu, spare);
+            sm.u.lkeys[dst] = ((uint64_t)in.eid(q) << 32) | __float_as_uint(in.v[q]);
+            pos += bit;
         }
     }
     if (tid == 0) {
@@ -1573,7 +1580,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         const uint32_t n = min(tot, kNucStage);
         uint64_t* list = a.nlist + (uint64_t)wrow * kNucList;
         for (uint32_t i = tid; i < n; i += NT) {
-            if (base + i < kNucList) list[base + i] = sm.u.lkeys[i];
+            const uint64_t w = sm.u.lkeys[i];
+            if (base + i < kNucList) list[base + i] = rank_key(__uint_as_float((uint32_t)w), (uint32_t)(w >> 32));
         }
         if (pos > kNucStage) {
             uint32_t p = pos0;
