@@ -90,6 +90,7 @@ struct NucFinC {
     uint64_t gsorted[kGroupMax];
     double gw[kGroupMax];                 // weights in rank order
     uint64_t lkey[kNucKeyCache];          // the row's first compacted candidates (rank keys)
+    double bscale[kNucBins];              // exp(-(b + 1/2) / sx) per bin
 };
 struct NucSmem {
     union {
@@ -342,6 +343,32 @@ __device__ __forceinline__ uint32_t nuc_sub(float f, uint32_t b0, uint32_t b1) {
     const float s = fmul(f - (float)b0, (float)kNucSub / (float)(b1 - b0 + 1));
     const float c = fminf(s, (float)(kNucSub - 1));
     return c > 0.0f ? (uint32_t)c : 0u;
+}
+
+// exp(d) for d = (r + 1/2) / sx, r in [-1, 0], as sum_j q_j r^j: the
+// Taylor polynomial of exp about 0 of degree n (truncation below 5e-17
+// relative for n = 7 and sx >= 16, |d| <= 1/32, or n = 10 and sx >= 4,
+// |d| <= 1/8) re-expanded in r, q_j = sx^-j / j! * sum_{m <= n-j} c^m / m!
+// with c = 1/(2 sx); every q_j times `scale`, and q_0 without its leading
+// 1 when `minus_one` (the polynomial of exp(d) - 1).
+template <int n>
+__device__ __forceinline__ void nuc_taylor(float sx, double scale, bool minus_one, double (&q)[n + 1]) {
+    const double inv_sx = 1.0 / (double)sx, c = 0.5 * inv_sx;
+    double e[n + 1];   // e[m] = sum_{1 <= i <= m} c^i / i!
+    double t = 1.0;
+    e[0] = 0.0;
+#pragma unroll
+    for (int m = 1; m <= n; ++m) {
+        t = t * c * (1.0 / (double)m);   // (a constant after unrolling: no division)
+        e[m] = e[m - 1] + t;
+    }
+    double aj = scale;   // scale sx^-j / j!
+    q[0] = aj * (minus_one ? e[n] : 1.0 + e[n]);
+#pragma unroll
+    for (int j = 1; j <= n; ++j) {
+        aj = aj * inv_sx * (1.0 / (double)j);
+        q[j] = aj * (1.0 + e[n - j]);
+    }
 }
 
 // Row and mode of a finalize workgroup (one per row of the launch); false
@@ -713,11 +740,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     // Bin b holds sum exp(d), d = x + (b + 1/2) / sx = (r + 1/2) / sx with
     // r = b - f in [-1, 0] (|d| <= 1 / (2 sx)); the finalize scales it by
     // exp(-(b + 1/2) / sx). r is exact in float: b = floor(f) <= f <= b + 1
-    // (Sterbenz for b >= 1, r = -f for b = 0). exp(d) is the Taylor
-    // polynomial of degree n about 0 (n = 7 for sx >= 16, |d| <= 1/32; else
-    // n = 10, sx >= 4, |d| <= 1/8; truncation below 5e-17 relative) written
-    // as a polynomial in r: exp-Taylor_n(r/sx + c) = sum_j q_j r^j with
-    // c = 1/(2 sx) and q_j = sx^-j / j! * sum_{m <= n-j} c^m / m!.
+    // (Sterbenz for b >= 1, r = -f for b = 0). exp(d) is nuc_taylor's
+    // polynomial in r, degree 7 for sx >= 16, else 10.
     //
     // One LDS atomic per candidate carries its count and its mass: the word
     // 2^50 + v, v = rint((exp(d) - 1) 2^k) as a two's complement integer,
@@ -740,22 +764,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     const double two_k = 68719476736.0 * (double)sx;   // 2^36 sx
     auto fill = [&](auto deg, auto all) {
         constexpr int n = decltype(deg)::value;
-        const double inv_sx = 1.0 / (double)sx, c = 0.5 * inv_sx;
-        double e[n + 1], q[n + 1];   // e[m] = sum_{1 <= i <= m} c^i / i!
-        double t = 1.0;
-        e[0] = 0.0;
-#pragma unroll
-        for (int m = 1; m <= n; ++m) {
-            t = t * c * (1.0 / (double)m);   // (a constant after unrolling: no division)
-            e[m] = e[m - 1] + t;
-        }
-        double aj = two_k;   // 2^k sx^-j / j!
-        q[0] = aj * e[n];    // (q_0 - 1) 2^k
-#pragma unroll
-        for (int j = 1; j <= n; ++j) {
-            aj = aj * inv_sx * (1.0 / (double)j);
-            q[j] = aj * (1.0 + e[n - j]);
-        }
+        double q[n + 1];   // (exp(d) - 1) 2^k
+        nuc_taylor<n>(sx, two_k, true, q);
 #pragma unroll
         for (int k = 0; k < kSliceElems; ++k) {
             if (decltype(all)::value || ((cm >> k) & 1u)) {
@@ -1033,10 +1043,14 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     const double Stot = nr->S;
     const uint32_t ncand = nr->n_cand;
     NPROF(row, 8);
-    // sub-bin tables
+    // sub-bin tables, bin scales
     for (uint32_t i = tid; i < kNucRanges * kNucSub; i += NT) {
         sm.u.fc.scnt[i / kNucSub][i % kNucSub] = 0u;
         sm.u.fc.smass[i / kNucSub][i % kNucSub] = 0.0;
+    }
+    {
+        const double inv_sx = 1.0 / (double)sx;
+        for (uint32_t b = tid; b < kNucBins; b += NT) sm.u.fc.bscale[b] = exp_f64(-((double)b + 0.5) * inv_sx);
     }
     if (tid == 0) {
         sm.l.out_flag = n_all > kNucList ? 1u : 0u;
@@ -1054,10 +1068,11 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
     __syncthreads();
     const NucRange* rgl = sm.l.rgl;   // (rg in registers for the hot loops, rgl for computed indices)
     // range and sub-bin of a compacted candidate; its weight as the reference's
-    auto locate = [&](uint64_t key, uint32_t& k, uint32_t& s) -> float {
+    auto locate = [&](uint64_t key, uint32_t& k, uint32_t& s, uint32_t& b, float& r) -> float {
         const float x = tempered(rank_val(key), maxl, inv_t);
         const float f = nuc_f(x, sx);
-        const uint32_t b = nuc_bin(f);
+        b = nuc_bin(f);
+        r = fmaxf((float)b - f, -1.0f);   // exact on the grid (f <= kNucBins)
         k = kNucRanges;
         s = 0u;
 #pragma unroll
@@ -1087,14 +1102,38 @@ __device__ __attribute__((noinline)) void nuc_select_fin(uint32_t row, bool exac
         }
     }
     __syncthreads();
-    for (uint32_t i = tid; i < n; i += NT) {
-        uint32_t k, s;
-        const uint64_t key = i < kNucKeyCache ? sm.u.fc.lkey[i] : list[i];
-        const float x = locate(key, k, s);
-        g_code[i] = k < kNucRanges ? (uint16_t)(k * kNucSub + s) : kNoCode;
-        if (k < kNucRanges) {
-            atomicAdd(&sm.u.fc.scnt[k][s], 1u);
-            atomicAdd(&sm.u.fc.smass[k][s], exp_f64((double)x));
+    // a candidate's weight for the sub-bin masses: exp(-(b + 1/2) / sx) of
+    // its bin times nuc_taylor's polynomial in its remainder (within a few
+    // ulp of exp(x); the decisive groups' walks below use exp_f64 itself);
+    // candidates past the grid (weight below e^-128) count with at most that
+    double q[11];
+    nuc_taylor<10>(sx, 1.0, false, q);
+    // keys past the LDS cache come from the list in batches of PB per
+    // thread, every load of a batch issued before the first is used
+    constexpr uint32_t PB = 8;
+    for (uint32_t i0 = tid; i0 < n; i0 += PB * NT) {
+        uint64_t kb[PB];
+#pragma unroll
+        for (uint32_t j = 0; j < PB; ++j) {
+            const uint32_t i = i0 + j * NT;
+            kb[j] = i < kNucKeyCache ? sm.u.fc.lkey[i] : list[i < n ? i : 0u];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < PB; ++j) {
+            const uint32_t i = i0 + j * NT;
+            if (i < n) {
+                uint32_t k, s, b;
+                float r;
+                (void)locate(kb[j], k, s, b, r);
+                g_code[i] = k < kNucRanges ? (uint16_t)(k * kNucSub + s) : kNoCode;
+                if (k < kNucRanges) {
+                    double p = q[10];
+#pragma unroll
+                    for (int t = 9; t >= 0; --t) p = __builtin_fma(p, (double)r, q[t]);
+                    atomicAdd(&sm.u.fc.scnt[k][s], 1u);
+                    atomicAdd(&sm.u.fc.smass[k][s], sm.u.fc.bscale[b] * p);
+                }
+            }
         }
     }
     __syncthreads();
