@@ -346,9 +346,9 @@ __device__ __forceinline__ uint32_t nuc_sub(float f, uint32_t b0, uint32_t b1) {
 }
 
 // exp(d) for d = (r + 1/2) / sx, r in [-1, 0], as sum_j q_j r^j: the
-// Taylor polynomial of exp about 0 of degree n (truncation below 5e-17
-// relative for n = 7 and sx >= 16, |d| <= 1/32, or n = 10 and sx >= 4,
-// |d| <= 1/8) re-expanded in r, q_j = sx^-j / j! * sum_{m <= n-j} c^m / m!
+// Taylor polynomial of exp about 0 of degree n (relative truncation below
+// (1/(2 sx))^(n+1) / (n+1)! * e^(1/(2 sx)); 5e-17 for n = 10 and sx >= 4)
+// re-expanded in r, q_j = sx^-j / j! * sum_{m <= n-j} c^m / m!
 // with c = 1/(2 sx); every q_j times `scale`, and q_0 without its leading
 // 1 when `minus_one` (the polynomial of exp(d) - 1).
 template <int n>
@@ -741,7 +741,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     // r = b - f in [-1, 0] (|d| <= 1 / (2 sx)); the finalize scales it by
     // exp(-(b + 1/2) / sx). r is exact in float: b = floor(f) <= f <= b + 1
     // (Sterbenz for b >= 1, r = -f for b = 0). exp(d) is nuc_taylor's
-    // polynomial in r, degree 7 for sx >= 16, else 10.
+    // polynomial in r, of degree 5 for sx >= 64, 6 for sx >= 16, else 8:
+    // truncation below 3.2e-16, 5.8e-15 and 2.1e-14 relative, each under a
+    // thirtieth of the mass's rounding below.
     //
     // One LDS atomic per candidate carries its count and its mass: the word
     // 2^50 + v, v = rint((exp(d) - 1) 2^k) as a two's complement integer,
@@ -764,6 +766,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     const double two_k = 68719476736.0 * (double)sx;   // 2^36 sx
     auto fill = [&](auto deg, auto all) {
         constexpr int n = decltype(deg)::value;
+        constexpr bool off_grid = n == 8;   // (only when sx = 4: f may pass kNucBins)
         double q[n + 1];   // (exp(d) - 1) 2^k
         nuc_taylor<n>(sx, two_k, true, q);
 #pragma unroll
@@ -772,7 +775,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
                 const float x = tempered(in.v[k], maxl, inv_t);
                 const float f = nuc_f(x, sx);
                 const float fb = fminf(__builtin_floorf(f), (float)(kNucBins - 1));
-                const double r = (double)fmaxf(fb - f, -1.0f);
+                const double r = (double)(off_grid ? fmaxf(fb - f, -1.0f) : fb - f);
                 double p = q[n];
 #pragma unroll
                 for (int j = n - 1; j >= 0; --j) p = __builtin_fma(p, r, q[j]);
@@ -782,16 +785,20 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
             }
         }
     };
-    using D7 = std::integral_constant<int, 7>;
-    using D10 = std::integral_constant<int, 10>;
+    using D5 = std::integral_constant<int, 5>;
+    using D6 = std::integral_constant<int, 6>;
+    using D8 = std::integral_constant<int, 8>;
     using All = std::true_type;
     using Some = std::false_type;
-    if (sx >= 16.0f) {
-        if (all_cand) fill(D7{}, All{});
-        else fill(D7{}, Some{});
+    if (sx >= 64.0f) {
+        if (all_cand) fill(D5{}, All{});
+        else fill(D5{}, Some{});
+    } else if (sx >= 16.0f) {
+        if (all_cand) fill(D6{}, All{});
+        else fill(D6{}, Some{});
     } else {
-        if (all_cand) fill(D10{}, All{});
-        else fill(D10{}, Some{});
+        if (all_cand) fill(D8{}, All{});
+        else fill(D8{}, Some{});
     }
     __syncthreads();
     uint64_t* gp = a.nh_pk + ((uint64_t)wrow * kMaxSlices + slice) * kNucBins;
