@@ -87,7 +87,6 @@ __host__ __device__ inline uint32_t row_mode(const lcs_params& p, bool masked, u
 constexpr uint32_t kNucBins = 512;      // histogram bins over the tempered offset
 constexpr uint32_t kNucRows = 256;      // rows per nucleus launch (workspace rows)
 constexpr uint32_t kNucList = 32768;    // candidates the select pass compacts per row (HBM)
-constexpr uint32_t kNucStage = 4096;    // a slice's selections staged in LDS for coalesced stores
 constexpr uint32_t kNucRanges = 4;      // bin ranges a row's decisions can need
 constexpr uint32_t kNucSub = 128;       // sub-bins per range in the select pass
 constexpr float kNucXFloor = -128.0f;   // offsets below collapse into the last bin

@@ -94,7 +94,7 @@ struct NucFinC {
 };
 struct NucSmem {
     union {
-        uint32_t ovr[kSliceMax];          // penalty words per slice position
+        uint32_t ovr[kSliceMax];          // penalty words per slice position; the slice's values (pass C)
         uint4 ovr4[kSliceMax / 4];
         struct {
             uint32_t cnt[kNucBins];
@@ -102,7 +102,6 @@ struct NucSmem {
             uint64_t top[kMaxSlices * kTopMax];   // top-n merge (pass B finalize, wave 1)
         } h;                              // histogram (pass B finalize)
         uint64_t pk[kNucBins];            // histogram (pass B): packed count and mass per bin
-        uint64_t lkeys[kNucStage + kWave];   // the slice's selections (pass C: id << 32 | value bits), thread order; a spare slot per lane
         NucFinC fc;                       // select finalize
         ExactSmem<kSliceThreads, kFbBins, kFbCap, kFbHistCap> ex;
     } u;
@@ -1586,11 +1585,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
             }
         }
     }
-    // the workgroup's selections in thread order (one block scan) staged in
-    // LDS, one reservation in the row list, coalesced stores; selections past
-    // the LDS stage (rare) go to the list directly; positions past kNucList
-    // are dropped (the finalize then sees list_n > kNucList and takes the
-    // exact path)
+    // One reservation in the row's list for the workgroup's selections (a
+    // block scan of the per-thread counts places each thread's run), then
+    // each lane writes its own: the slice's values go to LDS in slice order
+    // (where a lane reads its selected element q at a computed address, as a
+    // register cannot be indexed per lane), and a loop over the lane's set
+    // bits, as long as the wave's longest run, stores (value, id) rank keys.
+    // Positions past kNucList are dropped (the finalize then sees list_n >
+    // kNucList and takes the exact path).
     const uint32_t cnt = (uint32_t)__popc(sel);
     const uint32_t incl = wave_scan_incl_u(cnt);
     if (lane == kWave - 1) sm.l.nall[wv] = incl;
@@ -1602,42 +1604,25 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         pos += k < wv ? t : 0u;
         tot += t;
     }
-    const uint32_t pos0 = pos;
-    if (ballot(sel != 0u)) {
-        // every lane stores (value bits, id) at every position, branch-free:
-        // a selection to its staged place, anything else to the lane's spare
-        // slot; a selection past the stage lands among the spare slots too
-        // (min with the spare index), which nothing reads
-        const uint32_t spare = kNucStage + (uint32_t)lane;
-#pragma unroll
-        for (int q = 0; q < kSliceElems; ++q) {
-            const uint32_t bit = (sel >> q) & 1u;
-            const uint32_t dst = min(bit ? pos : 0xffffffffu, spare);
-            sm.u.lkeys[dst] = ((uint64_t)in.eid(q) << 32) | __float_as_uint(in.v[q]);
-            pos += bit;
-        }
-    }
     if (tid == 0) {
         sm.l.gbase = tot ? __hip_atomic_fetch_add(&nr->list_n, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
     }
-    __syncthreads();
-    {
-        const uint32_t base = sm.l.gbase;
-        const uint32_t n = min(tot, kNucStage);
-        uint64_t* list = a.nlist + (uint64_t)wrow * kNucList;
-        for (uint32_t i = tid; i < n; i += NT) {
-            const uint64_t w = sm.u.lkeys[i];
-            if (base + i < kNucList) list[base + i] = rank_key(__uint_as_float((uint32_t)w), (uint32_t)(w >> 32));
-        }
-        if (pos > kNucStage) {
-            uint32_t p = pos0;
+    const bool wave_sel = ballot(sel != 0u) != 0u;
+    if (wave_sel) {
 #pragma unroll
-            for (int q = 0; q < kSliceElems; ++q) {
-                if ((sel >> q) & 1u) {
-                    if (p >= kNucStage && base + p < kNucList) list[base + p] = rank_key(in.v[q], in.eid(q));
-                    ++p;
-                }
-            }
+        for (int q = 0; q < kSliceElems; ++q) sm.u.ovr[in.eid(q) - in.lo] = __float_as_uint(in.v[q]);
+    }
+    __syncthreads();
+    if (wave_sel) {
+        const uint32_t base = sm.l.gbase;
+        uint64_t* list = a.nlist + (uint64_t)wrow * kNucList;
+        uint32_t rest = sel;
+        while (rest) {
+            const int q = __builtin_ctz(rest);
+            rest &= rest - 1u;
+            const uint32_t off = ((uint32_t)(q / G) * NT + tid) * G + (uint32_t)(q % G);   // in.eid(q) - in.lo
+            if (base + pos < kNucList) list[base + pos] = rank_key(__uint_as_float(sm.u.ovr[off]), in.lo + off);
+            ++pos;
         }
     }
     }
