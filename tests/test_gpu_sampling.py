@@ -424,6 +424,56 @@ def test_nucleus_rows(sampler):
     compare(w32, run(sampler, wb), O.sample_batch(w32, threads=16), "nucleus-bf16", expect_paths={4, 6})
 
 
+def test_nucleus_histogram_extremes(sampler):
+    """Nucleus rows at the limits of the histogram pass's packed bin words
+    (count in bits 50-63, mass as an integer below 2^48.1 per slice): every
+    candidate of a full 8192-logit slice in one bin (all logits equal, also
+    masked and bf16; one such slice in a row of distinct values, its bin
+    carrying 4% of the mass below the decisions), two values only, the widest bin scale (candidates within
+    1e-3 of the max: sx = 2^19), the narrowest (a candidate 1000 below the max:
+    x_lo floored at -128, sx = 4, off-grid candidates) and a temperature that
+    spreads the row over all 512 bins. The tied rows' decisive groups exceed
+    what the finalize ranks, so they finish on the exact path after the
+    histogram pass has binned them."""
+    V = 3 * 8192 + 5
+    rows = 8
+    g = np.random.default_rng(47)
+    logits = np.empty((rows, V), dtype=np.float32)
+    logits[0] = 0.25                                     # all equal
+    logits[1] = np.where(g.random(V) < 0.5, 0.0, -1.0)   # two values
+    logits[2] = g.random(V) * 1e-3                       # within 1e-3: sx = 2^19
+    logits[3] = g.standard_normal(V)
+    logits[3, g.integers(0, V, 7)] = -1000.0             # x_lo floored: sx = 4, off-grid candidates
+    logits[4] = g.standard_normal(V) * 8.0               # wide spread at T = 0.25
+    logits[5] = 0.25                                     # all equal, masked to two full slices
+    logits[6] = g.standard_normal(V)
+    logits[7] = g.standard_normal(V)                     # one full slice in one bin, 4% of the mass,
+    logits[7, 8192:2 * 8192] = -2.0                      # below the decisions
+    p = W.default_params(rows)
+    p["temperature"][:] = [1.0, 1.0, 0.8, 1.2, 0.25, 1.0, 1.5, 0.7]
+    p["top_p"][:] = [0.9, 0.7, 0.95, 0.5, 0.99, 0.6, 0.98, 0.95]
+    bits = np.ones((rows, V), dtype=bool)
+    bits[5, 2 * 8192:] = False
+    has = np.zeros(rows, dtype=np.uint8)
+    has[5] = 1
+    seeds = np.array([W.row_seed(4747, r) for r in range(rows)], dtype=np.uint64)
+    u = W.uniforms(seeds)
+    w = W.Workload("nucleus-extremes", rows, V, "f32", logits, p, seeds, u, mask=W.pack_mask(bits),
+                   n_top=2, want_logprobs=True)
+    gg = run(sampler, w, has_mask=sampler.torch.from_numpy(has).cuda())
+    compare(w, gg, O.sample_batch(w, threads=16, has_mask=has), "nucleus-extremes", expect_paths={4, 6})
+    # (rows of equal logits have decisive groups far above 256 candidates and
+    # finish on the exact path; the others decide on the nucleus path)
+    assert (gg["diag"]["path"][[2, 3, 4, 6, 7]] == 6).all(), gg["diag"]["path"].tolist()
+    b16 = W.bf16_rne(logits)
+    wb = W.Workload("nucleus-extremes-bf16", rows, V, "bf16", b16, p, seeds, u, mask=W.pack_mask(bits),
+                    n_top=2, want_logprobs=True)
+    w32 = W.Workload("nucleus-extremes-bf16-as-f32", rows, V, "f32", W.bf16_to_f32(b16), p, seeds, u,
+                     mask=W.pack_mask(bits), n_top=2, want_logprobs=True)
+    compare(w32, run(sampler, wb, has_mask=sampler.torch.from_numpy(has).cuda()),
+            O.sample_batch(w32, threads=16, has_mask=has), "nucleus-extremes-bf16", expect_paths={4, 6})
+
+
 def _all_paths_workload(V, seed, dtype="f32"):
     """Nine rows over vocab V, one per row path and filter mix: greedy (also
     masked), min-p window, sliced top-k, nucleus (top-p, masked, plain
