@@ -147,7 +147,8 @@ struct SliceIn {
     bool hany, htwo;
     uint32_t hoff, hstart, nwin_h;
     uint4 raw[NG];
-    uint32_t mbits;    // bit q: element q allowed (load_mask)
+    uint32_t mbits;    // bit q: element q allowed (finish_mask)
+    uint32_t mw[NG];   // the mask words as loaded (load_mask)
     uint32_t hA[HC], hB[HC];
     uint32_t oA, oB;
     float rA[HC], rB[HC];
@@ -208,19 +209,26 @@ struct SliceIn {
             dst[j] = load16(rp, (e0 < h0 ? e0 : l0) / G);
         }
     }
-    // the thread's 32 mask bits (bit q for element q), where the row is masked
+    // the thread's 32 mask bits (bit q for element q), where the row is
+    // masked: load_mask issues the loads, finish_mask (before the first use
+    // of mbits) combines them, so that the work between waits for neither
     __device__ __forceinline__ void load_mask() {
         if (!mrow) return;
-        uint32_t w[NG];
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            const uint32_t e0 = lo + (j * NT + tid_x()) * G;
+            mw[j] = mrow[(e0 < hi ? e0 : lo) >> 5];
+        }
+    }
+    __device__ __forceinline__ void finish_mask() {
+        if (!mrow) return;
+        uint32_t m = 0;
 #pragma unroll
         for (int j = 0; j < NG; ++j) {
             const uint32_t e0 = lo + (j * NT + tid_x()) * G;
             const uint32_t ee = e0 < hi ? e0 : lo;
-            w[j] = mrow[ee >> 5] >> (ee & 31u);
+            m |= ((mw[j] >> (ee & 31u)) & ((1u << G) - 1u)) << (j * G);
         }
-        uint32_t m = 0;
-#pragma unroll
-        for (int j = 0; j < NG; ++j) m |= (w[j] & ((1u << G) - 1u)) << (j * G);
         mbits = m;
     }
     __device__ __forceinline__ void clear(NucSmem& sm) const {
@@ -505,6 +513,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         }
     }
     if (in.hany) in.apply(sm);
+    in.finish_mask();
     // penalised candidate statistics over all ids and over the allowed ids
     {
         float bv = NEG, mv = NEG, nb = __builtin_huge_valf(), nm = __builtin_huge_valf();
@@ -760,6 +769,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     // -1: mass below e^-128 each, also far under the guard. A wave skips an
     // element position none of its lanes holds a candidate at (sparse
     // constraint masks); a wave whose lanes hold only candidates tests none.
+    if (masked) in.finish_mask();
     const uint32_t cm = in.cand_bits(use_mask);
     const bool all_cand = ballot(cm != 0xffffffffu) == 0u;
     const double two_k = 68719476736.0 * (double)sx;   // 2^36 sx
@@ -1501,7 +1511,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
     SliceIn<G> in;
     in.start(a, row, slice, P, masked, early ? pre : nullptr);
     if (use_mask) in.load_mask();   // (its loads arrive with the logits')
-    in.penalise(sm, P);
     const float inv_t = fdiv(1.0f, P.temperature);
     // A logit's bin b(p) = nuc_bin(nuc_f(tempered(p))) is non-increasing in
     // p (each step is monotone), so a range of bins [b0, b1] is an interval
@@ -1520,7 +1529,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         const bool up = ((uint32_t)wv & 1u) != 0u;
         float bound = up ? -__builtin_huge_valf() : __builtin_huge_valf();   // empty
         if (r < nrg) {   // (uniform in the wave)
-            const uint32_t b0 = nr->r[r].b0, b1 = nr->r[r].b1;
+            // (scalar loads: a wait for them leaves the slice's logit loads in flight)
+            const uint32_t ru = __builtin_amdgcn_readfirstlane(r);
+            const uint32_t b0 = scalar_load(&nr->r[ru].b0), b1 = scalar_load(&nr->r[ru].b1);
             // pred(k): phi search: bin >= b0 (true from -inf up); plo search:
             // bin > b1 (true from -inf up to just below plo)
             auto pred = [&](uint32_t k) {
@@ -1529,15 +1540,15 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
             };
             constexpr uint32_t kMinus = 0x007fffffu, kPlus = 0xff800000u;   // keys of -inf, +inf
             // invariant: pred(lo) holds or lo = kMinus - 1; pred(hi) fails or hi = kPlus + 1
-            uint64_t lo = up ? kMinus : (uint64_t)kMinus - 1u, hi = (uint64_t)kPlus + 1u;
+            // (32 bits suffice: every probe and bound stays below hi + 64 <= 0xff800041)
+            uint32_t lo = up ? kMinus : kMinus - 1u, hi = kPlus + 1u;
             while (hi - lo > 1u) {   // (uniform)
-                const uint64_t step = (hi - lo + 63u) / 64u;
-                const uint64_t k = lo + ((uint64_t)lane + 1u) * step;
-                const bool t = k < hi && pred((uint32_t)k);
+                const uint32_t step = (hi - lo + 63u) / 64u;
+                const uint32_t k = lo + ((uint32_t)lane + 1u) * step;
+                const bool t = k < hi && pred(k);
                 const uint32_t nt = (uint32_t)__builtin_popcountll(ballot(t));
-                const uint64_t nlo = lo + (uint64_t)nt * step;
-                const uint64_t nhi = lo + ((uint64_t)nt + 1u) * step;
-                lo = nlo;
+                const uint32_t nhi = lo + (nt + 1u) * step;
+                lo = lo + nt * step;
                 hi = nhi < hi ? nhi : hi;
             }
             // phi: the greatest key with bin >= b0; plo: the least with bin <= b1
@@ -1555,8 +1566,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void nu
         }
         sm.l.bmap[tid] = w;
     }
+    // (the searches above need no logit: they run while the loads arrive)
+    in.penalise(sm, P);
     __syncthreads();
     // bit q: element q is a candidate inside a planned range
+    if (use_mask) in.finish_mask();
     const uint32_t cm = in.cand_bits(use_mask);
     uint32_t sel = 0;
     if (iv) {
