@@ -18,8 +18,9 @@
 //                  the top-n logprobs.
 //   B  nuc_hist:   the reference's weights exp((double)((p - maxl) * inv_t))
 //                  (sampling.cpp:101-109) binned by the tempered offset into
-//                  kNucBins bins (counts, f64 masses). The row's finalize
-//                  merges the row's histograms and plans the few bin ranges
+//                  kNucBins bins (count and mass packed in one integer
+//                  word per bin, so sums are exact in any order). The row's
+//                  finalize merges the row's histograms and plans the few bin ranges
 //                  that can hold the top-p crossing, the min-p cut and the
 //                  draw (sampling.cpp:113-147).
 //   C  nuc_select: the candidates of those ranges are compacted into a row
@@ -32,8 +33,9 @@
 //
 // Bin-level decisions carry a 1e-10 relative guard (a target that close to
 // a bin or sub-bin edge takes both neighbours). A plan that would compact
-// more than kNucList candidates, or a decisive sub-bin group larger than
-// one wave can rank, resolves the row with the exact single-workgroup path.
+// more than kNucList candidates, or a decisive sub-bin group larger than the
+// kGroupMax (256) the workgroup ranks at once, resolves the row with the
+// exact single-workgroup path.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
