@@ -405,6 +405,25 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t& e
     return total;
 }
 
+// Inclusive prefix sum of one double per thread (wave scans, then the waves'
+// totals in wave order); returns the block total.
+template <int NT>
+__device__ __forceinline__ double block_scan_incl(double v, double& incl, double* red) {
+    const int lane = tid_x() & 63, w = tid_x() / kWave;
+    const double inc = wave_scan_incl(v);
+    if (lane == 63) red[w] = inc;
+    __syncthreads();
+    double base = 0.0, total = 0.0;
+#pragma unroll
+    for (int k = 0; k < NT / kWave; ++k) {
+        if (k < w) base += red[k];
+        total += red[k];
+    }
+    __syncthreads();
+    incl = base + inc;
+    return total;
+}
+
 // ------------------------------------------------ LDS bitonic sort (u64) ----
 // Ascending sort of n (a power of two) keys in LDS by NT threads.
 template <int NT>

@@ -234,6 +234,7 @@ struct ExactSeg {
     double mb;           // exact mass before the region
 };
 constexpr uint32_t kSubBins = 256;
+constexpr uint32_t kIdFilterWords = kMaxVocab / 8 / 32;   // one bit per 8 ids
 
 template <int NT, uint32_t NB, uint32_t CAP, uint32_t DCAP>
 struct ExactSmem {
@@ -257,16 +258,14 @@ struct ExactSmem {
     unsigned long long sub_lo[kSubBins];
     uint32_t sub_hi[kSubBins];
     uint64_t red64[NT / kWave];
+    uint32_t idf[kIdFilterWords];   // bit k: some penalised id lies in [8k, 8k + 8)
+    uint32_t wbins[NB / 32];        // bins a compaction pass wants
     ExactSeg bc_seg;
     uint32_t nlist;
     uint32_t mp_count;
     uint32_t flag;
     uint32_t bincap;   // thread 0: a selection bin overflowed, so the row's id is -1
-    int32_t out_id;
-    uint32_t out_keep;
-    float out_boundary;
-    double out_kept_sum;
-    double out_S;
+    double walk_at;    // the running value where a parallel walk stopped
     SampleArgs args;   // the launch arguments, for the out-of-line call (no private copy)
 };
 
@@ -340,6 +339,8 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
     float* d_pen = a.d_pen + (uint64_t)row * a.max_hist;
 
     if (tid == 0) sm.bincap = 0u;   // (thread 0 alone writes and reads it)
+    for (uint32_t k = tid; k < kIdFilterWords; k += NT) sm.idf[k] = 0u;
+    __syncthreads();
 
     // ---- P0: distinct penalised ids of the window (apply_penalties) ----
     uint32_t nD = 0;
@@ -386,6 +387,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
                     if (sm.u.dsort[mid] <= d) lo = mid + 1; else hi = mid;
                 }
                 const float raw = load_elem(rowp, a.dtype, d);
+                atomicOr(&sm.idf[d >> 8], 1u << ((d >> 3) & 31u));
                 d_ids[base] = d;
                 d_raw[base] = raw;
                 d_pen[base] = penalize(raw, lo - i, P);
@@ -394,6 +396,12 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
             __syncthreads();
         }
     }
+
+    // a penalised id: the LDS filter first (most ids are not), then a binary
+    // search of the sorted list in global memory
+    auto is_pen = [&](uint32_t e) -> bool {
+        return ((sm.idf[e >> 8] >> ((e >> 3) & 31u)) & 1u) && d_find(d_ids, nD, e) >= 0;
+    };
 
     // ---- P1: raw stats, logsumexp, top-n, candidate max/min ----
     float rmax = -kInfF, cmax = -kInfF, rmin = kInfF, cmin = kInfF;
@@ -484,7 +492,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
                 for (uint32_t k = 0; k < nv; ++k) {
                     const uint32_t e = e0 + k;
                     if (((mw >> k) & 1u) && (nmi == kNoIdx || vi_better(v[k], e, nm, nmi)) &&
-                        d_find(d_ids, nD, e) < 0) {
+                        !is_pen(e)) {
                         nm = v[k];
                         nmi = e;
                     }
@@ -535,10 +543,40 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
             f = fminf(f, (float)(NB - 1));
             return f > 0.0f ? (uint32_t)f : 0u;
         };
-        auto weight = [&](float p) -> double { return exp((double)tempered(p, maxl, inv_t)); };
+        // (exp_f64: the inline f64 exponential of the other paths, within 1
+        // ulp of libm's)
+        auto weight = [&](float p) -> double { return exp_f64((double)tempered(p, maxl, inv_t)); };
         auto quant = [](double w) -> unsigned long long {
             return (unsigned long long)__double2ull_rn(w * kTwo63);
         };
+        // The reference's sequential walks (sampling.cpp:113-147), by the
+        // whole workgroup NT items at a time: the first item i < n whose
+        // running value base + sum_{j <= i} val(j) satisfies hit(i, running),
+        // or n when none does; `at` receives the running value there (the
+        // total over the n items when none does). The running values come
+        // from block prefix sums, so they round differently from a one-by-one
+        // sum only in the last places. Every thread calls it.
+        auto first_hit = [&](uint32_t n, double base, auto&& val, auto&& hit, double& at) -> uint32_t {
+            double carry = base;
+            for (uint32_t c0 = 0; c0 < n; c0 += NT) {   // (uniform)
+                const uint32_t i = c0 + tid;
+                double incl;
+                const double tot = block_scan_incl<NT>(i < n ? val(i) : 0.0, incl, sm.redd);
+                const double run = carry + incl;
+                const uint64_t f = block_min_u64<NT>(i < n && hit(i, run) ? (uint64_t)i : ~0ull, sm.red64);
+                if (f != ~0ull) {   // (uniform)
+                    if ((uint64_t)i == f) sm.walk_at = run;
+                    __syncthreads();
+                    at = sm.walk_at;
+                    __syncthreads();
+                    return (uint32_t)f;
+                }
+                carry += tot;
+            }
+            at = carry;
+            return n;
+        };
+        auto never = [](uint32_t, double) { return false; };
         for (uint32_t b = tid; b < NB; b += NT) {
             sm.u.h.cnt[b] = 0; sm.u.h.mlo[b] = 0; sm.u.h.mhi[b] = 0;
         }
@@ -546,7 +584,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
         auto hist_add = [&](float p) {
             const float x = tempered(p, maxl, inv_t);
             const uint32_t b = bin_of(x);
-            const unsigned long long q = quant(exp((double)x));
+            const unsigned long long q = quant(exp_f64((double)x));
             atomicAdd(&sm.u.h.cnt[b], 1u);
             const unsigned long long old = atomicAdd(&sm.u.h.mlo[b], q);
             if (old + q < old) atomicAdd(&sm.u.h.mhi[b], 1u);
@@ -554,7 +592,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
         auto hist_sub = [&](float p) {
             const float x = tempered(p, maxl, inv_t);
             const uint32_t b = bin_of(x);
-            const unsigned long long q = quant(exp((double)x));
+            const unsigned long long q = quant(exp_f64((double)x));
             atomicSub(&sm.u.h.cnt[b], 1u);
             const unsigned long long old = atomicAdd(&sm.u.h.mlo[b], (~q) + 1ull);
             if (old < q) atomicSub(&sm.u.h.mhi[b], 1u);
@@ -700,7 +738,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
                     const int b = (int)bin_of(tempered(v[k], maxl, inv_t));
                     if (!want(b)) continue;
                     const uint32_t e = e0 + k;
-                    if (nD > 0 && d_find(d_ids, nD, e) >= 0) continue;
+                    if (nD > 0 && is_pen(e)) continue;
                     f(v[k], e, b);
                 }
             });
@@ -729,12 +767,20 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
                 if (!dup && tot + segs[s].cnt <= CAP) { all[na++] = segs[s]; tot += segs[s].cnt; }
             }
             if (tid == 0) { sm.nlist = 0; sm.mp_count = 0; }
+            // the wanted bins as an LDS bitmap: one read per element
+            for (uint32_t w = tid; w < NB / 32u; w += NT) {
+                uint32_t m = 0;
+                for (uint32_t j = 0; j < 32u; ++j) {
+                    const int b = (int)(w * 32u + j);
+                    bool on = b >= mp_lo && b <= mp_hi;
+                    for (int s = 0; s < na; ++s) on = on || (b >= all[s].blo && b <= all[s].bhi);
+                    m |= on ? 1u << j : 0u;
+                }
+                sm.wbins[w] = m;
+            }
             __syncthreads();
             for_cands(
-                [&](int b) {
-                    for (int s = 0; s < na; ++s) if (b >= all[s].blo && b <= all[s].bhi) return true;
-                    return b >= mp_lo && b <= mp_hi;
-                },
+                [&](int b) { return ((sm.wbins[(uint32_t)b >> 5] >> ((uint32_t)b & 31u)) & 1u) != 0u; },
                 [&](float p, uint32_t e, int b) {
                     const uint64_t rk = rank_key(p, e);
                     for (int s = 0; s < na; ++s) {
@@ -877,67 +923,51 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
             const ExactSeg s = bin_seg(0, b_lim);
             nseg = 0;
             compact(&s, 1);
-            if (tid == 0) {
-                const uint32_t n = segs[0].cnt;          // candidates listed from position 0
-                const uint32_t lim = min(kk, n);
-                double sum = 0.0;
-                if (kk < n_cand) {
-                    for (uint32_t i = 0; i < kk; ++i) sum += weight(rank_val(sm.list[i]));
-                } else {
-                    sum = S;                              // full normaliser (exact)
-                }
-                uint32_t kp = kk;
-                if (use_p) {
-                    double cum = 0.0;
-                    for (uint32_t i = 0; i < lim; ++i) {
-                        cum += weight(rank_val(sm.list[i])) / sum;
-                        if (cum >= (double)P.top_p) { kp = i + 1; break; }
-                    }
-                }
-                uint32_t kv = kp;
-                if (use_m) {
-                    const double thresh = (double)P.min_p * (1.0 / sum);
-                    const uint32_t l2 = min(kp, n);
-                    uint32_t i = 1;
-                    for (; i < l2; ++i) {
-                        if (weight(rank_val(sm.list[i])) / sum < thresh) break;
-                    }
-                    kv = i < l2 ? i : (kp <= n ? kp : n);
-                }
-                kv = max(1u, min(kv, kk));
-                double ks = 0.0;
-                for (uint32_t i = 0; i < kv; ++i) ks += weight(rank_val(sm.list[i]));
-                double r = a.u[row] * (ks - 0.0) + 0.0;
-                uint32_t pos = kv - 1;
-                for (uint32_t i = 0; i < kv; ++i) {
-                    r -= weight(rank_val(sm.list[i]));
-                    if (r <= 0.0) { pos = i; break; }
-                }
-                sm.out_keep = kv;
-                sm.out_kept_sum = ks;
-                sm.out_boundary = rank_val(sm.list[kv - 1]);
-                sm.out_id = (int32_t)rank_idx(sm.list[pos]);
-                sm.out_S = sum;
+            const uint32_t n = segs[0].cnt;          // candidates listed from position 0
+            const uint32_t lim = min(kk, n);
+            auto wt = [&](uint32_t i) -> double { return weight(rank_val(sm.list[i])); };
+            double sum = S;                          // full normaliser (exact)
+            if (kk < n_cand) (void)first_hit(kk, 0.0, wt, never, sum);
+            uint32_t kp = kk;
+            if (use_p) {
+                // cum += w / sum, the first position reaching top_p
+                double at;
+                const uint32_t f = first_hit(lim, 0.0, [&](uint32_t i) { return wt(i) / sum; },
+                                             [&](uint32_t, double c) { return c >= (double)P.top_p; }, at);
+                if (f < lim) kp = f + 1;
             }
-            __syncthreads();
-            keep = sm.out_keep;
-            kept_sum = sm.out_kept_sum;
-            boundary = sm.out_boundary;
-            chosen = sm.out_id;
-            S = sm.out_S;
+            uint32_t kv = kp;
+            if (use_m) {
+                // the first i >= 1 with w_i / sum < min_p * w_0 / sum, w_0 =
+                // 1 (w falls with rank, so the survivors are a count)
+                const double thresh = (double)P.min_p * (1.0 / sum);
+                const uint32_t l2 = min(kp, n);
+                uint32_t c = 0;
+                for (uint32_t i = 1 + tid; i < l2; i += NT) c += wt(i) / sum >= thresh ? 1u : 0u;
+                const uint32_t i = 1u + block_sum_u<NT>(c, sm.redu);
+                kv = i < l2 ? i : (kp <= n ? kp : n);
+            }
+            kv = max(1u, min(kv, kk));
+            double ks;
+            (void)first_hit(kv, 0.0, wt, never, ks);
+            const double r = a.u[row] * (ks - 0.0) + 0.0;
+            double at;
+            const uint32_t f = first_hit(kv, 0.0, wt, [&](uint32_t, double run) { return r - run <= 0.0; }, at);
+            const uint32_t pos = f < kv ? f : kv - 1;
+            keep = kv;
+            kept_sum = ks;
+            boundary = rank_val(sm.list[kv - 1]);
+            chosen = (int32_t)rank_idx(sm.list[pos]);
+            S = sum;
         } else {
             // ---- targeted regions (large nuclei) ----
             if (kk < n_cand) {
                 const ExactSeg r = region_for_count(kk - 1);
                 if (!covered(r)) compact(&r, 1);
-                if (tid == 0) {
-                    const int s = seg_of(kk - 1);
-                    double sum = segs[s].mb;
-                    for (uint32_t pos = segs[s].cb; pos < kk; ++pos) sum += weight(rank_val(list_at(pos)));
-                    sm.out_S = sum;
-                }
-                __syncthreads();
-                S = sm.out_S;
+                const int s = seg_of(kk - 1);
+                const uint32_t cb = segs[s].cb;
+                (void)first_hit(kk - cb, segs[s].mb, [&](uint32_t i) { return weight(rank_val(list_at(cb + i))); },
+                                never, S);
             }
             uint32_t keep_p = kk;
             if (use_p) {
@@ -948,22 +978,16 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
                     mp_thresh = (double)P.min_p * (1.0 / S);
                 }
                 if (!covered(rp) || use_m) compact(&rp, 1);
-                if (tid == 0) {
-                    double cum = rp.mb / S;
-                    uint32_t kp = 0;
-                    const uint32_t end = min(rp.cb + rp.cnt, kk);
-                    for (uint32_t pos = rp.cb; pos < end; ++pos) {
-                        cum += weight(rank_val(list_at(pos))) / S;
-                        if (cum >= (double)P.top_p) { kp = pos + 1; break; }
-                    }
-                    if (kp == 0) {
-                        kp = end;
-                        if (end < kk) { atomicOr(a.status, kStatusBinCap); sm.bincap = 1u; }
-                    }
-                    sm.out_keep = kp;
+                const uint32_t end = min(rp.cb + rp.cnt, kk);
+                double at;
+                const uint32_t f = first_hit(end > rp.cb ? end - rp.cb : 0u, rp.mb / S,
+                                             [&](uint32_t i) { return weight(rank_val(list_at(rp.cb + i))) / S; },
+                                             [&](uint32_t, double c) { return c >= (double)P.top_p; }, at);
+                keep_p = rp.cb + f + 1u;
+                if (rp.cb + f >= end) {
+                    keep_p = end;
+                    if (end < kk && tid == 0) { atomicOr(a.status, kStatusBinCap); sm.bincap = 1u; }
                 }
-                __syncthreads();
-                keep_p = sm.out_keep;
             } else if (use_m) {
                 mp_lo = max(b_m - 1, 0);
                 mp_hi = min(b_m + 1, (int)NB - 1);
@@ -986,14 +1010,10 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
                 } else {
                     const ExactSeg r = region_for_count(keep - 1);
                     if (!covered(r)) compact(&r, 1);
-                    if (tid == 0) {
-                        const int s = seg_of(keep - 1);
-                        double ks = segs[s].mb;
-                        for (uint32_t pos = segs[s].cb; pos < keep; ++pos) ks += weight(rank_val(list_at(pos)));
-                        sm.out_kept_sum = ks;
-                    }
-                    __syncthreads();
-                    kept_sum = sm.out_kept_sum;
+                    const int s = seg_of(keep - 1);
+                    const uint32_t cb = segs[s].cb;
+                    (void)first_hit(keep - cb, segs[s].mb,
+                                    [&](uint32_t i) { return weight(rank_val(list_at(cb + i))); }, never, kept_sum);
                 }
             }
             // draw (sampling.cpp:135-147)
@@ -1002,26 +1022,25 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
             ExactSeg need[2] = {rr, region_for_count(keep - 1)};
             const int nneed = rr.cnt + need[1].cnt <= CAP ? 2 : 1;
             if (!covered(need[0]) || (nneed == 2 && !covered(need[1]))) compact(need, nneed);
-            if (tid == 0) {
-                double r = r0 - rr.mb;
+            {
+                // r -= w one by one, the first position reaching r <= 0
+                const double r = r0 - rr.mb;
                 const uint32_t end = min(rr.cb + rr.cnt, keep);
-                int32_t id = -1;
-                for (uint32_t pos = rr.cb; pos < end; ++pos) {
-                    const uint64_t k = list_at(pos);
-                    r -= weight(rank_val(k));
-                    if (r <= 0.0) { id = (int32_t)rank_idx(k); break; }
-                }
-                if (id < 0) {
-                    if (end < keep) { atomicOr(a.status, kStatusBinCap); sm.bincap = 1u; }
+                double at;
+                const uint32_t f = first_hit(end > rr.cb ? end - rr.cb : 0u, 0.0,
+                                             [&](uint32_t i) { return weight(rank_val(list_at(rr.cb + i))); },
+                                             [&](uint32_t, double run) { return r - run <= 0.0; }, at);
+                int32_t id;
+                if (rr.cb + f < end) {
+                    id = (int32_t)rank_idx(list_at(rr.cb + f));
+                } else {
+                    if (end < keep && tid == 0) { atomicOr(a.status, kStatusBinCap); sm.bincap = 1u; }
                     id = (int32_t)rank_idx(list_at(keep - 1));  // reference fallback (last survivor)
                 }
                 const uint64_t kb = list_at(keep - 1);
-                sm.out_boundary = kb == ~0ull ? maxl : rank_val(kb);
-                sm.out_id = id;
+                boundary = kb == ~0ull ? maxl : rank_val(kb);
+                chosen = id;
             }
-            __syncthreads();
-            chosen = sm.out_id;
-            boundary = sm.out_boundary;
         }
         if (tid == 0) {
             // a row whose selection overflowed a bin reports -1 (with the
