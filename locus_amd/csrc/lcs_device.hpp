@@ -481,9 +481,23 @@ __device__ __forceinline__ uint32_t scalar_load_u8(const uint8_t* p) {
 }
 
 // ------------------------------------------------------- vector loads ----
+// Global-memory views. A load through an address_space(1) pointer compiles to
+// global_load also inside an out-of-line function, where a generic pointer
+// gives flat_load, whose wait covers every outstanding LDS operation too.
+#define LCS_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ const LCS_GLOBAL T* glb(const T* p) { return (const LCS_GLOBAL T*)p; }
+// The same for LDS: a generic reference to a __shared__ object, passed into an
+// out-of-line function, read and written with ds_* rather than flat_*
+// instructions (only for objects that are in LDS).
+template <class T>
+__device__ __forceinline__ T& lds_ref(T& r) { return *(T*)(__attribute__((address_space(3))) T*)&r; }
+
 // 16-byte group loads: 4 f32 or 8 bf16 elements.
 __device__ __forceinline__ uint4 load16(const void* base, uint64_t group) {
-    return reinterpret_cast<const uint4*>(base)[group];
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 w = glb(reinterpret_cast<const u32x4*>(base))[group];
+    return make_uint4(w.x, w.y, w.z, w.w);
 }
 template <int G>
 __device__ __forceinline__ void decode(const uint4& r, float (&v)[G]);
@@ -504,18 +518,43 @@ __device__ __forceinline__ void decode<8>(const uint4& r, float (&v)[8]) {
 // Scalar element load for either dtype.
 __device__ __forceinline__ float load_elem(const void* row, uint32_t dtype, uint32_t i) {
     if (dtype == LCS_BF16) {
-        const uint16_t b = reinterpret_cast<const uint16_t*>(row)[i];
+        const uint16_t b = glb(reinterpret_cast<const uint16_t*>(row))[i];
         return __uint_as_float(static_cast<uint32_t>(b) << 16);
     }
-    return reinterpret_cast<const float*>(row)[i];
+    return glb(reinterpret_cast<const float*>(row))[i];
 }
 
 // --------------------------------------------------------- streaming pass --
 // Walks a row in 16-byte groups of G elements (4 f32 / 8 bf16); all loads of
 // an unrolled step are issued before any use. f(group, values, n_valid).
+constexpr int kStreamU = 8;   // 16-byte groups in flight per thread and step
+// As stream_groups, but every thread calls f for each of its group slots, in
+// uniform control flow (wave-wide operations are allowed in f); nv = 0 for a
+// slot past the row, whose v holds no data.
+template <int NT, int G, class F>
+__device__ __forceinline__ void stream_groups_all(const void* rowp, uint32_t V, F&& f) {
+    constexpr int U = kStreamU;
+    const uint32_t ng = (V + G - 1) / G;
+    for (uint32_t g0 = 0; g0 < ng; g0 += NT * U) {
+        uint4 r[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t gi = g0 + u * NT + tid_x();
+            r[u] = load16(rowp, gi < ng ? gi : 0u);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t gi = g0 + u * NT + tid_x();
+            float v[G];
+            decode<G>(r[u], v);
+            f(gi, v, gi < ng ? min((uint32_t)G, V - gi * G) : 0u);
+        }
+    }
+}
+
 template <int NT, int G, class F>
 __device__ __forceinline__ void stream_groups(const void* rowp, uint32_t V, F&& f) {
-    constexpr int U = 4;
+    constexpr int U = kStreamU;
     const uint32_t ng = (V + G - 1) / G;
     for (uint32_t g0 = 0; g0 < ng; g0 += NT * U) {
         uint4 r[U];

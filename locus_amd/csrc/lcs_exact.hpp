@@ -165,64 +165,55 @@ __device__ __forceinline__ uint32_t bucket_update(uint64_t* bkt, uint64_t (&ent)
 }
 
 // ------------------------------------------------------------- top-n list --
-// Per-thread descending (value, index) list of the n best raw logits seen.
-struct TopList {
-    float v[kTopMax];
-    uint32_t i[kTopMax];
-    float thv;
-    uint32_t thi;
-    __device__ void init() {
-#pragma unroll
-        for (int j = 0; j < (int)kTopMax; ++j) { v[j] = -kInfF; i[j] = kNoIdx; }
-        thv = -kInfF;
-        thi = kNoIdx;
-    }
-    __device__ __forceinline__ void offer(float x, uint32_t e, uint32_t n) {
-        if (!vi_better(x, e, thv, thi)) return;
-        float cv = x;
-        uint32_t ci = e;
-#pragma unroll
-        for (int j = 0; j < (int)kTopMax; ++j) {
-            if (j < (int)n && vi_better(cv, ci, v[j], i[j])) {
-                const float tv = v[j]; const uint32_t ti = i[j];
-                v[j] = cv; i[j] = ci; cv = tv; ci = ti;
+// Wave-wide descending top-n list of (value, index), n <= kTopMax <= 64: lane
+// j < n holds entry j; (tv, ti) is entry n-1, the bar a new element must beat
+// (the same in every lane).
+struct WaveTop {
+    float v;
+    uint32_t i;
+    float tv;
+    uint32_t ti;
+    __device__ void init() { v = -kInfF; i = kNoIdx; tv = -kInfF; ti = kNoIdx; }
+    // One element per lane (ok: the lane has one). Every lane of the wave
+    // calls it, in uniform control flow. The best waiting element enters
+    // first, so one call makes at most n insertions.
+    __device__ __forceinline__ void offer(bool ok, float x, uint32_t e, uint32_t n) {
+        const uint32_t lane = (uint32_t)lane_id();
+        bool c = ok && vi_better(x, e, tv, ti);
+        while (__ballot(c)) {
+            float bx = c ? x : -kInfF;
+            uint32_t be = c ? e : kNoIdx;
+            wave_argmax(bx, be);
+            const uint32_t pos = (uint32_t)__popcll(__ballot(lane < n && vi_better(v, i, bx, be)));
+            const float pv = __shfl_up(v, 1, kWave);
+            const uint32_t pi = __shfl_up(i, 1, kWave);
+            if (lane < n && lane >= pos) {
+                v = lane == pos ? bx : pv;
+                i = lane == pos ? be : pi;
             }
+            tv = __shfl(v, (int)n - 1, kWave);
+            ti = __shfl(i, (int)n - 1, kWave);
+            c = c && !(e == be) && vi_better(x, e, tv, ti);
         }
-#pragma unroll
-        for (int j = 0; j < (int)kTopMax; ++j) {
-            if (j == (int)n - 1) { thv = v[j]; thi = i[j]; }
-        }
-    }
-    __device__ __forceinline__ void pop() {
-#pragma unroll
-        for (int j = 0; j < (int)kTopMax - 1; ++j) { v[j] = v[j + 1]; i[j] = i[j + 1]; }
-        v[kTopMax - 1] = -kInfF;
-        i[kTopMax - 1] = kNoIdx;
     }
 };
 
-// Block-wide top-n of the per-thread lists into buf[0..n) as rank keys
+// Block-wide top-n of the waves' lists into buf[0..n) as rank keys
 // (sentinel ~0 for missing). buf must hold next_pow2((NT/64)*kTopMax).
 template <int NT>
-__device__ void block_topn(TopList& t, uint32_t n, uint64_t* buf) {
+__device__ void block_topn(const WaveTop& t, uint32_t n, uint64_t* buf) {
     constexpr uint32_t kSlots = (NT / kWave) * kTopMax;
     const uint32_t p2 = next_pow2(kSlots);
     for (uint32_t i = tid_x(); i < p2; i += NT) buf[i] = ~0ull;
     __syncthreads();
-    const int lane = tid_x() & 63, w = tid_x() / kWave;
-    for (uint32_t r = 0; r < n; ++r) {
-        float bv = t.v[0];
-        uint32_t bi = t.i[0];
-        wave_argmax(bv, bi);
-        if (lane == 0 && bi != kNoIdx) buf[w * kTopMax + r] = rank_key(bv, bi);
-        if (bi != kNoIdx && t.i[0] == bi) t.pop();
-    }
+    const uint32_t lane = tid_x() & 63u, w = tid_x() / kWave;
+    if (lane < n && t.i != kNoIdx) buf[w * kTopMax + lane] = rank_key(t.v, t.i);
     __syncthreads();
     bitonic_sort<NT>(buf, p2);
 }
 
 __device__ __forceinline__ bool mask_bit(const uint32_t* mrow, uint32_t e) {
-    return (mrow[e >> 5] >> (e & 31u)) & 1u;
+    return (glb(mrow)[e >> 5] >> (e & 31u)) & 1u;
 }
 
 // =================================================== exact single-WG path ==
@@ -244,6 +235,11 @@ struct ExactSmem {
             uint32_t cnt[NB];
             unsigned long long mlo[NB];
             uint32_t mhi[NB];
+            // penalised-id membership (set after P0, read by every later pass):
+            // fpre[w] = set filter bits in words [0, w); fmask holds one byte
+            // per set filter bit, in that order, with bit (id & 7) per id
+            uint16_t fpre[kIdFilterWords];
+            uint32_t fmask[DCAP / 4];
         } h;
     } u;
     uint64_t list[CAP];
@@ -277,8 +273,10 @@ __device__ __forceinline__ double mass_to_double(unsigned long long hi, unsigned
     return (ldexp((double)hi, 64) + (double)lo) * (1.0 / kTwo63);
 }
 
-// Binary search of a distinct penalised id; returns its slot or -1.
-__device__ __forceinline__ int d_find(const uint32_t* ids, uint32_t n, uint32_t e) {
+// Binary search of a distinct penalised id (a list in global memory); returns
+// its slot or -1.
+__device__ __forceinline__ int d_find(const uint32_t* ids_g, uint32_t n, uint32_t e) {
+    const LCS_GLOBAL uint32_t* ids = glb(ids_g);
     uint32_t lo = 0, hi = n;
     while (lo < hi) {
         const uint32_t mid = (lo + hi) >> 1;
@@ -320,9 +318,13 @@ __device__ __forceinline__ void write_logprobs(const SampleArgs& a, uint32_t row
     }
 }
 
+// a_lds and sm_lds are __shared__ objects of the calling kernel.
 template <int NT, uint32_t NB, uint32_t CAP, uint32_t DCAP, int G>
-__device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_t row, ExactSmem<NT, NB, CAP, DCAP>& sm) {
+__device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uint32_t row,
+                                                    ExactSmem<NT, NB, CAP, DCAP>& sm_lds) {
     static_assert(NB % NT == 0 || NT % NB == 0, "bins vs threads");
+    const SampleArgs& a = lds_ref(a_lds);
+    ExactSmem<NT, NB, CAP, DCAP>& sm = lds_ref(sm_lds);
     const uint32_t tid = tid_x();
     const lcs_params P = a.params[row];
     const uint32_t V = a.vocab;
@@ -397,10 +399,40 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
         }
     }
 
-    // a penalised id: the LDS filter first (most ids are not), then a binary
-    // search of the sorted list in global memory
+    // Exact membership of the penalised ids in LDS: the filter's set bits
+    // ranked by a prefix count over its words, and a byte per set bit with a
+    // bit for each of its 8 ids.
+    if (nD > 0) {
+        constexpr uint32_t WPT = (kIdFilterWords + NT - 1) / NT;
+        uint32_t c = 0;
+        for (uint32_t k = 0; k < WPT; ++k) {
+            const uint32_t w = tid * WPT + k;
+            if (w < kIdFilterWords) c += __popc(sm.idf[w]);
+        }
+        uint32_t base = 0;
+        block_exclusive_scan<NT>(c, base, sm.redu);
+        for (uint32_t k = 0; k < WPT; ++k) {
+            const uint32_t w = tid * WPT + k;
+            if (w < kIdFilterWords) {
+                sm.u.h.fpre[w] = (uint16_t)base;
+                base += __popc(sm.idf[w]);
+            }
+        }
+        for (uint32_t k = tid; k < (nD + 3u) / 4u; k += NT) sm.u.h.fmask[k] = 0u;
+        __syncthreads();
+        for (uint32_t j = tid; j < nD; j += NT) {
+            const uint32_t d = d_ids[j];
+            const uint32_t wd = sm.idf[d >> 8], bit = (d >> 3) & 31u;
+            const uint32_t rank = sm.u.h.fpre[d >> 8] + __popc(wd & ((1u << bit) - 1u));
+            atomicOr(&sm.u.h.fmask[rank >> 2], 1u << ((rank & 3u) * 8u + (d & 7u)));
+        }
+        __syncthreads();
+    }
     auto is_pen = [&](uint32_t e) -> bool {
-        return ((sm.idf[e >> 8] >> ((e >> 3) & 31u)) & 1u) && d_find(d_ids, nD, e) >= 0;
+        const uint32_t wd = sm.idf[e >> 8], bit = (e >> 3) & 31u;
+        if (!((wd >> bit) & 1u)) return false;
+        const uint32_t rank = sm.u.h.fpre[e >> 8] + __popc(wd & ((1u << bit) - 1u));
+        return (sm.u.h.fmask[rank >> 2] >> ((rank & 3u) * 8u + (e & 7u))) & 1u;
     };
 
     // ---- P1: raw stats, logsumexp, top-n, candidate max/min ----
@@ -408,11 +440,11 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
     uint32_t rarg = kNoIdx, carg = kNoIdx, nall = 0;
     float om = -kInfF;
     double os = 0.0;
-    TopList tl;
+    WaveTop tl;
     tl.init();
-    stream_groups<NT, G>(rowp, V, [&](uint32_t gi, const float (&v)[G], uint32_t nv) {
+    stream_groups_all<NT, G>(rowp, V, [&](uint32_t gi, const float (&v)[G], uint32_t nv) {
         const uint32_t e0 = gi * G;
-        const uint32_t mw = mrow ? (mrow[e0 >> 5] >> (e0 & 31u)) : 0xffffffffu;
+        const uint32_t mw = mrow && nv ? (glb(mrow)[e0 >> 5] >> (e0 & 31u)) : 0xffffffffu;
         float gm = -kInfF;
         for (uint32_t k = 0; k < nv; ++k) gm = fmaxf(gm, v[k]);
         if (gm > om) {
@@ -434,7 +466,10 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
                 if (carg == kNoIdx || x > cmax) { cmax = x; carg = e; }
                 cmin = fminf(cmin, x);
             }
-            if (ntop) tl.offer(x, e, ntop);
+        }
+        if (ntop) {
+#pragma unroll
+            for (uint32_t k = 0; k < (uint32_t)G; ++k) tl.offer(k < nv, v[k], e0 + k, ntop);
         }
     });
     {
@@ -488,7 +523,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
             nmi = kNoIdx;
             stream_groups<NT, G>(rowp, V, [&](uint32_t gi, const float (&v)[G], uint32_t nv) {
                 const uint32_t e0 = gi * G;
-                const uint32_t mw = use_mask ? (mrow[e0 >> 5] >> (e0 & 31u)) : 0xffffffffu;
+                const uint32_t mw = use_mask ? (glb(mrow)[e0 >> 5] >> (e0 & 31u)) : 0xffffffffu;
                 for (uint32_t k = 0; k < nv; ++k) {
                     const uint32_t e = e0 + k;
                     if (((mw >> k) & 1u) && (nmi == kNoIdx || vi_better(v[k], e, nm, nmi)) &&
@@ -599,7 +634,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
         };
         stream_groups<NT, G>(rowp, V, [&](uint32_t gi, const float (&v)[G], uint32_t nv) {
             const uint32_t e0 = gi * G;
-            const uint32_t mw = use_mask ? (mrow[e0 >> 5] >> (e0 & 31u)) : 0xffffffffu;
+            const uint32_t mw = use_mask ? (glb(mrow)[e0 >> 5] >> (e0 & 31u)) : 0xffffffffu;
             for (uint32_t k = 0; k < nv; ++k) {
                 if ((mw >> k) & 1u) hist_add(v[k]);
             }
@@ -732,7 +767,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
         auto for_cands = [&](auto&& want, auto&& f) {
             stream_groups<NT, G>(rowp, V, [&](uint32_t gi, const float (&v)[G], uint32_t nv) {
                 const uint32_t e0 = gi * G;
-                const uint32_t mw = use_mask ? (mrow[e0 >> 5] >> (e0 & 31u)) : 0xffffffffu;
+                const uint32_t mw = use_mask ? (glb(mrow)[e0 >> 5] >> (e0 & 31u)) : 0xffffffffu;
                 for (uint32_t k = 0; k < nv; ++k) {
                     if (!((mw >> k) & 1u)) continue;
                     const int b = (int)bin_of(tempered(v[k], maxl, inv_t));
@@ -811,7 +846,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a, uint32_
         // Narrows one bin holding > CAP candidates to a rank-key interval
         // containing candidate position `pos` (by_count) or the crossing of
         // cumulative mass `mt`, by 8-bit MSD radix steps on the rank key.
-        auto narrow = [&](int b, bool by_count, uint32_t pos, double mt) -> ExactSeg {
+        auto narrow = [&](int b, bool by_count, uint32_t pos, double mt) __attribute__((always_inline)) -> ExactSeg {
             ExactSeg s = bin_seg(b, b);
             uint64_t mn = ~0ull, mx = 0;
             for_cands([&](int bb) { return bb == b; }, [&](float p, uint32_t e, int) {
