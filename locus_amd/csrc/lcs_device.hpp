@@ -531,9 +531,8 @@ constexpr int kStreamU = 8;   // 16-byte groups in flight per thread and step
 // As stream_groups, but every thread calls f for each of its group slots, in
 // uniform control flow (wave-wide operations are allowed in f); nv = 0 for a
 // slot past the row, whose v holds no data.
-template <int NT, int G, class F>
+template <int NT, int G, int U = 4, class F>
 __device__ __forceinline__ void stream_groups_all(const void* rowp, uint32_t V, F&& f) {
-    constexpr int U = kStreamU;
     const uint32_t ng = (V + G - 1) / G;
     for (uint32_t g0 = 0; g0 < ng; g0 += NT * U) {
         uint4 r[U];

@@ -225,6 +225,11 @@ struct ExactSeg {
     double mb;           // exact mass before the region
 };
 constexpr uint32_t kSubBins = 256;
+constexpr int kExactSegs = 4;   // regions listed at once
+struct ExactBox {               // a region's bins and rank-key interval
+    int blo, bhi;
+    uint64_t rlo, rhi;
+};
 constexpr uint32_t kIdFilterWords = kMaxVocab / 8 / 32;   // one bit per 8 ids
 
 template <int NT, uint32_t NB, uint32_t CAP, uint32_t DCAP>
@@ -240,6 +245,7 @@ struct ExactSmem {
             // per set filter bit, in that order, with bit (id & 7) per id
             uint16_t fpre[kIdFilterWords];
             uint32_t fmask[DCAP / 4];
+            uint2 q[NT];   // per wave, 64 staged (logit bits, id) of a candidate pass
         } h;
     } u;
     uint64_t list[CAP];
@@ -257,6 +263,7 @@ struct ExactSmem {
     uint32_t idf[kIdFilterWords];   // bit k: some penalised id lies in [8k, 8k + 8)
     uint32_t wbins[NB / 32];        // bins a compaction pass wants
     ExactSeg bc_seg;
+    ExactBox cbox[kExactSegs];   // the regions a compaction collects
     uint32_t nlist;
     uint32_t mp_count;
     uint32_t flag;
@@ -447,13 +454,18 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
         const uint32_t mw = mrow && nv ? (glb(mrow)[e0 >> 5] >> (e0 & 31u)) : 0xffffffffu;
         float gm = -kInfF;
         for (uint32_t k = 0; k < nv; ++k) gm = fmaxf(gm, v[k]);
-        if (gm > om) {
-            os = (om == -kInfF) ? 0.0 : os * exp((double)om - (double)gm);
-            om = gm;
+        // the running offset is the wave's max so far, so its rescale is a
+        // uniform branch taken when that max rises
+        const float wm = wave_max(gm);
+        if (wm > om) {
+            os = (om == -kInfF) ? 0.0 : os * exp_f64((double)om - (double)wm);
+            om = wm;
         }
         if (om != -kInfF) {
+            // (this sum feeds only the logprobs' normaliser, so the fast
+            // exponential's few-ulp error is far inside their tolerance)
             float gs = 0.0f;
-            for (uint32_t k = 0; k < nv; ++k) gs += expf(fsub(v[k], om));
+            for (uint32_t k = 0; k < nv; ++k) gs += __expf(fsub(v[k], om));
             os += (double)gs;
         }
         for (uint32_t k = 0; k < nv; ++k) {
@@ -461,13 +473,19 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
             const float x = v[k];
             if (rarg == kNoIdx || x > rmax) { rmax = x; rarg = e; }
             rmin = fminf(rmin, x);
-            if ((mw >> k) & 1u) {
-                ++nall;
-                if (carg == kNoIdx || x > cmax) { cmax = x; carg = e; }
-                cmin = fminf(cmin, x);
+        }
+        if (mrow) {   // (an unmasked row takes the raw figures below)
+            for (uint32_t k = 0; k < nv; ++k) {
+                if ((mw >> k) & 1u) {
+                    const float x = v[k];
+                    ++nall;
+                    if (carg == kNoIdx || x > cmax) { cmax = x; carg = e0 + k; }
+                    cmin = fminf(cmin, x);
+                }
             }
         }
-        if (ntop) {
+        // (a group whose max is below the wave's bar offers nothing)
+        if (ntop && __ballot(nv > 0u && !(gm < tl.tv))) {
 #pragma unroll
             for (uint32_t k = 0; k < (uint32_t)G; ++k) tl.offer(k < nv, v[k], e0 + k, ntop);
         }
@@ -734,7 +752,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
         // token id: exact ties are separated by id). Regions in the list are
         // disjoint and the list is sorted by rank, so each region occupies a
         // contiguous run of the list starting at `off`.
-        constexpr int kSegs = 4;
+        constexpr int kSegs = kExactSegs;
         ExactSeg segs[kSegs];
         int nseg = 0;
         auto bin_seg = [&](int blo, int bhi) {
@@ -743,9 +761,6 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
             s.cb = cnt_incl(blo - 1); s.cnt = cnt_incl(bhi) - s.cb; s.off = 0;
             s.mb = mass_incl(blo - 1);
             return s;
-        };
-        auto seg_has = [](const ExactSeg& s, int b, uint64_t rk) {
-            return b >= s.blo && b <= s.bhi && rk >= s.rlo && rk <= s.rhi;
         };
         auto seg_of = [&](uint32_t pos) -> int {
             for (int s = 0; s < nseg; ++s)
@@ -762,21 +777,45 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
             if (s < 0) return ~0ull;
             return sm.list[min(segs[s].off + (pos - segs[s].cb), CAP - 1)];
         };
-        // f(p, e, b) over candidates whose bin passes want(b), penalised values
-        // (raw ids of the window are replaced by their penalised entries)
+        // f(value, id, bin) over every candidate whose bin want() accepts,
+        // penalised values (raw ids of the window are replaced by their
+        // penalised entries). A pass wants few, scattered elements, so each
+        // wave stages them in LDS (64 slots) and runs f with its lanes full,
+        // instead of once per element position in which any lane has one.
         auto for_cands = [&](auto&& want, auto&& f) {
-            stream_groups<NT, G>(rowp, V, [&](uint32_t gi, const float (&v)[G], uint32_t nv) {
+            uint2* q = sm.u.h.q + (tid & ~63u);
+            const uint32_t lane = tid & 63u;
+            uint32_t qn = 0;   // staged entries (the same in every lane)
+            auto flush = [&]() {
+                wave_sync();
+                if (lane < qn) {
+                    const uint2 t = q[lane];
+                    const float p = __uint_as_float(t.x);
+                    f(p, t.y, (int)bin_of(tempered(p, maxl, inv_t)));
+                }
+                wave_sync();
+                qn = 0;
+            };
+            stream_groups_all<NT, G>(rowp, V, [&](uint32_t gi, const float (&v)[G], uint32_t nv) {
                 const uint32_t e0 = gi * G;
-                const uint32_t mw = use_mask ? (glb(mrow)[e0 >> 5] >> (e0 & 31u)) : 0xffffffffu;
-                for (uint32_t k = 0; k < nv; ++k) {
-                    if (!((mw >> k) & 1u)) continue;
-                    const int b = (int)bin_of(tempered(v[k], maxl, inv_t));
-                    if (!want(b)) continue;
-                    const uint32_t e = e0 + k;
-                    if (nD > 0 && is_pen(e)) continue;
-                    f(v[k], e, b);
+                const uint32_t mw = use_mask && nv ? (glb(mrow)[e0 >> 5] >> (e0 & 31u)) : 0xffffffffu;
+#pragma unroll
+                for (uint32_t k = 0; k < (uint32_t)G; ++k) {
+                    bool ok = k < nv && ((mw >> k) & 1u);
+                    if (ok) ok = want((int)bin_of(tempered(v[k], maxl, inv_t))) && !(nD > 0 && is_pen(e0 + k));
+                    const uint64_t m = __ballot(ok);
+                    const uint32_t c = (uint32_t)__popcll(m);
+                    if (c == 0u) continue;
+                    if (qn + c > (uint32_t)kWave) flush();
+                    if (ok) {
+                        const uint32_t at = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)m, qn));
+                        q[at] = make_uint2(__float_as_uint(v[k]), e0 + k);
+                    }
+                    qn += c;
                 }
             });
+            if (qn > 0u) flush();
             for (uint32_t j = tid; j < nD; j += NT) {
                 const uint32_t d = d_ids[j];
                 if (!is_cand(d)) continue;
@@ -802,6 +841,11 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
                 if (!dup && tot + segs[s].cnt <= CAP) { all[na++] = segs[s]; tot += segs[s].cnt; }
             }
             if (tid == 0) { sm.nlist = 0; sm.mp_count = 0; }
+            if (tid < (uint32_t)na) {
+                ExactBox bx;
+                bx.blo = all[tid].blo; bx.bhi = all[tid].bhi; bx.rlo = all[tid].rlo; bx.rhi = all[tid].rhi;
+                sm.cbox[tid] = bx;
+            }
             // the wanted bins as an LDS bitmap: one read per element
             for (uint32_t w = tid; w < NB / 32u; w += NT) {
                 uint32_t m = 0;
@@ -818,12 +862,17 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
                 [&](int b) { return ((sm.wbins[(uint32_t)b >> 5] >> ((uint32_t)b & 31u)) & 1u) != 0u; },
                 [&](float p, uint32_t e, int b) {
                     const uint64_t rk = rank_key(p, e);
-                    for (int s = 0; s < na; ++s) {
-                        if (seg_has(all[s], b, rk)) {
-                            const uint32_t slot = atomicAdd(&sm.nlist, 1u);
-                            if (slot < CAP) sm.list[slot] = rk;
-                            break;
+                    bool in = false;
+#pragma unroll
+                    for (int s = 0; s < kSegs; ++s) {
+                        if (s < na) {
+                            const ExactBox bx = sm.cbox[s];
+                            in = in || (b >= bx.blo && b <= bx.bhi && rk >= bx.rlo && rk <= bx.rhi);
                         }
+                    }
+                    if (in) {
+                        const uint32_t slot = atomicAdd(&sm.nlist, 1u);
+                        if (slot < CAP) sm.list[slot] = rk;
                     }
                     if (b >= mp_lo && b <= mp_hi && weight(p) / S >= mp_thresh) atomicAdd(&sm.mp_count, 1u);
                 });

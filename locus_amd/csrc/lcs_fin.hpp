@@ -86,7 +86,7 @@ struct FinSmem {
             uint64_t tkey[kSsTopKMerge];   // top-k rows past kRowWin candidates: the slices' lists, kTopKMax apart
             float traw[kSsTopKMerge];
         } f;
-        ExactSmem<kFinThreads, kFbBins, kFbCap, kFbHistCap> ex;
+        ExactSmem<kFinThreads, kFinFbBins, kFinFbCap, kFbHistCap> ex;
     } u;
     double log_z, fin_S, fin_rel, fin_invS;
     float chosen_raw, fin_maxl;
@@ -682,7 +682,7 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
     // holds the same headers, so the test is uniform)
     if (ballot((uint32_t)lane < S && ((uint32_t)(hd[0] >> 48) & (rec::kFlagPenOverflow | rec::kFlagExact)) != 0u)) {
         stage_args(&sm.args, a);
-        exact_row<kFinThreads, kFbBins, kFbCap, kFbHistCap, G>(sm.args, row, sm.u.ex);
+        exact_row<kFinThreads, kFinFbBins, kFinFbCap, kFbHistCap, G>(sm.args, row, sm.u.ex);
         return;
     }
     PROF_AT(kProfFin + row, 20 + wv);
@@ -753,7 +753,7 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
     // the records cannot settle this row: the exact single-workgroup path
     // (out of line: it reads the kernel arguments from an LDS copy)
     stage_args(&sm.args, a);
-    exact_row<kFinThreads, kFbBins, kFbCap, kFbHistCap, G>(sm.args, row, sm.u.ex);
+    exact_row<kFinThreads, kFinFbBins, kFinFbCap, kFbHistCap, G>(sm.args, row, sm.u.ex);
 }
 
 // One workgroup per row (the sliced path's second kernel). The leading

@@ -58,10 +58,16 @@ constexpr int kGenThreads = 1024;
 constexpr uint32_t kGenBins = 2048;
 constexpr uint32_t kGenCap = 2048;
 constexpr uint32_t kGenHistCap = 8192;
-// inline fallback inside the sliced kernel (256 threads, small LDS)
+// inline fallback inside the nucleus finalize kernels (256 threads; the
+// LDS block shares the nucleus passes' union, so it stays within 32 KB)
 constexpr uint32_t kFbBins = 512;
 constexpr uint32_t kFbCap = 512;
 constexpr uint32_t kFbHistCap = kFastHistMax;
+// inline fallback inside row_fin (256 threads, one workgroup per row): bins
+// and list as wide as the general kernel's, so a wide min-p window rarely
+// needs a radix narrowing
+constexpr uint32_t kFinFbBins = 2048;
+constexpr uint32_t kFinFbCap = 2048;
 
 enum RowMode : uint32_t { kModeGreedy = 1, kModeWindow = 2, kModeGeneral = 4, kModeTopK = 8, kModeNucleus = 16 };
 constexpr uint32_t kTopKMax = 64;         // top_k served by the sliced path
