@@ -639,6 +639,34 @@ def test_window_rows_with_many_entries_per_slice(sampler):
     assert (paths[[7, 8]] == 4).all(), paths.tolist()
 
 
+def test_wide_min_p_windows(sampler):
+    """C2-shaped rows whose min-p windows hold thousands of ids (far past a
+    slice's 64-entry record), so row_fin resolves them on the exact path: with
+    and without penalties, top-p on and off, f32 and bf16."""
+    base = W.make("c2", rows=16, set_index=31)
+    rng = np.random.default_rng(2031)
+    lg = (base.logits / 3.0).astype(np.float32)       # N(0, 1)
+    p = base.params.copy()
+    p["temperature"][:8], p["min_p"][:8] = 1.5, 0.01
+    p["temperature"][8:], p["min_p"][8:] = 1.0, 0.05
+    p["top_p"][::3] = 1.0
+    for r in range(1, base.rows, 4):
+        p["repeat_penalty"][r], p["frequency_penalty"][r], p["presence_penalty"][r] = 1.0, 0.0, 0.0
+    lg[5, rng.choice(base.vocab, 4000, replace=False)] += 2.0   # a denser head
+    w = W.Workload("wide-min-p", base.rows, base.vocab, "f32", lg, p, base.seeds, base.u,
+                   base.hist_off, base.hist_ids, None, 5, True)
+    g = run(sampler, w)
+    compare(w, g, O.sample_batch(w, threads=8), "wide-min-p", expect_paths={3, 4})
+    assert (g["diag"]["keep"] > 64).all(), g["diag"]["keep"].tolist()
+    assert (g["diag"]["path"] == 4).sum() >= 14, g["diag"]["path"].tolist()
+    b16 = W.bf16_rne(lg)
+    wb = W.Workload("wide-min-p-bf16", w.rows, w.vocab, "bf16", b16, p, w.seeds, w.u,
+                    w.hist_off, w.hist_ids, None, 5, True)
+    w32 = W.Workload("wide-min-p-bf16-as-f32", w.rows, w.vocab, "f32", W.bf16_to_f32(b16), p, w.seeds, w.u,
+                     w.hist_off, w.hist_ids, None, 5, True)
+    compare(w32, run(sampler, wb), O.sample_batch(w32, threads=8), "wide-min-p-bf16", expect_paths={3, 4})
+
+
 def test_top_n_with_clustered_maxima(sampler):
     """Top-n logprobs where many logits near the top share the upper 16 bits
     of their sort keys (the slice's candidate bound is cut to 16 bits): 40
