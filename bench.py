@@ -33,7 +33,8 @@ MALL_BYTES = 256 << 20
 # pattern (SQL LIKE) matching them, and the stem of their profile summaries
 # ("a|b" matches either)
 KERNEL = {"c1g": ("slice_stats|row_fin", "sliced"), "c1s": ("slice_stats|row_fin", "sliced"),
-          "c2": ("slice_stats|row_fin", "sliced"), "c3": ("nuc_", "nucleus"),
+          "c2": ("slice_stats|row_fin", "sliced"), "c2w": ("slice_stats|row_fin", "sliced"),
+          "c3": ("nuc_", "nucleus"),
           "c4": ("nuc_", "nucleus"), "c5": ("verify_kernel|accept_kernel", "verify")}
 
 
@@ -46,6 +47,8 @@ CONFIG_TEXT = {
     "c1g": "B=1 V=128256 f32 greedy",
     "c1s": "B=1 V=128256 f32 T0.8 top-k40 top-p0.95",
     "c2": "B=64 V=128256 f32 pen(1.1,0.5,0.3,last2048) T0.7 min-p0.05 top-p0.9 top-5 logprobs",
+    "c2w": "c2 with N(0,1) logits, T1.5, min-p0.01: wide min-p windows, every row on the exact path "
+           "inside row_fin (stress case, not a BASELINE config)",
     "c3": "B=256 V=151936 f32 T1.5 top-p0.98",
     "c4": "B=32 V=128256 f32 JSON-mask T1.0 top-p0.95 top-1 logprob",
     "c5": "4096 rows (512x8) V=163840 bf16 verify: argmax + lp(draft) + accept length",
@@ -355,6 +358,76 @@ def phase_clocks(workload: str, rows: int | None, calls: int = 16):
                      f"{d.max():.2f} max)")
     tot = F[:, 16] - F[:, 0]
     lines.append(f"row_fin per row, start to outputs: median {np.median(tot):.2f}, max {tot.max():.2f}")
+    return "\n".join(lines)
+
+
+EXACT_PHASES = {0: "start", 1: "distinct penalised ids (history sort)", 2: "stats pass (raw max, sums, top-n)",
+                3: "maximum penalised candidate", 4: "histogram pass", 5: "prefix sums over bins",
+                10: "region search", 11: "compaction: wanted bins + candidate pass",
+                12: "compaction: sort of the list", 13: "compaction: regions", 20: "region search",
+                21: "narrowing: key range pass", 22: "narrowing: radix step pass", 23: "narrowing: end",
+                99: "walks, decision and outputs"}
+
+
+def exact_clocks(workload: str, rows: int | None, calls: int = 8):
+    """Per-phase wall clocks (s_memrealtime, 100 MHz) of the exact path that
+    row_fin runs for rows the slice records cannot settle, from the
+    LCS_PROFILE build: each phase's time since the row's previous stamp, in
+    us, median / max over rows and calls, for the rows whose stamp sequence
+    is the most common one."""
+    import collections
+    import ctypes as C
+    import torch
+
+    from locus_amd import build as B
+    from locus_amd import sampler as SM
+    if not os.path.exists(B.PROFILE_SO):
+        raise SystemExit(f"{B.PROFILE_SO} is missing: run __graft_entry__.build()")
+    SM.LIB_PATH = B.PROFILE_SO
+    L = SM.lib()
+    L.lcs_xprof_read.restype = C.c_int
+    L.lcs_xprof_read.argtypes = [C.c_void_p, C.c_void_p]
+    L.lcs_xprof_clear.restype = C.c_int
+    w = W.make(workload, rows=rows)
+    s = SM.Sampler(device=0, max_rows=w.rows, max_vocab=262144, max_hist=4096, max_top=20)
+    d = s.upload(w)
+    run = s.prepare(d, s.alloc_out(w.rows, w.n_top, w.want_logprobs, diag=False))
+    h = s.stream_handle()
+    seqs = []
+    for it in range(calls + 2):
+        if L.lcs_xprof_clear() != 0:
+            raise SystemExit("lcs_xprof_clear failed")
+        run(h)
+        torch.cuda.synchronize()
+        buf = np.zeros(4096 * 64, dtype=np.uint64)
+        cnt = np.zeros(4096, dtype=np.uint32)
+        if L.lcs_xprof_read(buf.ctypes.data, cnt.ctypes.data) != 0:
+            raise SystemExit("lcs_xprof_read failed")
+        if it < 2:
+            continue
+        t = buf.reshape(4096, 32, 2).astype(np.int64)
+        for r in range(w.rows):
+            n = int(cnt[r])
+            if n:
+                seqs.append((tuple(int(x) for x in t[r, :n, 1]), (t[r, :n, 0] - t[r, 0, 0]) / 100.0))
+    s.close()
+    if not seqs:
+        return f"# exact path phase clocks, workload {workload}: no row took the exact path"
+    common, nrow = collections.Counter(q for q, _ in seqs).most_common(1)[0]
+    T = np.stack([ts for q, ts in seqs if q == common])
+    lines = [f"# exact path phase clocks inside row_fin, workload {workload} ({w.rows} rows), {calls} calls: "
+             f"{len(seqs)} row finalizes took the exact path, {nrow} with the stamp sequence below",
+             "# time since the previous stamp, us: median / max over those rows",
+             "  tag  phase                                           median     max"]
+    for j, tag in enumerate(common):
+        dt = T[:, j] - (T[:, j - 1] if j else 0.0)
+        lines.append(f"  {tag:3d}  {EXACT_PHASES.get(tag, str(tag)):46s} {np.median(dt):8.2f}  {dt.max():8.2f}")
+    tot = T[:, -1]
+    lines.append(f"exact path per row, first to last stamp: median {np.median(tot):.2f}, max {tot.max():.2f}")
+    lines.append("# every stamp sequence: rows, first-to-last median / max (us), tags")
+    for q, c in collections.Counter(q for q, _ in seqs).most_common():
+        tq = np.array([ts[-1] for qq, ts in seqs if qq == q])
+        lines.append(f"  {c:4d}  {np.median(tq):8.2f}  {tq.max():8.2f}  {' '.join(str(x) for x in q)}")
     return "\n".join(lines)
 
 
@@ -686,10 +759,16 @@ def main():
                     help="only time the engine's batched step (BatchSampler::sample_step) end to end on C2")
     ap.add_argument("--phase-clocks", action="store_true",
                     help="only print the sliced path's phase clocks (the LCS_PROFILE build) on --workload")
-    ap.add_argument("--rows", type=int, default=None, help="rows of the workload (--phase-clocks)")
+    ap.add_argument("--exact-clocks", action="store_true",
+                    help="only print the phase clocks of row_fin's exact path (the LCS_PROFILE build) on "
+                         "--workload (c2w sends every row there)")
+    ap.add_argument("--rows", type=int, default=None, help="rows of the workload (--phase-clocks, --exact-clocks)")
     args = ap.parse_args()
     if args.phase_clocks:
         print(phase_clocks(args.workload, args.rows))
+        return
+    if args.exact_clocks:
+        print(exact_clocks(args.workload, args.rows))
         return
     if args.batch_sampler:
         print(json.dumps(batch_sampler_bench(args.steps, args.warmup)))

@@ -425,23 +425,42 @@ __device__ __forceinline__ double block_scan_incl(double v, double& incl, double
 }
 
 // ------------------------------------------------ LDS bitonic sort (u64) ----
-// Ascending sort of n (a power of two) keys in LDS by NT threads.
-template <int NT>
-__device__ void bitonic_sort(uint64_t* a, uint32_t n) {
+// Ascending sort of n (a power of two) keys in LDS by NT threads. Each step
+// of the network compares the n/2 pairs (i, i + j), i with bit j clear; a
+// thread takes pairs p, p + NT, ... (i = p with a 0 bit inserted at j), four
+// at a time with all their loads issued before any compare.
+template <int NT, class T>
+__device__ void bitonic_sort_keys(T* a, uint32_t n) {
+    const uint32_t half = n >> 1;
     for (uint32_t k = 2; k <= n; k <<= 1) {
         for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-            for (uint32_t i = tid_x(); i < n; i += NT) {
-                const uint32_t ixj = i ^ j;
-                if (ixj > i) {
-                    const uint64_t x = a[i], y = a[ixj];
-                    const bool up = (i & k) == 0;
-                    if ((x > y) == up) { a[i] = y; a[ixj] = x; }
+            for (uint32_t p0 = tid_x(); p0 < half; p0 += 4u * NT) {
+                uint32_t ii[4];
+                T x[4], y[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t p = p0 + (uint32_t)u * NT;
+                    ii[u] = ((p & ~(j - 1u)) << 1) | (p & (j - 1u));
+                    if (p < half) {
+                        x[u] = a[ii[u]];
+                        y[u] = a[ii[u] | j];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t p = p0 + (uint32_t)u * NT;
+                    if (p < half && (x[u] > y[u]) == ((ii[u] & k) == 0u)) {
+                        a[ii[u]] = y[u];
+                        a[ii[u] | j] = x[u];
+                    }
                 }
             }
             __syncthreads();
         }
     }
 }
+template <int NT>
+__device__ void bitonic_sort(uint64_t* a, uint32_t n) { bitonic_sort_keys<NT>(a, n); }
 constexpr uint32_t next_pow2_c(uint32_t n) {
     uint32_t p = 1;
     while (p < n) p <<= 1;

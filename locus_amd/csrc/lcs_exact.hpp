@@ -217,6 +217,35 @@ __device__ __forceinline__ bool mask_bit(const uint32_t* mrow, uint32_t e) {
 }
 
 // =================================================== exact single-WG path ==
+#ifdef LCS_PROFILE
+// Phase stamps of exact_row (wall clock, 100 MHz) for performance work: row
+// r's stamp j at g_xprof[r * 64 + 2j] (clock) and g_xprof[r * 64 + 2j + 1]
+// (phase tag, ExactPhase), at most 32 a row; g_xprof_n[r] counts them.
+// Thread 0 writes. Each translation unit has its own copy and reader.
+static __device__ uint64_t g_xprof[4096 * 64];
+static __device__ uint32_t g_xprof_n[4096];
+#define XPROF(tag)                                                                             \
+    do {                                                                                       \
+        if (tid_x() == 0 && row < 4096u) {                                                     \
+            const uint32_t c_ = g_xprof_n[row];                                                \
+            if (c_ < 32u) {                                                                    \
+                g_xprof[row * 64u + 2u * c_] = __builtin_amdgcn_s_memrealtime();               \
+                g_xprof[row * 64u + 2u * c_ + 1u] = (uint64_t)(tag);                           \
+                g_xprof_n[row] = c_ + 1u;                                                      \
+            }                                                                                  \
+        }                                                                                      \
+    } while (0)
+#else
+#define XPROF(tag) \
+    do {           \
+    } while (0)
+#endif
+// (the tags, as bench.py --exact-clocks names them)
+enum ExactPhase : uint32_t {
+    kXpStart = 0, kXpIds = 1, kXpStats = 2, kXpMaxPen = 3, kXpHist = 4, kXpPrefix = 5,
+    kXpCompact = 10, kXpCompactPass = 11, kXpCompactSort = 12, kXpCompactEnd = 13,
+    kXpNarrow = 20, kXpNarrowRange = 21, kXpNarrowStep = 22, kXpNarrowEnd = 23, kXpDone = 99
+};
 struct ExactSeg {
     int blo, bhi;        // bin range
     uint64_t rlo, rhi;   // rank-key interval inside the bins
@@ -295,19 +324,7 @@ __device__ __forceinline__ int d_find(const uint32_t* ids_g, uint32_t n, uint32_
 
 template <int NT>
 __device__ void bitonic_sort_u32(uint32_t* a, uint32_t n) {
-    for (uint32_t k = 2; k <= n; k <<= 1) {
-        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-            for (uint32_t i = tid_x(); i < n; i += NT) {
-                const uint32_t ixj = i ^ j;
-                if (ixj > i) {
-                    const uint32_t x = a[i], y = a[ixj];
-                    const bool up = (i & k) == 0;
-                    if ((x > y) == up) { a[i] = y; a[ixj] = x; }
-                }
-            }
-            __syncthreads();
-        }
-    }
+    bitonic_sort_keys<NT>(a, n);
 }
 
 // Writes the logprob outputs of a row: chosen lp and top-n from sorted rank
@@ -347,6 +364,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
     float* d_raw = a.d_raw + (uint64_t)row * a.max_hist;
     float* d_pen = a.d_pen + (uint64_t)row * a.max_hist;
 
+    XPROF(kXpStart);
     if (tid == 0) sm.bincap = 0u;   // (thread 0 alone writes and reads it)
     for (uint32_t k = tid; k < kIdFilterWords; k += NT) sm.idf[k] = 0u;
     __syncthreads();
@@ -442,6 +460,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
         return (sm.u.h.fmask[rank >> 2] >> ((rank & 3u) * 8u + (e & 7u))) & 1u;
     };
 
+    XPROF(kXpIds);
     // ---- P1: raw stats, logsumexp, top-n, candidate max/min ----
     float rmax = -kInfF, cmax = -kInfF, rmin = kInfF, cmin = kInfF;
     uint32_t rarg = kNoIdx, carg = kNoIdx, nall = 0;
@@ -514,6 +533,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
     if (ntop) block_topn<NT>(tl, ntop, sm.topbuf);
     auto is_cand = [&](uint32_t e) { return !use_mask || mask_bit(mrow, e); };
 
+    XPROF(kXpStats);
     // ---- maximum penalised candidate (value and first index) ----
     float maxl = cmax;
     uint32_t maxi = carg;
@@ -587,9 +607,14 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
     }
 
     {
+        XPROF(kXpMaxPen);
         // ---- P4: fixed-point mass histogram over tempered offsets ----
+        // The bins span [x_lo, 0], x_lo no lower than -32: weights below
+        // e^-32 (1.3e-14 of the largest) share the last bin, so heavily
+        // penalised outliers do not coarsen the bins where the mass is (a
+        // crossing in the last bin is still found, by radix narrowing).
         float x_lo = tempered(lo_c, maxl, inv_t);
-        if (!(x_lo > -64.0f)) x_lo = -64.0f;
+        if (!(x_lo > -32.0f)) x_lo = -32.0f;
         const float sx = x_lo < 0.0f ? fdiv((float)NB, -x_lo) : 0.0f;
         auto bin_of = [&](float x) -> uint32_t {
             float f = fmul(-x, sx);
@@ -663,6 +688,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
         }
         __syncthreads();
 
+        XPROF(kXpHist);
         // inclusive prefix sums over bins (counts and 128-bit masses)
         {
             constexpr uint32_t BPT = NB >= (uint32_t)NT ? NB / NT : 1u;
@@ -723,6 +749,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
             }
             __syncthreads();
         }
+        XPROF(kXpPrefix);
         auto cnt_incl = [&](int b) -> uint32_t { return b < 0 ? 0u : sm.u.h.cnt[b]; };
         auto mass_incl = [&](int b) -> double {
             return b < 0 ? 0.0 : mass_to_double(sm.u.h.mhi[b], sm.u.h.mlo[b]);
@@ -831,6 +858,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
         // Compacts the wanted regions (plus, space permitting, the regions
         // already listed) in one streaming pass.
         auto compact = [&](const ExactSeg* want, int n) {
+            XPROF(kXpCompact);
             ExactSeg all[kSegs];
             int na = 0;
             uint32_t tot = 0;
@@ -877,11 +905,13 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
                     if (b >= mp_lo && b <= mp_hi && weight(p) / S >= mp_thresh) atomicAdd(&sm.mp_count, 1u);
                 });
             __syncthreads();
+            XPROF(kXpCompactPass);
             const uint32_t nl = min(sm.nlist, CAP);
             const uint32_t p2 = next_pow2(max(nl, 2u));
             for (uint32_t i = nl + tid; i < p2; i += NT) sm.list[i] = ~0ull;
             __syncthreads();
             bitonic_sort<NT>(sm.list, p2);
+            XPROF(kXpCompactSort);
             for (int i = 1; i < na; ++i) {
                 for (int j = i; j > 0 && (all[j].cb < all[j - 1].cb); --j) {
                     const ExactSeg t = all[j]; all[j] = all[j - 1]; all[j - 1] = t;
@@ -891,11 +921,13 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
             for (int s = 0; s < na; ++s) { all[s].off = off; off += all[s].cnt; segs[s] = all[s]; }
             nseg = na;
             if (sm.nlist > CAP && tid == 0) { atomicOr(a.status, kStatusBinCap); sm.bincap = 1u; }
+            XPROF(kXpCompactEnd);
         };
         // Narrows one bin holding > CAP candidates to a rank-key interval
         // containing candidate position `pos` (by_count) or the crossing of
         // cumulative mass `mt`, by 8-bit MSD radix steps on the rank key.
         auto narrow = [&](int b, bool by_count, uint32_t pos, double mt) __attribute__((always_inline)) -> ExactSeg {
+            XPROF(kXpNarrow);
             ExactSeg s = bin_seg(b, b);
             uint64_t mn = ~0ull, mx = 0;
             for_cands([&](int bb) { return bb == b; }, [&](float p, uint32_t e, int) {
@@ -904,6 +936,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
                 mx = rk > mx ? rk : mx;
             });
             mn = block_min_u64<NT>(mn, sm.red64);
+            XPROF(kXpNarrowRange);
             mx = ~block_min_u64<NT>(~mx, sm.red64);
             s.rlo = mn;
             s.rhi = mx;
@@ -964,7 +997,9 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
                 }
                 __syncthreads();
                 s = sm.bc_seg;
+                XPROF(kXpNarrowStep);
             }
+            XPROF(kXpNarrowEnd);
             return s;
         };
         auto region_for_count = [&](uint32_t pos) -> ExactSeg {
@@ -1147,6 +1182,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
             }
         }
     }
+    XPROF(kXpDone);
 write_back:
     if ((a.flags & LCS_WRITE_PENALIZED) && a.dtype == LCS_F32) {
         __syncthreads();

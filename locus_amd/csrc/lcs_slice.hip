@@ -42,6 +42,17 @@ constexpr uint32_t kWinLds = 256;    // window entries one slice can rank
 extern "C" int lcs_prof_read(uint64_t* out, uint32_t n) {
     return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_prof), (size_t)n * 8, 0, hipMemcpyDeviceToHost);
 }
+// The exact path's stamps inside row_fin (4096 rows x 64 words, then the
+// per-row counts), and their reset.
+extern "C" int lcs_xprof_read(uint64_t* out, uint32_t* cnt) {
+    const hipError_t e = hipMemcpyFromSymbol(cnt, HIP_SYMBOL(g_xprof_n), 4096 * 4, 0, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return (int)e;
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_xprof), 4096 * 64 * 8, 0, hipMemcpyDeviceToHost);
+}
+extern "C" int lcs_xprof_clear() {
+    static const uint32_t zero[4096] = {};
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_xprof_n), zero, sizeof zero, 0, hipMemcpyHostToDevice);
+}
 #endif
 
 // ============================================================ slice_stats ==

@@ -12,6 +12,9 @@ Configurations (seed base ``S = 20261200 + n`` for configuration n):
 * ``c2`` - B=64, V=128256 f32 ~ N(0, 3^2); 2048-id Zipf(1.1) history per row
   through a seeded permutation; repeat 1.1, frequency 0.5, presence 0.3,
   repeat_last_n 2048; T=0.7, min_p 0.05, top_p 0.9; top-5 logprobs.
+* ``c2w`` - ``c2`` with N(0, 1) logits, T=1.5 and min_p 0.01: min-p windows
+  of thousands of ids, past a slice's window record, so every row takes the
+  exact path inside the row finalize (a stress case, not a BASELINE config).
 * ``c3`` - B=256, V=151936 f32 ~ N(0, 1); T=1.5, top_p 0.98.
 * ``c4`` - B=32, V=128256 f32 ~ N(0, 2.5^2); per-row allow mask of V/32
   words with log-uniform density in [5e-4, 0.3] built from runs of 1..64 ids;
@@ -225,6 +228,14 @@ def make_c2(rows: int | None = None, set_index: int = 0, hist_len: int = 2048) -
                     hist_ids=hist.reshape(-1), n_top=5, want_logprobs=True)
 
 
+def make_c2w(rows: int | None = None, set_index: int = 0) -> Workload:
+    w = make_c2(rows, set_index)
+    p = w.params.copy()
+    p["temperature"], p["min_p"] = 1.5, 0.01
+    return dataclasses.replace(w, name="c2w", logits=(w.logits / np.float32(3.0)).astype(np.float32),
+                               params=p)
+
+
 def make_c3(rows: int | None = None, set_index: int = 0) -> Workload:
     S, V = CFG_SEED["c3"], VOCAB["c3"]
     rows = FULL_ROWS["c3"] if rows is None else rows
@@ -297,6 +308,8 @@ def make(name: str, rows: int | None = None, set_index: int = 0) -> Workload:
         return make_c1(False, set_index)
     if name == "c2":
         return make_c2(rows, set_index)
+    if name == "c2w":
+        return make_c2w(rows, set_index)
     if name == "c3":
         return make_c3(rows, set_index)
     if name == "c4":
