@@ -342,15 +342,31 @@ __device__ __forceinline__ void write_logprobs(const SampleArgs& a, uint32_t row
     }
 }
 
+// Row statistics a caller already holds for an unmasked stochastic row (the
+// slice records of the sliced path): with them exact_row skips its stats pass,
+// and the caller has written the row's top-n logprob outputs. (A stochastic
+// row's decision needs the penalised maximum's value, not its index.)
+struct ExactPre {
+    uint32_t on;      // the fields below are set
+    float maxl;       // penalised maximum over the row
+    double log_z;     // raw log-normaliser (logprobs)
+};
+
 // a_lds and sm_lds are __shared__ objects of the calling kernel.
 template <int NT, uint32_t NB, uint32_t CAP, uint32_t DCAP, int G>
 __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uint32_t row,
-                                                    ExactSmem<NT, NB, CAP, DCAP>& sm_lds) {
+                                                    ExactSmem<NT, NB, CAP, DCAP>& sm_lds,
+                                                    const ExactPre pre = ExactPre{}) {
     static_assert(NB % NT == 0 || NT % NB == 0, "bins vs threads");
     const SampleArgs& a = lds_ref(a_lds);
     ExactSmem<NT, NB, CAP, DCAP>& sm = lds_ref(sm_lds);
     const uint32_t tid = tid_x();
     const lcs_params P = a.params[row];
+    if (pre.on && (P.temperature <= 0.0f || (a.mask != nullptr && (a.has_mask == nullptr || a.has_mask[row] != 0)))) {
+        // (pre is for unmasked stochastic rows only: a caller mistake)
+        if (tid == 0) { atomicOr(a.status, kStatusBinCap); a.ids[row] = -1; }
+        return;
+    }
     const uint32_t V = a.vocab;
     const uint32_t esz = a.dtype == LCS_BF16 ? 2u : 4u;
     const void* rowp = static_cast<const char*>(a.logits) + (uint64_t)row * a.row_stride * esz;
@@ -468,6 +484,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
     double os = 0.0;
     WaveTop tl;
     tl.init();
+    if (!pre.on) {
     stream_groups_all<NT, G>(rowp, V, [&](uint32_t gi, const float (&v)[G], uint32_t nv) {
         const uint32_t e0 = gi * G;
         const uint32_t mw = mrow && nv ? (glb(mrow)[e0 >> 5] >> (e0 & 31u)) : 0xffffffffu;
@@ -526,19 +543,21 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
         cmin = block_min<NT>(cmin, sm.redf);
         nall = block_sum_u<NT>(nall, sm.redu);
     }
-    const double log_z = log(os) + (double)rmax;
+    }   // (!pre.on)
+    const double log_z = pre.on ? pre.log_z : log(os) + (double)rmax;
     const bool use_mask = mrow != nullptr && nall > 0;
     const uint32_t n_cand = use_mask ? nall : V;
     if (!use_mask) { cmax = rmax; carg = rarg; cmin = rmin; }
-    if (ntop) block_topn<NT>(tl, ntop, sm.topbuf);
+    const uint32_t ntop_out = pre.on ? 0u : ntop;   // top-n entries exact_row writes
+    if (ntop_out) block_topn<NT>(tl, ntop_out, sm.topbuf);
     auto is_cand = [&](uint32_t e) { return !use_mask || mask_bit(mrow, e); };
 
     XPROF(kXpStats);
     // ---- maximum penalised candidate (value and first index) ----
-    float maxl = cmax;
-    uint32_t maxi = carg;
-    float lo_c = cmin;
-    if (nD > 0) {
+    float maxl = pre.on ? pre.maxl : cmax;
+    uint32_t maxi = pre.on ? kNoIdx : carg;
+    float lo_c = pre.on ? -kInfF : cmin;   // (unknown with pre: the bins then span [-32, 0])
+    if (nD > 0 && !pre.on) {
         float dmax = -kInfF, dmin = kInfF;
         uint32_t dmi = kNoIdx;
         for (uint32_t j = tid; j < nD; j += NT) {
@@ -594,7 +613,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
                 const bool inr = lid >= 0 && (uint32_t)lid < V;
                 const int j = inr && nD > 0 ? d_find(d_ids, nD, (uint32_t)lid) : -1;
                 const float raw = j >= 0 ? d_raw[j] : (inr ? load_elem(rowp, a.dtype, (uint32_t)lid) : 0.0f);
-                write_logprobs(a, row, lid, raw, log_z, sm.topbuf, ntop);
+                write_logprobs(a, row, lid, raw, log_z, sm.topbuf, ntop_out);
             }
             if (a.diag) {
                 lcs_row_diag dg{};
@@ -1170,7 +1189,7 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
                 const bool inr = lid >= 0 && (uint32_t)lid < V;
                 const int j = inr && nD > 0 ? d_find(d_ids, nD, (uint32_t)lid) : -1;
                 const float raw = j >= 0 ? d_raw[j] : (inr ? load_elem(rowp, a.dtype, (uint32_t)lid) : 0.0f);
-                write_logprobs(a, row, lid, raw, log_z, sm.topbuf, ntop);
+                write_logprobs(a, row, lid, raw, log_z, sm.topbuf, ntop_out);
             }
             if (a.diag) {
                 lcs_row_diag dg{};

@@ -717,6 +717,7 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
         fin_window_rank(sm, wv, inv_t);
         __syncthreads();
     }
+    bool topn_done = false;   // (the same in every wave)
     if (!fin_any_fb(sm)) {
         // logprob of the chosen token, or of the caller's lp_ids token (thread
         // 0, once the row's choice and log-normaliser are in)
@@ -734,6 +735,7 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
         };
         // the top-n outputs (wave 1) beside the decision (wave 0)
         if (wv == 1 && ntop) fin_topn_merge(a, S, row, ntop, sm);
+        topn_done = true;
         if (!(stoch || topk)) {
             if (tid == 0 && want_lp) write_lp();
             return;
@@ -751,9 +753,20 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
         if (!sm.fin_fb_decide) return;
     }
     // the records cannot settle this row: the exact single-workgroup path
-    // (out of line: it reads the kernel arguments from an LDS copy)
+    // (out of line: it reads the kernel arguments from an LDS copy). Unless
+    // the log-normaliser's wave flagged the row, the records still give its
+    // penalised maximum, log-normaliser and top-n, and the exact path skips
+    // its stats pass (the top-n merge reads the union that exact_row reuses:
+    // stage_args's barrier orders the two)
+    ExactPre pre{};
+    if (!masked && (stoch || topk) && !(want_lp && sm.fin_fb[1] != 0u)) {
+        if (!topn_done && wv == 1 && ntop) fin_topn_merge(a, S, row, ntop, sm);
+        pre.on = 1u;
+        pre.maxl = wave_max((uint32_t)lane < S ? __uint_as_float((uint32_t)hd[2]) : -__builtin_huge_valf());
+        pre.log_z = want_lp ? sm.log_z : 0.0;
+    }
     stage_args(&sm.args, a);
-    exact_row<kFinThreads, kFinFbBins, kFinFbCap, kFbHistCap, G>(sm.args, row, sm.u.ex);
+    exact_row<kFinThreads, kFinFbBins, kFinFbCap, kFbHistCap, G>(sm.args, row, sm.u.ex, pre);
 }
 
 // One workgroup per row (the sliced path's second kernel). The leading
