@@ -293,6 +293,7 @@ struct ExactSmem {
     uint32_t wbins[NB / 32];        // bins a compaction pass wants
     ExactSeg bc_seg;
     ExactBox cbox[kExactSegs];   // the regions a compaction collects
+    uint32_t soff[kExactSegs];   // their offsets in the sorted list
     uint32_t nlist;
     uint32_t mp_count;
     uint32_t flag;
@@ -795,9 +796,10 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
         // ---- regions of the candidate order, compacted into the LDS list ----
         // A region is a contiguous bin range or, inside one bin holding more
         // than CAP candidates, an interval of 64-bit rank keys (logit, then
-        // token id: exact ties are separated by id). Regions in the list are
-        // disjoint and the list is sorted by rank, so each region occupies a
-        // contiguous run of the list starting at `off`.
+        // token id: exact ties are separated by id). Listed regions may
+        // overlap: the list holds their union, each candidate once, sorted by
+        // rank, so each region occupies a contiguous run of the list starting
+        // at `off`.
         constexpr int kSegs = kExactSegs;
         ExactSeg segs[kSegs];
         int nseg = 0;
@@ -936,8 +938,26 @@ __device__ __attribute__((noinline)) void exact_row(const SampleArgs& a_lds, uin
                     const ExactSeg t = all[j]; all[j] = all[j - 1]; all[j - 1] = t;
                 }
             }
-            uint32_t off = 0;
-            for (int s = 0; s < na; ++s) { all[s].off = off; off += all[s].cnt; segs[s] = all[s]; }
+            // each region's offset: its first entry in the sorted list (bins
+            // ascend with the rank key), which stays right when regions
+            // overlap: the list holds their union, each candidate once
+            // (thread s searches for region s)
+            if (tid < (uint32_t)na) {
+                const ExactSeg me = all[tid];
+                uint32_t lo = 0, hi = nl;
+                while (lo < hi) {
+                    const uint32_t mid = (lo + hi) >> 1;
+                    const uint64_t k = sm.list[mid];
+                    const int b = (int)bin_of(tempered(rank_val(k), maxl, inv_t));
+                    if (b > me.blo || (b == me.blo && k >= me.rlo)) hi = mid; else lo = mid + 1;
+                }
+                sm.soff[tid] = lo;
+            }
+            __syncthreads();
+            for (int s = 0; s < na; ++s) {
+                all[s].off = sm.soff[s];
+                segs[s] = all[s];
+            }
             nseg = na;
             if (sm.nlist > CAP && tid == 0) { atomicOr(a.status, kStatusBinCap); sm.bincap = 1u; }
             XPROF(kXpCompactEnd);
