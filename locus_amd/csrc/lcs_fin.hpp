@@ -717,7 +717,11 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
         fin_window_rank(sm, wv, inv_t);
         __syncthreads();
     }
-    bool topn_done = false;   // (the same in every wave)
+    // the top-n outputs (wave 1, beside the decision on wave 0), from the
+    // records unless the log-normaliser's wave flagged the row: also when
+    // the row then takes the exact path
+    const bool logz_ok = !(want_lp && sm.fin_fb[1] != 0u);
+    if (logz_ok && wv == 1 && ntop) fin_topn_merge(a, S, row, ntop, sm);
     if (!fin_any_fb(sm)) {
         // logprob of the chosen token, or of the caller's lp_ids token (thread
         // 0, once the row's choice and log-normaliser are in)
@@ -733,9 +737,6 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
             }
             a.chosen_lp[row] = inr ? (float)((double)raw - sm.log_z) : 0.0f;
         };
-        // the top-n outputs (wave 1) beside the decision (wave 0)
-        if (wv == 1 && ntop) fin_topn_merge(a, S, row, ntop, sm);
-        topn_done = true;
         if (!(stoch || topk)) {
             if (tid == 0 && want_lp) write_lp();
             return;
@@ -755,12 +756,11 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
     // the records cannot settle this row: the exact single-workgroup path
     // (out of line: it reads the kernel arguments from an LDS copy). Unless
     // the log-normaliser's wave flagged the row, the records still give its
-    // penalised maximum, log-normaliser and top-n, and the exact path skips
-    // its stats pass (the top-n merge reads the union that exact_row reuses:
-    // stage_args's barrier orders the two)
+    // penalised maximum and log-normaliser (and the top-n is written), and
+    // the exact path skips its stats pass (the top-n merge read the union
+    // that exact_row reuses: stage_args's barrier orders the two)
     ExactPre pre{};
-    if (!masked && (stoch || topk) && !(want_lp && sm.fin_fb[1] != 0u)) {
-        if (!topn_done && wv == 1 && ntop) fin_topn_merge(a, S, row, ntop, sm);
+    if (!masked && (stoch || topk) && logz_ok) {
         pre.on = 1u;
         pre.maxl = wave_max((uint32_t)lane < S ? __uint_as_float((uint32_t)hd[2]) : -__builtin_huge_valf());
         pre.log_z = want_lp ? sm.log_z : 0.0;
