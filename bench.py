@@ -800,7 +800,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); "
-              "rows shard across GPUs with no exchange, see DESIGN.md", file=sys.stderr)
+              "a batch's rows would shard across GPUs with no exchange between them", file=sys.stderr)
         sys.exit(2)
     w, ms_step, wall_ms, ms_launch, nsets = gpu_bench(args.workload, args.steps, args.warmup)
     ceiling = copy_ceiling()
