@@ -74,7 +74,21 @@ __device__ __forceinline__ double ent_bound(double S, uint32_t n, float mk) {
 }
 
 // ================================================================ row_fin ==
+// (the small fields come first: an LDS instruction's immediate offset stops at
+// 64 KiB, and the union, with the exact path's block, ends past it)
 struct FinSmem {
+    double log_z, fin_S, fin_rel, fin_invS;
+    float chosen_raw, fin_maxl;
+    float fin_premax;        // penalised maximum over the slices' headers (wave 3)
+    uint32_t fin_fb[4];      // per wave: the records cannot settle the row (exact path)
+    uint32_t fin_fb_decide;  // wave 0's decision could not be certified (exact path)
+    uint32_t fin_L0;
+    uint32_t tk_ns[kSsMaxSlices];                    // top-k rows: entries of each slice's list,
+    uint32_t tk_cs[kSsMaxSlices], tk_base[kSsMaxSlices];   // its candidates (keys <= U), their offset
+    uint64_t tk_u[4];                                // top-k rows: each wave's bound
+    uint32_t tn_ns[kRecsPerRow];                     // top-n list lengths (logprobs)
+    uint32_t prof_row;   // (phase clocks: the row)
+    SampleArgs args;   // the kernel arguments (exact_row reads them from here)
     union {
         struct {
             uint64_t top[kRecsPerRow * kTopMax];    // the records' top-n lists
@@ -88,17 +102,6 @@ struct FinSmem {
         } f;
         ExactSmem<kFinThreads, kFinFbBins, kFinFbCap, kFbHistCap> ex;
     } u;
-    double log_z, fin_S, fin_rel, fin_invS;
-    float chosen_raw, fin_maxl;
-    uint32_t fin_fb[4];      // per wave: the records cannot settle the row (exact path)
-    uint32_t fin_fb_decide;  // wave 0's decision could not be certified (exact path)
-    uint32_t fin_L0;
-    uint32_t tk_ns[kSsMaxSlices];                    // top-k rows: entries of each slice's list,
-    uint32_t tk_cs[kSsMaxSlices], tk_base[kSsMaxSlices];   // its candidates (keys <= U), their offset
-    uint64_t tk_u[4];                                // top-k rows: each wave's bound
-    uint32_t tn_ns[kRecsPerRow];                     // top-n list lengths (logprobs)
-    uint32_t prof_row;   // (phase clocks: the row)
-    SampleArgs args;   // the kernel arguments (exact_row reads them from here)
 };
 
 // Whether a wave flagged the row for the exact path (read after a barrier
@@ -710,6 +713,11 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
         if (stoch) fin_norm(hd, S, sm, inv_t);
     }
     PROF_AT(kProfFin + row, 8 + wv);
+    // (wave 3: the penalised maximum over the slices, for an exact fallback)
+    if (wv == 3) {
+        const float pm = wave_max((uint32_t)lane < S ? __uint_as_float((uint32_t)hd[2]) : -__builtin_huge_valf());
+        if (lane == 0) sm.fin_premax = pm;
+    }
     if (lane == 0) sm.fin_fb[wv] = fb ? 1u : 0u;
     __syncthreads();
     PROF_AT(kProfFin + row, 12 + wv);
@@ -720,8 +728,7 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
     // the top-n outputs (wave 1, beside the decision on wave 0), from the
     // records unless the log-normaliser's wave flagged the row: also when
     // the row then takes the exact path
-    const bool logz_ok = !(want_lp && sm.fin_fb[1] != 0u);
-    if (logz_ok && wv == 1 && ntop) fin_topn_merge(a, S, row, ntop, sm);
+    if (!(want_lp && sm.fin_fb[1] != 0u) && wv == 1 && ntop) fin_topn_merge(a, S, row, ntop, sm);
     if (!fin_any_fb(sm)) {
         // logprob of the chosen token, or of the caller's lp_ids token (thread
         // 0, once the row's choice and log-normaliser are in)
@@ -759,10 +766,12 @@ __device__ __forceinline__ void fin_row(const lcs_params* params, const uint64_t
     // penalised maximum and log-normaliser (and the top-n is written), and
     // the exact path skips its stats pass (the top-n merge read the union
     // that exact_row reuses: stage_args's barrier orders the two)
+    // (only window and top-k rows, unmasked, get here; the fields come from
+    // LDS so that nothing stays live across the finalize for them)
     ExactPre pre{};
-    if (!masked && (stoch || topk) && logz_ok) {
+    if (!(want_lp && sm.fin_fb[1] != 0u)) {
         pre.on = 1u;
-        pre.maxl = wave_max((uint32_t)lane < S ? __uint_as_float((uint32_t)hd[2]) : -__builtin_huge_valf());
+        pre.maxl = sm.fin_premax;
         pre.log_z = want_lp ? sm.log_z : 0.0;
     }
     stage_args(&sm.args, a);
